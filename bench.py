@@ -1,0 +1,251 @@
+"""Benchmark: LuminaV optimizer step on one MI355X (BASELINE.json metric and configs).
+
+Default workload = configs[4] of BASELINE.json, the headline: buffer="T2", cautious=True, bf16
+params and grads with fp32 m/v, one contiguous 6,738,415,616-element bucket (Llama-7B shape),
+grads 1e-3 * Student-t(df=3). Inputs are generated on the GPU and stay resident in HBM; a step is
+one drop-in `LuminaV.step()` (one fused HIP kernel launch at steady state).
+
+Prints ONE JSON line with params/s (whole job), ms per step, achieved HBM GB/s against the
+8 TB/s peak (`roofline`), and the CPU oracle timed on a bounded sample on this host
+(`cpu_baseline`).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+# Llama-7B (32 layers, d=4096, ffn=11008, vocab 32000) and Llama-1B-style shapes as one bucket.
+N5 = 32 * (4 * 4096 * 4096 + 3 * 4096 * 11008 + 2 * 4096) + 2 * 32000 * 4096 + 4096
+N4 = 16 * (4 * 2048 * 2048 + 3 * 2048 * 5632 + 2 * 2048) + 2 * 32000 * 2048 + 2048
+N3 = 12 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768) + 50 * 768 + 50257 * 768
+
+# Algorithmic bytes per parameter per steady-state step: every buffer read once, written once.
+#   T2/CLM bf16 p,g + f32 m,v: p 2+2, g 2, m 4+4, v 4+4 = 22
+#   T1/TD-CLM bf16 p,g + f32 m: p 2+2, g 2, m 4+4 = 14
+#   CLM fp32: p 4+4, g 4, m 4+4, v 4+4 = 28 ; TD-CLM fp32: 20
+WORKLOADS = {
+    5: dict(name="cfg5: LuminaV T2 cautious, bf16 p/g + fp32 m/v, one 6,738,415,616-elem bucket (Llama-7B)",
+            n=N5, buffer="T2", pdt="bf16", cautious=True, bytes_per_param=22, grad="student_t3"),
+    4: dict(name="cfg4: LuminaV T1 (lam=0.3), bf16 p/g + fp32 m, one 953,223,168-elem bucket (Llama-1B)",
+            n=N4, buffer="T1", pdt="bf16", cautious=True, bytes_per_param=14, grad="normal"),
+    3: dict(name="cfg3: LuminaV buffer=2 cautious, fp32, one 123,570,432-elem bucket (GPT-2 small)",
+            n=N3, buffer=2, pdt="f32", cautious=True, bytes_per_param=28, grad="normal"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def fill_inputs(torch, n: int, pdt, grad_kind: str, seed: int = 1234):
+    """p ~ N(0, 0.02), g ~ 1e-3 * N(0,1) or 1e-3 * t(df=3); generated in chunks on the GPU."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    p = torch.empty(n, dtype=pdt, device="cuda")
+    g = torch.empty(n, dtype=pdt, device="cuda")
+    chunk = 1 << 27
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        k = e - s
+        z = torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
+        p[s:e].copy_(z.mul_(0.02))
+        z = torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
+        if grad_kind == "student_t3":
+            chi2 = torch.zeros(k, device="cuda", dtype=torch.float32)
+            for _ in range(3):
+                w = torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
+                chi2.addcmul_(w, w)
+            z.div_(chi2.div_(3.0).sqrt_())
+            del chi2
+        g[s:e].copy_(z.mul_(1e-3))
+        del z
+    return p, g
+
+
+def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
+    """The CPU oracle (a C restatement of the reference's Rust CPU path with its structure:
+    serial bf16 decode/encode, 2,097,152-element chunks over threads) on a bounded sample of the
+    same workload, timed with perf_counter around the step call only."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    O.lib()
+    pdt = torch.bfloat16 if workload["pdt"] == "bf16" else torch.float32
+    cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"])
+    dual = workload["buffer"] in (2, "T2")
+
+    def make(n):
+        rng = np.random.default_rng(5)
+        p = torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)).to(pdt)
+        g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(pdt)
+        m = torch.zeros(n)
+        v = torch.zeros(n) if dual else None
+        sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
+        return p, g, m, v, sc
+
+    # calibrate on a small sample, then size the timed sample to ~target_s over 3 steps
+    n_cal = 1 << 22
+    p, g, m, v, sc = make(n_cal)
+    O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)
+    t0 = time.perf_counter()
+    O.step(cfg, [p], [g], [m], [v], [None], [sc], [2], [0], threads=threads)
+    rate = n_cal / max(time.perf_counter() - t0, 1e-6)
+    n = int(min(workload["n"], max(n_cal, rate * target_s / 3.0)))
+    n = (n // 2097152 + 1) * 2097152 if n > 2097152 else n
+    p, g, m, v, sc = make(n)
+    O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)  # step 1 (two-pass), untimed
+    times = []
+    for s in (2, 3, 4):
+        t0 = time.perf_counter()
+        O.step(cfg, [p], [g], [m], [v], [None], [sc], [s], [0], threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": n / t,
+        "unit": "params/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} elements of the same workload (median of 3 steady steps, {t * 1e3:.1f} ms/step), "
+                  f"{threads} threads on '{cpu_model}'",
+        "gb_per_s": n * workload["bytes_per_param"] / t / 1e9,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=5, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the step shards by "
+                                   "element ranges, see DESIGN.md)", "n_gpus": args.gpus}), flush=True)
+        return 2
+
+    import torch
+
+    from luminamoon_amd import LuminaV
+    from luminamoon_amd.optimizer import hip_backend
+
+    hip_backend.load_library()
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        return 1
+    wl = WORKLOADS[args.config]
+    pdt = torch.bfloat16 if wl["pdt"] == "bf16" else torch.float32
+    n = wl["n"]
+    free, total = torch.cuda.mem_get_info()
+    state_b = 4 * n * (2 if wl["buffer"] in (2, "T2") else 1)
+    need = n * (2 if pdt == torch.bfloat16 else 4) * 2 + state_b
+    log(f"workload {wl['name']}: n={n}, resident {need / 1e9:.1f} GB, free {free / 1e9:.1f} GB")
+    if need + (8 << 30) > free:
+        log("not enough HBM for this workload")
+        return 1
+
+    t0 = time.perf_counter()
+    p_data, g_data = fill_inputs(torch, n, pdt, wl["grad"])
+    p = torch.nn.Parameter(p_data, requires_grad=True)
+    p.grad = g_data
+    opt = LuminaV([p], lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"])
+    torch.cuda.synchronize()
+    log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
+
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        opt.step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    per_step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ms_avg = sum(per_step_ms) / len(per_step_ms)
+    ms_wall = wall * 1e3 / args.steps
+    params_per_s = n / (ms_wall / 1e3)
+    bytes_launch = n * wl["bytes_per_param"]
+    achieved = bytes_launch / (ms_avg / 1e3) / 1e9
+    log(f"per-step event ms: min {min(per_step_ms):.3f} avg {ms_avg:.3f} max {max(per_step_ms):.3f}; wall {ms_wall:.3f}")
+    sc = opt.state[p]["scratch"].tolist()
+    log(f"scratch after {args.warmup + args.steps} steps: {sc}")
+    if not all(math.isfinite(x) for x in sc):
+        log("non-finite scratch")
+        return 1
+    del opt, p, p_data, g_data
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        log(f"timing the CPU oracle with {threads} threads")
+        cpu = cpu_baseline(wl, threads)
+
+    out = {
+        "metric": "optimizer params updated/sec + achieved HBM GB/s (% of peak), 1 MI355X",
+        "value": params_per_s,
+        "unit": "params/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_wall,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (p ~ N(0,0.02), g = 1e-3*t(df=3) for cfg5 else 1e-3*N(0,1); generated on the GPU)",
+        "config": {
+            "workload": wl["name"],
+            "buffer": wl["buffer"],
+            "params": n,
+            "param_dtype": wl["pdt"],
+            "state_dtype": "f32",
+            "cautious": wl["cautious"],
+            "bytes_per_param": wl["bytes_per_param"],
+        },
+        "achieved_gb_per_s": achieved,
+        "hbm_frac": achieved / HBM_PEAK_GBS,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,935 @@
+// MI355X (gfx950) LuminaV optimizer step: HIP kernels + C ABI (include/luminav_hip.h).
+//
+// One fused, grid-stride, multi-tensor pass per (dtype, step, pass) class.  Each work unit is
+// 256 threads x 8 contiguous elements; a thread moves its 8 elements with 16-byte vector
+// loads/stores (one dwordx4 for bf16/f16, two for f32) and falls back to per-element access
+// for ragged tails and for tensors whose pointers are not 16-byte aligned.  The cautious mask
+// is counted exactly (per-thread integer counts, one u64 atomic per block and tensor), and the
+// last block of each tensor -- found with a per-tensor ticket -- finalises the 6-float scratch
+// on the device, so a step needs no host synchronisation and no extra launch.
+//
+// Per-element arithmetic follows the reference's scalar core operation for operation
+// (optimizer/crates/luminav-core/src/reference_cpu/dual.rs, reference_cpu/tdclm.rs,
+// math.rs, prng.rs): explicit fmaf exactly where the Rust code calls mul_add, separately
+// rounded products elsewhere (built with -ffp-contract=off), IEEE division and square root,
+// so results are bitwise equal to the reference CPU implementation.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "luminav_hip.h"
+
+namespace lv {
+
+constexpr int kThreads = 256;
+constexpr int kVec = 8;
+constexpr uint32_t kUnit = kThreads * kVec;  // elements per work unit
+constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table)
+
+enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
+
+enum Flags : uint32_t {
+    kFCautious = 1u << 0,
+    kFSR = 1u << 1,
+    kFMaster = 1u << 2,
+    kFWeightDecay = 1u << 3,
+    kFClampV = 1u << 4,
+    kFRadial = 1u << 5,
+    kFCoordinate = 1u << 6,
+};
+
+// One tensor of a launch (64 bytes, lives in the kernel argument segment).
+struct Desc {
+    void *p;
+    const void *g;
+    void *m;
+    void *v;
+    float *mp;
+    float *scratch;
+    uint64_t n;
+    uint32_t unit_begin;  // first work unit of this tensor in the launch's unit space
+    uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
+};
+
+// Launch-uniform constants: hyper-parameters, per-step coefficients, tensor table.
+struct Args {
+    float lr, b1, b2, omb1, omb2, b1sq, omb1sq, eps, lam, lam1, neg_lr_wd, ratio;
+    float c1, c2, c_sigma, ema, ema_c, clamp_min;
+    uint32_t seed_base;  // low 32 bits of seed + step * 0x9E3779B9 (prng.rs:4-13)
+    uint32_t flags;      // Flags | grad dtype << 8
+    uint32_t total_units;
+    int32_t ndesc;
+    unsigned long long *counters;  // 2 per tensor: cautious mask count, finished-unit ticket
+    Desc d[kMaxDesc];
+};
+
+// ------------------------------------------------------------------ device math
+
+__device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f_bits(float f) { return __float_as_uint(f); }
+
+// Rust f32::clamp: NaN passes through.
+__device__ __forceinline__ float rclamp(float x, float lo, float hi) {
+    x = x < lo ? lo : x;
+    return x > hi ? hi : x;
+}
+
+// prng.rs:21-26 -- wrapping i32 arithmetic, arithmetic right shifts.
+// The multipliers are the reference's decimal i32 constants; the first one is close to, but not,
+// MurmurHash3's fmix32 constant.
+__device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
+    constexpr uint32_t kAdd = (uint32_t)-1640531527;  // wrapping_sub(1_640_531_527)
+    constexpr uint32_t kMul1 = (uint32_t)-2048173461;
+    constexpr uint32_t kMul2 = (uint32_t)-1028477387;
+    int32_t z = (int32_t)((uint32_t)idx + (uint32_t)seed + kAdd);
+    z = (int32_t)((uint32_t)(z ^ (z >> 16)) * kMul1);
+    z = (int32_t)((uint32_t)(z ^ (z >> 13)) * kMul2);
+    return z ^ (z >> 16);
+}
+
+// prng.rs:137-160 (value form: f32 carrying the bf16 bits)
+__device__ __forceinline__ float sr_bf16(float v, int32_t seed, int32_t off) {
+    int32_t p = (int32_t)f_bits(v);
+    int32_t a = p & 0x7FFFFFFF;
+    if (a > 0x7F800000) return bits_f(((uint32_t)p | 0x00400000u) & 0xFFFF0000u);
+    int32_t noise = prng(seed, off) & 0xFFFF;
+    int32_t added = (int32_t)(((uint32_t)a + (uint32_t)noise) & 0xFFFF0000u);
+    int32_t r = (added > 0x7F7F0000 || added < 0) ? 0x7F7F0000 : added;
+    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
+}
+
+// prng.rs:162-178
+__device__ __forceinline__ float rne_bf16(float v) {
+    uint32_t b = f_bits(v);
+    uint32_t a = b & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return bits_f((b | 0x00400000u) & 0xFFFF0000u);
+    uint32_t r = (a + 0x7FFFu + ((a >> 16) & 1u)) & 0xFFFF0000u;
+    r = r > 0x7F7F0000u ? 0x7F7F0000u : r;
+    return bits_f((b & 0x80000000u) | r);
+}
+
+// prng.rs:29-67
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float val) {
+    uint32_t bits = f_bits(val);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x007FFFFFu;
+    if (exp == 255) return sign | (mant != 0 ? 0x7E00u : 0x7BFFu);
+    int32_t ne = exp - 112;
+    if (ne >= 31) return sign | 0x7BFFu;
+    if (ne <= 0) {
+        if (ne < -10) return sign;
+        uint32_t fm = mant | 0x00800000u;
+        uint32_t sh = (uint32_t)(14 - ne);
+        uint32_t half = 1u << (sh - 1);
+        uint32_t r = (fm + half - 1u + ((fm >> sh) & 1u)) >> sh;
+        return sign | r;
+    }
+    uint32_t r = mant + 0x0FFFu + ((mant >> 13) & 1u);
+    uint32_t body = ((uint32_t)ne << 10) + (r >> 13);
+    return body >= 0x7C00u ? (sign | 0x7BFFu) : (sign | body);
+}
+
+// prng.rs:69-96
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x03FFu;
+    if (exp == 0) {
+        if (mant == 0) return bits_f(sign);
+        // subnormal: normalise (leading one of a 10-bit field)
+        uint32_t lz = __clz(mant) - 21;  // shifts until bit 10 is set
+        uint32_t m = (mant << lz) & 0x03FFu;
+        uint32_t e = 113u - lz;
+        return bits_f(sign | (e << 23) | (m << 13));
+    }
+    if (exp == 31) return bits_f(sign | 0x7F800000u | (mant << 13));
+    return bits_f(sign | ((exp + 112u) << 23) | (mant << 13));
+}
+
+// prng.rs:98-130
+__device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
+    int32_t p = (int32_t)f_bits(v);
+    int32_t a = p & 0x7FFFFFFF;
+    int32_t ex = (a >> 23) & 0xFF;
+    int32_t sub = 113 - ex;
+    sub = sub > 0 ? sub : 0;
+    sub = sub < 11 ? sub : 11;
+    int32_t mask = (int32_t)((1u << (13 + sub)) - 1u);
+    int32_t noise = prng(seed, off) & mask;
+    int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
+    int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
+    return f16_to_f32(f32_to_f16_rne(bits_f((uint32_t)((p & (int32_t)0x80000000u) | r))));
+}
+
+__device__ __forceinline__ float rne_fp16(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
+
+// prng.rs:180-195; dtype is a compile-time constant at every call site.
+template <int DT>
+__device__ __forceinline__ float quantize(float v, int32_t seed, int32_t off, bool sr) {
+    if constexpr (DT == LV_DTYPE_BF16) {
+        return sr ? sr_bf16(v, seed, off) : rne_bf16(v);
+    } else if constexpr (DT == LV_DTYPE_F16) {
+        return sr ? sr_fp16(v, seed, off) : rne_fp16(v);
+    } else {
+        return v;
+    }
+}
+
+// math.rs:4-11
+__device__ __forceinline__ float sanitize(float g) {
+    return (__builtin_isfinite(g) && fabsf(g) < 1.0e38f) ? rclamp(g, -1.0e18f, 1.0e18f) : 0.0f;
+}
+
+// math.rs:83-118 -- [13/6] Pade tanh, Horner with fma.
+__device__ __forceinline__ float tanh_pade(float x_in) {
+    if (__builtin_isnan(x_in)) return bits_f(0x7FC00000u);  // Rust f32::NAN
+    float x = rclamp(x_in, -7.9988117f, 7.9988117f);
+    float x2 = x * x;
+    float p = __builtin_fmaf(-2.7607684e-16f, x2, 2.000188e-13f);
+    float q = __builtin_fmaf(1.1982584e-6f, x2, 1.1853471e-4f);
+    p = __builtin_fmaf(p, x2, -8.604672e-11f);
+    q = __builtin_fmaf(q, x2, 2.2684346e-3f);
+    p = __builtin_fmaf(p, x2, 5.122297e-8f);
+    q = __builtin_fmaf(q, x2, 4.8935246e-3f);
+    p = __builtin_fmaf(p, x2, 1.4857224e-5f);
+    p = __builtin_fmaf(p, x2, 6.3726193e-4f);
+    p = __builtin_fmaf(p, x2, 4.8935246e-3f);
+    return (x * p) / q;
+}
+
+// math.rs:162-186
+template <bool TRI>
+__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio) {
+    if constexpr (TRI) {
+        float b = ratio * (fabsf(p_init) + 1.0e-2f);
+        float bb = b * (b + fabsf(step));
+        return (bb * step) / __builtin_fmaf(step, step, bb);
+    } else {
+        float b = ratio * __builtin_sqrtf(__builtin_fmaf(p_init, p_init, 1.0e-4f));
+        return b * tanh_pade(step / b);
+    }
+}
+
+template <bool TRI>
+__device__ __forceinline__ float fp16_safety_bound(float step, float p_init) {
+    float b = __builtin_fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);
+    if constexpr (TRI) {
+        float bb = b * (b + fabsf(step));
+        return (bb * step) / __builtin_fmaf(step, step, bb);
+    } else {
+        return b * tanh_pade(step / b);
+    }
+}
+
+// math.rs:120-125
+__device__ __forceinline__ float cautious_scale(float mask_sum, float total, float clamp_min) {
+    float denom = __builtin_fmaxf(total, 1.0f);
+    return 1.0f / rclamp(mask_sum / denom, clamp_min, 1.0f);
+}
+
+// Round-to-nearest-even u64 -> f32 (Rust `as f32`), exact integer algorithm.
+__device__ __forceinline__ float u64_to_f32_rn(uint64_t x) {
+    if ((x >> 24) == 0) return (float)(uint32_t)x;
+    int bits = 64 - __clzll((long long)x);
+    int sh = bits - 24;
+    uint64_t mant = x >> sh;
+    uint64_t rem = x & ((1ull << sh) - 1ull);
+    uint64_t half = 1ull << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1ull))) mant += 1ull;
+    return ldexpf((float)(uint32_t)mant, sh);
+}
+
+// u, m_new, v_new for one element.
+// CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
+template <int MODE>
+__device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g, float m, float v,
+                                           float &m_new, float &v_new) {
+    m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
+    if constexpr (MODE == LV_BUFFER_DUAL) {
+        float clm = __builtin_fmaf(a.b1, m_new, a.omb1 * g);
+        float diff = rclamp(g - m_new, -1.0e18f, 1.0e18f);
+        v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
+        if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
+        float sigma = __builtin_fmaf(__builtin_sqrtf(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
+        return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
+    } else if constexpr (MODE == LV_BUFFER_T2) {
+        float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        float diff = rclamp(g - m, -1.0e18f, 1.0e18f);
+        v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
+        if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+        float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
+        float env = __builtin_fmaf(a.c_sigma, __builtin_sqrtf(__builtin_fmaxf(v_new, 0.0f)), env2);
+        return clm / env;
+    } else {
+        float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        float diff = rclamp(g - m, -1.0e18f, 1.0e18f);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+        float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
+        v_new = 0.0f;
+        return clm / env;
+    }
+}
+
+// ------------------------------------------------------------------ loads / stores
+
+template <int DT>
+__device__ __forceinline__ void load8(const void *base, uint64_t i, float out[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + i);
+        float4 x = q[0], y = q[1];
+        out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+        out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
+    } else {
+        uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + i);
+        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (DT == LV_DTYPE_BF16) {
+                out[2 * k] = bits_f(ws[k] << 16);
+                out[2 * k + 1] = bits_f(ws[k] & 0xFFFF0000u);
+            } else {
+                out[2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                out[2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void *base, uint64_t i, const float in[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        float4 *q = reinterpret_cast<float4 *>(static_cast<float *>(base) + i);
+        q[0] = make_float4(in[0], in[1], in[2], in[3]);
+        q[1] = make_float4(in[4], in[5], in[6], in[7]);
+    } else {
+        uint32_t ws[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t lo, hi;
+            if constexpr (DT == LV_DTYPE_BF16) {
+                lo = f_bits(in[2 * k]) >> 16;  // values are already bf16-exact (worker.rs:55-63)
+                hi = f_bits(in[2 * k + 1]) & 0xFFFF0000u;
+            } else {
+                lo = f32_to_f16_rne(in[2 * k]);
+                hi = f32_to_f16_rne(in[2 * k + 1]) << 16;
+            }
+            ws[k] = lo | hi;
+        }
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(base) + i) = make_uint4(ws[0], ws[1], ws[2], ws[3]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float load1(const void *base, uint64_t i) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        return static_cast<const float *>(base)[i];
+    } else if constexpr (DT == LV_DTYPE_BF16) {
+        return bits_f((uint32_t) static_cast<const uint16_t *>(base)[i] << 16);
+    } else {
+        return f16_to_f32(static_cast<const uint16_t *>(base)[i]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store1(void *base, uint64_t i, float x) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        static_cast<float *>(base)[i] = x;
+    } else if constexpr (DT == LV_DTYPE_BF16) {
+        static_cast<uint16_t *>(base)[i] = (uint16_t)(f_bits(x) >> 16);
+    } else {
+        static_cast<uint16_t *>(base)[i] = (uint16_t)f32_to_f16_rne(x);
+    }
+}
+
+__device__ __forceinline__ void load8_dyn(int dt, const void *base, uint64_t i, float out[8]) {
+    if (dt == LV_DTYPE_BF16) load8<LV_DTYPE_BF16>(base, i, out);
+    else if (dt == LV_DTYPE_F32) load8<LV_DTYPE_F32>(base, i, out);
+    else load8<LV_DTYPE_F16>(base, i, out);
+}
+
+__device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i) {
+    if (dt == LV_DTYPE_BF16) return load1<LV_DTYPE_BF16>(base, i);
+    if (dt == LV_DTYPE_F32) return load1<LV_DTYPE_F32>(base, i);
+    return load1<LV_DTYPE_F16>(base, i);
+}
+
+// ------------------------------------------------------------------ element update
+
+struct Seeds {
+    int32_t m, p, v;
+};
+
+// Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
+// Returns the cautious mask bit.
+template <int MODE, int PT, int ST>
+__device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const Seeds &sd, int32_t off,
+                                               float cs, float bs, float p_init, float g_raw, float &m_io,
+                                               float &v_io, float &p_out, float &mp_out) {
+    constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    const bool sr = flags & kFSR;
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    bool active = (u * g) > 0.0f;
+    float m_mask = active ? 1.0f : 0.0f;
+    m_io = quantize<ST>(m_new, sd.m, off, sr);
+    if constexpr (kDual) v_io = quantize<ST>(v_new, sd.v, off, sr);
+    float delta = (flags & kFCautious) ? (u * m_mask) * cs : u;
+    float step = a.lr * delta;
+    if (flags & kFRadial) step *= bs;
+    else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio);
+    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init);
+    float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
+    float p_upd = p_dec - step;
+    if (flags & kFMaster) {
+        mp_out = p_upd;
+        p_out = quantize<PT>(p_upd, sd.p, off, false);
+    } else {
+        p_out = quantize<PT>(p_upd, sd.p, off, sr);
+    }
+    return active ? 1u : 0u;
+}
+
+// Counting path for one element (dual.rs:279-303, dual.rs:720-746, tdclm.rs:232-248).
+template <int MODE>
+__device__ __forceinline__ uint32_t count_elem(const Args &a, uint32_t flags, float g_raw, float m, float v) {
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, flags & kFClampV, g, m, v, m_new, v_new);
+    return (u * g) > 0.0f ? 1u : 0u;
+}
+
+// ------------------------------------------------------------------ scratch finalisation
+
+// Last block of tensor t: dual.rs:255-259 + math.rs:188-239 (fused), dual.rs:330-351 +
+// dual.rs:436-438 (two-pass count).  Thread 0 only.
+template <int PASS>
+__device__ void finalize_scratch(const Args &a, const Desc &D, unsigned long long mask_count) {
+    float *s = D.scratch;
+    const bool cautious = a.flags & kFCautious;
+    float mask_sum = u64_to_f32_rn(mask_count);
+    float total = u64_to_f32_rn(D.n);
+    float s3;
+    if constexpr (PASS == kFused) {
+        s3 = cautious ? __builtin_fmaf(a.ema, s[3], a.ema_c * cautious_scale(mask_sum, total, a.clamp_min)) : 1.0f;
+    } else {
+        s3 = cautious ? cautious_scale(mask_sum, total, a.clamp_min) : 1.0f;
+    }
+    s[0] = 0.0f;
+    s[1] = 0.0f;
+    s[2] = 0.0f;
+    s[3] = s3;
+    s[4] = 1.0f;
+    s[5] = 0.0f;
+}
+
+// Block-wide sum of the per-thread mask counts, then the per-tensor ticket.
+template <int PASS>
+__device__ void flush_tensor(const Args &a, int t, uint32_t n_units, uint32_t cnt, uint32_t units_here,
+                             uint32_t *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; w++) tot += red[w];
+        unsigned long long *ctr = a.counters + 2 * t;
+        if (tot) atomicAdd(&ctr[0], (unsigned long long)tot);
+        __threadfence();
+        unsigned long long prev = atomicAdd(&ctr[1], (unsigned long long)units_here);
+        if (prev + units_here == (unsigned long long)n_units) {
+            __threadfence();
+            unsigned long long total = atomicAdd(&ctr[0], 0ull);
+            finalize_scratch<PASS>(a, a.d[t], total);
+            atomicExch(&ctr[0], 0ull);
+            atomicExch(&ctr[1], 0ull);
+        }
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ the kernel
+
+template <int MODE, int PT, int ST, int PASS>
+__global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    __shared__ uint32_t red[kThreads / 64];
+
+    const uint32_t flags = a.flags;
+    const int gdt = (int)((flags >> 8) & 3u);
+    const bool master = flags & kFMaster;
+    const uint32_t total_units = a.total_units;
+
+    int t = -1;
+    uint32_t t_begin = 0, t_end = 0;
+    uint64_t n = 0;
+    bool vec_ok = false;
+    float cs = 1.0f, bs = 1.0f;
+    Seeds sd{0, 0, 0};
+    uint32_t cnt = 0, units_here = 0;
+
+    for (uint32_t unit = blockIdx.x; unit < total_units; unit += gridDim.x) {
+        if (unit >= t_end) {
+            if constexpr (kCounting) {
+                if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
+            }
+            int lo = t + 1, hi = a.ndesc - 1;  // units only grow, so search right of t
+            while (lo < hi) {
+                int mid = (lo + hi + 1) >> 1;
+                if (a.d[mid].unit_begin <= unit) lo = mid;
+                else hi = mid - 1;
+            }
+            t = lo;
+            const Desc &D = a.d[t];
+            t_begin = D.unit_begin;
+            t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : total_units;
+            n = D.n;
+            uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
+            if (kDual) al |= (uintptr_t)D.v;
+            if (master) al |= (uintptr_t)D.mp;
+            vec_ok = (al & 15u) == 0;
+            uint32_t raw = a.seed_base + D.pidx * 10007u;
+            sd.m = (int32_t)(raw & 0x7FFFFFFFu);
+            sd.p = (int32_t)(((uint32_t)sd.m + 0x55555555u) & 0x7FFFFFFFu);
+            sd.v = (int32_t)(((uint32_t)sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
+            if constexpr (PASS == kFused || PASS == kApply) {
+                cs = D.scratch[3];
+                bs = D.scratch[4];
+            }
+            if constexpr (PASS == kSingle) {
+                // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
+                // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
+                if (unit == t_begin && threadIdx.x == 0) {
+                    float *s = D.scratch;
+                    s[0] = 0.0f; s[1] = 0.0f; s[2] = 0.0f; s[3] = 1.0f; s[4] = 1.0f; s[5] = 0.0f;
+                }
+            }
+            cnt = 0;
+            units_here = 0;
+        }
+        const Desc &D = a.d[t];
+        const uint64_t e0 = (uint64_t)(unit - t_begin) * kUnit + (uint64_t)threadIdx.x * kVec;
+        if (vec_ok && e0 + kVec <= n) {
+            float g[8], m[8], v[8], pin[8];
+            load8_dyn(gdt, D.g, e0, g);
+            load8<ST>(D.m, e0, m);
+            if constexpr (kDual) load8<ST>(D.v, e0, v);
+            if constexpr (PASS == kCount) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f);
+            } else {
+                if (master) load8<LV_DTYPE_F32>(D.mp, e0, pin);
+                else load8<PT>(D.p, e0, pin);
+                float pout[8], mpout[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    float vj = kDual ? v[j] : 0.0f;
+                    uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)(e0 + j), cs, bs, pin[j],
+                                                            g[j], m[j], vj, pout[j], mpout[j]);
+                    if constexpr (kDual) v[j] = vj;
+                    if constexpr (kCounting) cnt += act;
+                }
+                store8<PT>(D.p, e0, pout);
+                if (master) store8<LV_DTYPE_F32>(D.mp, e0, mpout);
+                store8<ST>(D.m, e0, m);
+                if constexpr (kDual) store8<ST>(D.v, e0, v);
+            }
+        } else if (e0 < n) {
+            const uint64_t e1 = (e0 + kVec < n) ? e0 + kVec : n;
+            for (uint64_t i = e0; i < e1; i++) {
+                float g = load1_dyn(gdt, D.g, i);
+                float m = load1<ST>(D.m, i);
+                float v = kDual ? load1<ST>(D.v, i) : 0.0f;
+                if constexpr (PASS == kCount) {
+                    cnt += count_elem<MODE>(a, flags, g, m, v);
+                } else {
+                    float pin = master ? D.mp[i] : load1<PT>(D.p, i);
+                    float pout, mpout;
+                    uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)i, cs, bs, pin, g, m, v,
+                                                            pout, mpout);
+                    store1<PT>(D.p, i, pout);
+                    if (master) D.mp[i] = mpout;
+                    store1<ST>(D.m, i, m);
+                    if constexpr (kDual) store1<ST>(D.v, i, v);
+                    if constexpr (kCounting) cnt += act;
+                }
+            }
+        }
+        units_here++;
+    }
+    if constexpr (kCounting) {
+        if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
+    }
+}
+
+// ------------------------------------------------------------------ host side
+
+using KernelFn = void (*)(Args);
+
+template <int MODE, int PT, int ST>
+KernelFn pick_pass(int pass) {
+    switch (pass) {
+    case kSingle: return step_kernel<MODE, PT, ST, kSingle>;
+    case kFused: return step_kernel<MODE, PT, ST, kFused>;
+    case kCount: return step_kernel<MODE, PT, ST, kCount>;
+    default: return step_kernel<MODE, PT, ST, kApply>;
+    }
+}
+
+template <int MODE, int PT>
+KernelFn pick_state(int st, int pass) {
+    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass) : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass);
+}
+
+template <int MODE>
+KernelFn pick_param(int pt, int st, int pass) {
+    switch (pt) {
+    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass);
+    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass);
+    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass);
+    }
+}
+
+static KernelFn pick_kernel(int mode, int pt, int st, int pass) {
+    switch (mode) {
+    case LV_BUFFER_TDCLM: return pick_param<LV_BUFFER_TDCLM>(pt, st, pass);
+    case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass);
+    case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass);
+    default: return pick_param<LV_BUFFER_T2>(pt, st, pass);
+    }
+}
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+// compiler-builtins' __powidf2 (the lowering of Rust f64::powi): repeated squaring.
+static double powi_rs(double a, int32_t b) {
+    bool recip = b < 0;
+    uint32_t pw = recip ? (uint32_t)(-(int64_t)b) : (uint32_t)b;
+    double mul = 1.0;
+    for (;;) {
+        if (pw & 1u) mul *= a;
+        pw >>= 1;
+        if (pw == 0) break;
+        a *= a;
+    }
+    return recip ? 1.0 / mul : mul;
+}
+
+struct StepCoeffs {
+    float c1, c2, c_sigma;
+};
+
+// math.rs:27-81
+static StepCoeffs step_coeffs(uint64_t step, float beta1, float beta2, float eps, float tau, float lam) {
+    uint64_t safe = step > 1 ? step : 1;
+    double b1 = (double)beta1, b2 = (double)beta2;
+    double bc1 = safe < 2147483647ull ? 1.0 - powi_rs(b1, (int32_t)(safe + 1)) : 1.0 - std::pow(b1, (double)(safe + 1));
+    double bc2_raw = safe <= 2147483647ull ? 1.0 - powi_rs(b2, (int32_t)safe) : 1.0 - std::pow(b2, (double)safe);
+    double bc2 = std::fmax(bc2_raw, 1.0e-15);
+    StepCoeffs c;
+    c.c1 = (float)((bc1 * (double)tau) / std::sqrt(bc2));
+    c.c2 = (float)((double)eps * bc1 * (double)tau);
+    float bc2f = (float)bc2;
+    c.c_sigma = (0.5f * lam) / std::sqrt(std::fmax(bc2f, 1.0e-15f));
+    return c;
+}
+
+static int validate_config(const lv_config *c) {
+    auto fin = [](float x) { return std::isfinite(x); };
+    if (!fin(c->lr) || c->lr < 0.0f) return fail(LV_STATUS_INVALID_CONFIG, "Invalid learning rate: %g", c->lr);
+    if (!fin(c->beta1) || !(c->beta1 >= 0.0f && c->beta1 < 1.0f))
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid beta1 parameter: %g", c->beta1);
+    if (!fin(c->beta2) || !(c->beta2 >= 0.0f && c->beta2 < 1.0f))
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid beta2 parameter: %g", c->beta2);
+    if (!fin(c->eps) || c->eps <= 0.0f) return fail(LV_STATUS_INVALID_CONFIG, "Invalid epsilon value: %g", c->eps);
+    if (!fin(c->weight_decay) || c->weight_decay < 0.0f)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid weight_decay value: %g", c->weight_decay);
+    if (!fin(c->tau) || c->tau <= 0.0f) return fail(LV_STATUS_INVALID_CONFIG, "Invalid tau parameter: %g", c->tau);
+    if (!fin(c->lam) || c->lam < 0.0f) return fail(LV_STATUS_INVALID_CONFIG, "Invalid lam parameter: %g", c->lam);
+    if (!fin(c->cautious_clamp_min) || c->cautious_clamp_min <= 0.0f || c->cautious_clamp_min > 1.0f)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid cautious_clamp_min: %g", c->cautious_clamp_min);
+    if (!fin(c->bound_ratio) || c->bound_ratio <= 0.0f)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid bound_ratio: %g", c->bound_ratio);
+    if (!fin(c->ema_decay) || c->ema_decay <= 0.0f || c->ema_decay >= 1.0f)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid ema_decay: %g", c->ema_decay);
+    if (c->buffer < 1 || c->buffer > 4) return fail(LV_STATUS_INVALID_CONFIG, "Invalid buffer count: %d", c->buffer);
+    if (c->bound_type < 0 || c->bound_type > 2)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid bound_type: %d", c->bound_type);
+    if (c->master_weights < 0 || c->master_weights > 2)
+        return fail(LV_STATUS_INVALID_CONFIG, "Invalid master_weights: %d", c->master_weights);
+    return LV_STATUS_SUCCESS;
+}
+
+static int blocks_per_launch_cap() {
+    static int cap[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 2048;
+    if (cap[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        int per_cu = 8;
+        if (const char *e = std::getenv("LV_BLOCKS_PER_CU")) {
+            int v = std::atoi(e);
+            if (v > 0 && v <= 64) per_cu = v;
+        }
+        cap[dev] = cus * per_cu;
+    }
+    return cap[dev];
+}
+
+struct Item {
+    int idx;      // position in the caller's array (workspace slot)
+    int pass;     // first pass of this tensor
+    int pt, gt, st;
+    bool master;
+    bool clampv;  // fp16 param or fp16 state container: v <= 65000 (dual.rs:68-71)
+    uint64_t step;
+};
+
+static int launch(const Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
+    KernelFn fn = pick_kernel(mode, pt, st, pass);
+    uint32_t grid = std::min<uint32_t>(args.total_units, (uint32_t)blocks_per_launch_cap());
+    if (grid == 0) return LV_STATUS_SUCCESS;
+    void *kargs[] = {const_cast<Args *>(&args)};
+    hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(grid), dim3(kThreads), kargs, 0, stream);
+    if (e != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "kernel launch failed: %s", hipGetErrorString(e));
+    return LV_STATUS_SUCCESS;
+}
+
+}  // namespace lv
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+int lv_version(void) { return 100; }
+
+size_t lv_workspace_bytes(int n_tensors) {
+    if (n_tensors < 1) n_tensors = 1;
+    size_t b = (size_t)n_tensors * 2 * sizeof(unsigned long long);
+    return (b + 255) & ~(size_t)255;
+}
+
+const char *lv_last_error(void) { return lv::g_err; }
+
+int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, void *workspace,
+                  size_t workspace_bytes, void *stream_ptr) {
+    using namespace lv;
+    g_err[0] = 0;
+    if (!cfg) return fail(LV_STATUS_NULL_POINTER, "config is NULL");
+    if (count < 0) return fail(LV_STATUS_INVALID_CONFIG, "negative tensor count");
+    if (count == 0) return LV_STATUS_SUCCESS;
+    if (!tensors) return fail(LV_STATUS_NULL_POINTER, "tensor list is NULL");
+    int rc = validate_config(cfg);
+    if (rc != LV_STATUS_SUCCESS) return rc;
+    const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;  // config.rs:368-375
+    if (bound == LV_BOUND_RADIAL)
+        return fail(LV_STATUS_INVALID_CONFIG, "bound_type='radial' is not supported by this build of the HIP backend");
+    const bool dual = cfg->buffer == LV_BUFFER_DUAL || cfg->buffer == LV_BUFFER_T2;
+    const bool cautious = cfg->cautious != 0;
+    if (!workspace) return fail(LV_STATUS_NULL_POINTER, "workspace is NULL");
+    if (workspace_bytes < lv_workspace_bytes(count))
+        return fail(LV_STATUS_INVALID_CONFIG, "workspace too small: %zu < %zu", workspace_bytes, lv_workspace_bytes(count));
+    if (((uintptr_t)workspace & 15u) != 0) return fail(LV_STATUS_INVALID_CONFIG, "workspace must be 16-byte aligned");
+
+    std::vector<Item> items;
+    items.reserve(count);
+    for (int i = 0; i < count; i++) {
+        const lv_tensor &T = tensors[i];
+        if (T.numel == 0) continue;
+        if (!T.param || !T.grad || !T.exp_avg || !T.scratch)
+            return fail(LV_STATUS_NULL_POINTER, "tensor %d: null param/grad/exp_avg/scratch pointer", i);
+        if (dual && !T.exp_avg_sq)
+            return fail(LV_STATUS_NULL_POINTER, "tensor %d: Dual-buffer mode requires an initialized exp_avg_sq buffer", i);
+        if (T.param_dtype < 0 || T.param_dtype > 2 || T.grad_dtype < 0 || T.grad_dtype > 2 || T.state_dtype < 0 ||
+            T.state_dtype > 2)
+            return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: invalid dtype code", i);
+        if (T.step == 0) return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: step must be >= 1", i);
+        if (T.numel > (uint64_t)0xFFFFFFFFull * kUnit)
+            return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many elements", i);
+        // worker.rs:95-98 and worker.rs:153-156: an fp32 param aliasing its master has none.
+        bool mp_present = T.master_param && !(T.param_dtype == LV_DTYPE_F32 && (void *)T.master_param == T.param);
+        bool master = cfg->master_weights != 0 && mp_present;
+        if (cfg->master_weights != 0 && !mp_present && T.param_dtype != LV_DTYPE_F32)
+            return fail(LV_STATUS_NULL_POINTER, "tensor %d: Master weight mode requires an initialized master_param buffer", i);
+        if (T.grad == T.param || T.grad == T.exp_avg)
+            return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: grad aliases mutable state", i);  // mod.rs:310-318
+        Item it;
+        it.idx = i;
+        it.pt = T.param_dtype;
+        it.gt = T.grad_dtype;
+        it.st = T.state_dtype == LV_DTYPE_F32 ? LV_DTYPE_F32 : LV_DTYPE_BF16;  // fp16 state -> bf16 bits (worker.rs:107-113)
+        it.master = master;
+        it.clampv = T.param_dtype == LV_DTYPE_F16 || T.state_dtype == LV_DTYPE_F16;
+        it.step = T.step;
+        if (!cautious && bound != LV_BOUND_RADIAL) it.pass = kSingle;
+        else if (cfg->fused_single_pass && T.step > 1) it.pass = kFused;
+        else it.pass = kCount;
+        items.push_back(it);
+    }
+    if (items.empty()) return LV_STATUS_SUCCESS;
+
+    // Launch classes: identical (pass, step, dtypes, master). Stable order keeps the caller's order.
+    std::stable_sort(items.begin(), items.end(), [](const Item &x, const Item &y) {
+        if (x.pass != y.pass) return x.pass < y.pass;
+        if (x.step != y.step) return x.step < y.step;
+        if (x.pt != y.pt) return x.pt < y.pt;
+        if (x.gt != y.gt) return x.gt < y.gt;
+        if (x.st != y.st) return x.st < y.st;
+        if (x.clampv != y.clampv) return x.clampv < y.clampv;
+        return x.master < y.master;
+    });
+
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    unsigned long long *ctr = static_cast<unsigned long long *>(workspace);
+    size_t begin = 0;
+    while (begin < items.size()) {
+        const Item &h = items[begin];
+        size_t end = begin + 1;
+        while (end < items.size() && end - begin < (size_t)kMaxDesc) {
+            const Item &x = items[end];
+            if (x.pass != h.pass || x.step != h.step || x.pt != h.pt || x.gt != h.gt || x.st != h.st ||
+                x.master != h.master || x.clampv != h.clampv)
+                break;
+            end++;
+        }
+        Args args;
+        std::memset(&args, 0, sizeof args);
+        args.lr = cfg->lr;
+        args.b1 = cfg->beta1;
+        args.b2 = cfg->beta2;
+        args.omb1 = 1.0f - cfg->beta1;
+        args.omb2 = 1.0f - cfg->beta2;
+        args.b1sq = cfg->beta1 * cfg->beta1;
+        args.omb1sq = 1.0f - args.b1sq;
+        args.eps = cfg->eps;
+        args.lam = cfg->lam;
+        args.lam1 = 0.5f * cfg->lam;
+        args.neg_lr_wd = -(cfg->lr * cfg->weight_decay);
+        args.ratio = cfg->bound_ratio;
+        StepCoeffs sc = step_coeffs(h.step, cfg->beta1, cfg->beta2, cfg->eps, cfg->tau, cfg->lam);
+        args.c1 = sc.c1;
+        args.c2 = sc.c2;
+        args.c_sigma = sc.c_sigma;
+        args.ema = cfg->ema_decay;
+        args.ema_c = 1.0f - cfg->ema_decay;
+        args.clamp_min = cfg->cautious_clamp_min;
+        args.seed_base = (uint32_t)((uint64_t)cfg->seed + h.step * 0x9E3779B9ull);
+        uint32_t flags = 0;
+        if (cautious) flags |= kFCautious;
+        if (cfg->stochastic_rounding) flags |= kFSR;
+        if (h.master) flags |= kFMaster;
+        if (cfg->weight_decay != 0.0f) flags |= kFWeightDecay;
+        if (h.clampv) flags |= kFClampV;
+        if (bound == LV_BOUND_COORDINATE) flags |= kFCoordinate;
+        flags |= (uint32_t)h.gt << 8;
+        args.flags = flags;
+        uint64_t units = 0;
+        args.ndesc = (int32_t)(end - begin);
+        for (size_t k = begin; k < end; k++) {
+            const lv_tensor &T = tensors[items[k].idx];
+            Desc &D = args.d[k - begin];
+            D.p = T.param;
+            D.g = T.grad;
+            D.m = T.exp_avg;
+            D.v = T.exp_avg_sq;
+            D.mp = items[k].master ? T.master_param : nullptr;
+            D.scratch = T.scratch;
+            D.n = T.numel;
+            D.unit_begin = (uint32_t)units;
+            D.pidx = (uint32_t)T.param_index;
+            units += (T.numel + kUnit - 1) / kUnit;
+        }
+        if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
+        args.total_units = (uint32_t)units;
+        args.counters = ctr + 2 * begin;  // slots [begin, end) of this call's workspace
+        if (h.pass == kCount) {
+            rc = launch(args, cfg->buffer, h.pt, h.st, kCount, stream);
+            if (rc == LV_STATUS_SUCCESS) rc = launch(args, cfg->buffer, h.pt, h.st, kApply, stream);
+        } else {
+            rc = launch(args, cfg->buffer, h.pt, h.st, h.pass, stream);
+        }
+        if (rc != LV_STATUS_SUCCESS) return rc;
+        begin = end;
+    }
+    return LV_STATUS_SUCCESS;
+}
+
+int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq, float *master_param,
+                float *scratch, size_t num_elements, float lr, float beta1, float beta2, float eps,
+                float weight_decay, float tau, float lam, int buffer_mode, int cautious, int bound_mode,
+                float bound_ratio, uint64_t step, uint32_t seed, void *stream) {
+    using namespace lv;
+    static std::mutex mu;
+    static void *ws[64] = {nullptr};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(LV_STATUS_NO_DRIVER, "no HIP device");
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        if (!ws[dev]) {
+            void *p = nullptr;
+            if (hipMalloc(&p, lv_workspace_bytes(1)) != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "hipMalloc failed");
+            if (hipMemset(p, 0, lv_workspace_bytes(1)) != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "hipMemset failed");
+            ws[dev] = p;
+        }
+    }
+    lv_config c;
+    c.lr = lr;
+    c.beta1 = beta1;
+    c.beta2 = beta2;
+    c.eps = eps;
+    c.weight_decay = weight_decay;
+    c.tau = tau;
+    c.lam = lam;
+    c.cautious_clamp_min = 0.5f;
+    c.bound_ratio = bound_ratio;
+    c.ema_decay = (buffer_mode == LV_BUFFER_TDCLM || buffer_mode == LV_BUFFER_T1) ? 0.95f : 0.80f;
+    c.buffer = buffer_mode;
+    c.cautious = cautious;
+    c.stochastic_rounding = 1;
+    c.bound = 1;
+    c.bound_type = bound_mode;
+    c.master_weights = master_param ? 2 : 0;
+    c.fused_single_pass = 1;
+    c.seed = seed;
+    lv_tensor t;
+    std::memset(&t, 0, sizeof t);
+    t.param = param;
+    t.grad = grad;
+    t.exp_avg = exp_avg;
+    t.exp_avg_sq = exp_avg_sq;
+    t.master_param = master_param;
+    t.scratch = scratch;
+    t.numel = num_elements;
+    t.step = step;
+    t.param_index = 0;
+    t.param_dtype = t.grad_dtype = t.state_dtype = LV_DTYPE_F32;
+    return lv_step_multi(&c, &t, 1, ws[dev], lv_workspace_bytes(1), stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,231 @@
+"""ctypes binding of libluminav_hip.so (C ABI in include/luminav_hip.h) for ROCm tensors.
+
+This module is the whole device path of the optimizer: it turns a list of PyTorch-ROCm tensors
+into `lv_tensor` descriptors and calls `lv_step_multi` on the current stream. It replaces the
+reference's per-tensor Triton dispatch `LuminaVGpuMixin._step_gpu_group`
+(python/luminamoon/optimizer/gpu_backend.py:2603-2733). There is no fallback: if the shared
+library is missing the step raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Any, Dict, List, Optional, Sequence
+
+import torch
+
+_LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib")
+LIB_PATH = os.path.join(_LIB_DIR, "libluminav_hip.so")
+
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+BUFFER_CODES = {1: 1, 2: 2, "T1": 3, "T2": 4}
+
+STATUS_NAMES = {0: "SUCCESS", -1: "NULL_POINTER", -2: "NO_DRIVER", -3: "INVALID_CONFIG", -4: "EXECUTION_FAILED"}
+
+
+class LvConfig(ctypes.Structure):
+    _fields_ = [
+        ("lr", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("tau", ctypes.c_float),
+        ("lam", ctypes.c_float),
+        ("cautious_clamp_min", ctypes.c_float),
+        ("bound_ratio", ctypes.c_float),
+        ("ema_decay", ctypes.c_float),
+        ("buffer", ctypes.c_int32),
+        ("cautious", ctypes.c_int32),
+        ("stochastic_rounding", ctypes.c_int32),
+        ("bound", ctypes.c_int32),
+        ("bound_type", ctypes.c_int32),
+        ("master_weights", ctypes.c_int32),
+        ("fused_single_pass", ctypes.c_int32),
+        ("seed", ctypes.c_uint32),
+    ]
+
+
+class LvTensor(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("exp_avg", ctypes.c_void_p),
+        ("exp_avg_sq", ctypes.c_void_p),
+        ("master_param", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("numel", ctypes.c_uint64),
+        ("step", ctypes.c_uint64),
+        ("param_index", ctypes.c_uint64),
+        ("param_dtype", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("state_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+EXPORTED_SYMBOLS = ("lv_version", "lv_workspace_bytes", "lv_step_multi", "lv_step_f32", "lv_last_error")
+
+_lib: Optional[ctypes.CDLL] = None
+_lib_lock = threading.Lock()
+
+
+class HipBackendUnavailable(RuntimeError):
+    pass
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libluminav_hip.so and declare its signatures. Raises if it is not built."""
+    global _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise HipBackendUnavailable(
+                f"LuminaV HIP backend not built: {path} is missing. Run __graft_entry__.build() "
+                "(hipcc --offload-arch=gfx950) before stepping ROCm tensors."
+            )
+        L = ctypes.CDLL(path)
+        L.lv_version.restype = ctypes.c_int
+        L.lv_version.argtypes = []
+        L.lv_workspace_bytes.restype = ctypes.c_size_t
+        L.lv_workspace_bytes.argtypes = [ctypes.c_int]
+        L.lv_step_multi.restype = ctypes.c_int
+        L.lv_step_multi.argtypes = [
+            ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+            ctypes.c_void_p,
+        ]
+        f, P = ctypes.c_float, ctypes.c_void_p
+        L.lv_step_f32.restype = ctypes.c_int
+        L.lv_step_f32.argtypes = [P, P, P, P, P, P, ctypes.c_size_t, f, f, f, f, f, f, f, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, f, ctypes.c_uint64, ctypes.c_uint32, P]
+        L.lv_last_error.restype = ctypes.c_char_p
+        L.lv_last_error.argtypes = []
+        _lib = L
+        return L
+
+
+def make_config(group: Dict[str, Any]) -> LvConfig:
+    """C config from a normalised param group (python/luminamoon/optimizer/luminav.py:1825-1846)."""
+    return LvConfig(
+        float(group["lr"]), float(group["betas"][0]), float(group["betas"][1]), float(group["eps"]),
+        float(group["weight_decay"]), float(group["tau"]), float(group["lam"]), float(group["cautious_clamp_min"]),
+        float(group["bound_ratio"]), float(group["ema_decay"]), BUFFER_CODES[group["buffer"]],
+        int(bool(group["cautious"])), int(bool(group["stochastic_rounding"])), int(bool(group["bound"])),
+        int(group["bound_type"]), int(group["master_weights"]), int(bool(group["fused_single_pass"])),
+        int(group["seed"]) & 0xFFFFFFFF,
+    )
+
+
+class _Workspace:
+    """Per-device zero-filled counter workspace; kernels leave it zeroed after each call."""
+
+    def __init__(self) -> None:
+        self._bufs: Dict[Any, torch.Tensor] = {}
+
+    def get(self, device: torch.device, n_tensors: int) -> torch.Tensor:
+        need = int(load_library().lv_workspace_bytes(max(1, n_tensors)))
+        buf = self._bufs.get(device)
+        if buf is None or buf.numel() < need:
+            cap = max(need, 4096)
+            buf = torch.zeros(cap, dtype=torch.uint8, device=device)
+            self._bufs[device] = buf
+        return buf
+
+
+class HipStepper:
+    """Runs one optimizer step for a list of same-device tensors through lv_step_multi."""
+
+    def __init__(self) -> None:
+        self.workspace = _Workspace()
+
+    def step(
+        self,
+        group: Dict[str, Any],
+        params: Sequence[torch.Tensor],
+        grads: Sequence[torch.Tensor],
+        exp_avgs: Sequence[torch.Tensor],
+        exp_avg_sqs: Sequence[Optional[torch.Tensor]],
+        master_params: Sequence[Optional[torch.Tensor]],
+        scratches: Sequence[torch.Tensor],
+        steps: Sequence[int],
+        param_indices: Sequence[int],
+    ) -> None:
+        n = len(params)
+        if n == 0:
+            return
+        lib = load_library()
+        device = params[0].device
+        if device.type != "cuda":
+            raise RuntimeError(
+                "LuminaV (MI355X build) steps ROCm device tensors only; got a tensor on "
+                f"'{device}'. Move the model to the GPU before calling step()."
+            )
+        items = (LvTensor * n)()
+        for i in range(n):
+            p, g, m = params[i], grads[i], exp_avgs[i]
+            v, mp, sc = exp_avg_sqs[i], master_params[i], scratches[i]
+            for name, t in (("param", p), ("grad", g), ("exp_avg", m), ("scratch", sc)):
+                if t.device != device:
+                    raise ValueError(f"LuminaV: {name} of param index {param_indices[i]} is on {t.device}, expected {device}.")
+                if not t.is_contiguous():
+                    raise ValueError(f"LuminaV: {name} of param index {param_indices[i]} must be contiguous.")
+            numel = p.numel()
+            if g.numel() != numel or m.numel() != numel:
+                raise ValueError(
+                    f"Shape mismatch for param index {param_indices[i]}: param={numel}, grad={g.numel()}, exp_avg={m.numel()}."
+                )
+            if sc.dtype != torch.float32 or sc.numel() < 6:
+                raise ValueError(f"LuminaV: scratch of param index {param_indices[i]} must be float32[6].")
+            vp = 0
+            if v is not None:
+                if v.numel() != numel:
+                    raise ValueError(
+                        f"Shape mismatch for exp_avg_sq at param index {param_indices[i]}: expected {numel}, got {v.numel()}."
+                    )
+                if v.dtype != m.dtype:
+                    raise ValueError(
+                        f"DType mismatch between exp_avg ({m.dtype}) and exp_avg_sq ({v.dtype}) at param index {param_indices[i]}."
+                    )
+                if v.device != device or not v.is_contiguous():
+                    raise ValueError(f"LuminaV: exp_avg_sq of param index {param_indices[i]} must be contiguous on {device}.")
+                vp = v.data_ptr()
+            mpp = 0
+            if mp is not None:
+                if mp.numel() != numel:
+                    raise ValueError(
+                        f"Shape mismatch for master_param at param index {param_indices[i]}: expected {numel}, got {mp.numel()}."
+                    )
+                if mp.dtype != torch.float32:
+                    raise ValueError("Tensor/buffer 'master_param' must have dtype float32.")
+                if mp.device != device or not mp.is_contiguous():
+                    raise ValueError(f"LuminaV: master_param of param index {param_indices[i]} must be contiguous on {device}.")
+                mpp = mp.data_ptr()
+            items[i] = LvTensor(
+                p.data_ptr(), g.data_ptr(), m.data_ptr(), vp, mpp, sc.data_ptr(), numel, int(steps[i]),
+                int(param_indices[i]), DTYPE_CODES[p.dtype], DTYPE_CODES[g.dtype], DTYPE_CODES[m.dtype], 0,
+            )
+        cfg = make_config(group)
+        ws = self.workspace.get(device, n)
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device).cuda_stream
+            rc = lib.lv_step_multi(ctypes.byref(cfg), items, n, ws.data_ptr(), ws.numel(), stream)
+        if rc != 0:
+            msg = lib.lv_last_error().decode(errors="replace")
+            if rc in (-1, -3):
+                raise ValueError(f"LuminaV HIP step rejected the call ({STATUS_NAMES.get(rc, rc)}): {msg}")
+            raise RuntimeError(f"LuminaV HIP step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
+
+
+def device_info() -> Dict[str, Any]:
+    info: Dict[str, Any] = {"hip_backend_built": os.path.exists(LIB_PATH)}
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(torch.cuda.current_device())
+        info["gpu_device_name"] = props.name
+        info["gpu_arch"] = getattr(props, "gcnArchName", None)
+        info["compute_units"] = props.multi_processor_count
+        info["hbm_bytes"] = props.total_memory
+    else:
+        info["gpu_device_name"] = None
+    return info

@@ -1,0 +1,996 @@
+"""LuminaV optimizer: the drop-in `LuminaV(params, ...)` / `step()` surface over the HIP backend.
+
+Mirrors the reference class python/luminamoon/optimizer/luminav.py:
+  - constructor, defaults and alias normalisation with the same error strings (:175-470, :472-761);
+  - bounded contiguous bucket fusion with zero-copy views (:763-952) and its re-sync (:1293-1374);
+  - lazy per-parameter state allocation and step counting (:1665-1798);
+  - step routing, fused-bucket stepping with grad=None isolation (:1376-1606);
+  - state_dict / load_state_dict format (:1030-1292).
+The device work is one call of the C ABI lv_step_multi per (group, device) through
+hip_backend.HipStepper; there is no per-tensor kernel loop and no CPU compute fallback.
+
+Deliberate difference (the state-buffer allocation the MI355X path changes): 16-bit params get
+fp32 exp_avg / exp_avg_sq by default (`state_precision="fp32"`), which is what the reference's
+Rust core supports (python_ffi/mod.rs:57-125) and what the 7B bf16 bucket needs (12 B/param);
+`state_precision="param"` restores the reference Python default (state in the param dtype
+unless master_weights="full", luminav.py:1668-1672).
+"""
+from __future__ import annotations
+
+import logging
+import math
+import warnings
+from typing import Any, Callable, Dict, List, Optional, Set, Tuple, Union
+
+import torch
+from torch.optim import Optimizer
+
+from . import hip_backend
+from .constants import (
+    DEFAULT_BETAS,
+    DEFAULT_BOUND_RATIO,
+    DEFAULT_BUCKET_CAP_MB,
+    DEFAULT_CAUTIOUS_CLAMP_MIN,
+    DEFAULT_EPS,
+    DEFAULT_FUSE_TENSORS,
+    DEFAULT_FUSED_SINGLE_PASS,
+    DEFAULT_GPU_DISPATCH_THRESHOLD,
+    DEFAULT_LAM,
+    DEFAULT_LR,
+    DEFAULT_OPTIMIZER_SEED,
+    DEFAULT_PREWARM_JIT,
+    DEFAULT_STATE_PRECISION,
+    DEFAULT_TAU,
+    DEFAULT_WEIGHT_DECAY,
+    TEMP_STATE_DICT_KEYS,
+    VALID_BOUND_TYPE_CANDIDATES,
+    VALID_BUFFER_CANDIDATES,
+    VALID_EXECUTION_MODE_CANDIDATES,
+    VALID_MASTER_WEIGHTS_CANDIDATES,
+    VALID_STATE_PRECISION_CANDIDATES,
+)
+from .validation import is_valid_number, suggest_closest, validate_supported_dtype
+from .version import (
+    DEFAULT_LUMINAV_VERSION,
+    SUPPORTED_VERSIONS,
+    HybridVersionMethod,
+    get_capabilities,
+    validate_version,
+)
+
+logger = logging.getLogger("LuminaV")
+
+_BUFFER_ERR = "LuminaV only supports buffer=1 (Single-Buffer TD-CLM) or buffer=2 (Dual-Buffer CLM)."
+_SCRATCH_INIT = (0.0, 0.0, 0.0, 1.0, 1.0, 0.0)
+
+
+def _new_scratch(device: torch.device) -> torch.Tensor:
+    """ScratchBuffer::new() (luminav-core/src/state.rs:17-23)."""
+    return torch.tensor(_SCRATCH_INIT, dtype=torch.float32, device=device)
+
+
+# --------------------------------------------------------------------- fp16-container state codecs
+# An fp16 *state* container holds bfloat16 bits (worker.rs:107-113, luminav.py:1096-1101).
+
+def _decode_state_f32(buf: torch.Tensor) -> torch.Tensor:
+    if buf.dtype == torch.float16:
+        return buf.contiguous().view(torch.bfloat16).float()
+    return buf.float()
+
+
+def _encode_bf16_bits_rne(val: torch.Tensor) -> torch.Tensor:
+    """f32 -> bf16 bits with the reference's RNE (prng.rs:162-178: overflow clamps to max finite)."""
+    bits = val.contiguous().float().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    absb = bits & 0x7FFFFFFF
+    sign = bits & 0x80000000
+    lsb = (absb >> 16) & 1
+    rnd = (absb + 0x7FFF + lsb) & 0xFFFF0000
+    rnd = torch.minimum(rnd, torch.full_like(rnd, 0x7F7F0000))
+    out = sign | rnd
+    nan = absb > 0x7F800000
+    out = torch.where(nan, (bits | 0x00400000) & 0xFFFF0000, out)
+    hi = (out >> 16).to(torch.int32)
+    hi = torch.where(hi >= 0x8000, hi - 0x10000, hi).to(torch.int16)
+    return hi.view(torch.bfloat16)
+
+
+def _convert_state_buffer(src: torch.Tensor, device: torch.device, target: torch.dtype,
+                          fp16_is_bf16_bits: bool = True) -> torch.Tensor:
+    """Move a state buffer to `device`/`target`, honouring fp16 containers of bf16 bits
+    (reference luminav.py:124-146)."""
+    buf = src.to(device=device).contiguous()
+    if src.dtype == target:
+        if src.dtype == torch.float16 and not fp16_is_bf16_bits:
+            return _encode_bf16_bits_rne(buf.float()).view(torch.float16)
+        return buf.clone()
+    if src.dtype == torch.float16 or target == torch.float16:
+        val = _decode_state_f32(buf) if (src.dtype != torch.float16 or fp16_is_bf16_bits) else buf.float()
+        if target == torch.float16:
+            return _encode_bf16_bits_rne(val).view(torch.float16)
+        return val.to(dtype=target).contiguous()
+    return buf.to(dtype=target).contiguous()
+
+
+class LuminaV(Optimizer):
+    """LuminaV optimizer (CLM `buffer=2`, TD-CLM `buffer=1`, Triangle family `"T1"`/`"T2"`) on MI355X.
+
+    Same constructor and `step()` as the reference `luminamoon.LuminaV`; the update runs in
+    hand-written HIP kernels (libluminav_hip.so) and is bitwise equal to the reference CPU
+    implementation. Parameters must live on a ROCm device.
+    """
+
+    ALGORITHM_SPEC: str = DEFAULT_LUMINAV_VERSION
+    ALGORITHM_MATH: str = DEFAULT_LUMINAV_VERSION
+    _default_version: str = DEFAULT_LUMINAV_VERSION
+
+    def __init__(
+        self,
+        params,
+        lr: float = DEFAULT_LR,
+        betas: Tuple[float, float] = DEFAULT_BETAS,
+        eps: float = DEFAULT_EPS,
+        weight_decay: float = DEFAULT_WEIGHT_DECAY,
+        tau: float = DEFAULT_TAU,
+        lam: float = DEFAULT_LAM,
+        cautious: bool = True,
+        cautious_clamp_min: float = DEFAULT_CAUTIOUS_CLAMP_MIN,
+        buffer: Union[int, str] = 2,
+        stochastic_rounding: bool = True,
+        bound: bool = True,
+        bound_type: Union[int, str] = "coordinate",
+        bound_ratio: float = DEFAULT_BOUND_RATIO,
+        master_weights: Union[bool, int, str] = "none",
+        execution: Union[int, str] = "auto",
+        fused_single_pass: bool = DEFAULT_FUSED_SINGLE_PASS,
+        fuse_tensors: bool = DEFAULT_FUSE_TENSORS,
+        bucket_cap_mb: float = DEFAULT_BUCKET_CAP_MB,
+        prewarm_jit: bool = DEFAULT_PREWARM_JIT,
+        ema_decay: Optional[Union[float, str]] = "auto",
+        fsdp_sync: bool = False,
+        seed: int = DEFAULT_OPTIMIZER_SEED,
+        version: Optional[str] = None,
+        spec: Optional[str] = None,
+        state_precision: str = DEFAULT_STATE_PRECISION,
+    ):
+        chosen = version if version is not None else spec
+        self.version: str = validate_version(chosen if chosen is not None else self._default_version)
+        defaults: Dict[str, Any] = dict(
+            lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, tau=tau, lam=lam, cautious=cautious,
+            cautious_clamp_min=cautious_clamp_min, buffer=buffer, stochastic_rounding=stochastic_rounding,
+            bound=bound, bound_type=bound_type, bound_ratio=bound_ratio, master_weights=master_weights,
+            execution=execution, fused_single_pass=fused_single_pass, fuse_tensors=fuse_tensors,
+            bucket_cap_mb=bucket_cap_mb, prewarm_jit=prewarm_jit, ema_decay=ema_decay, fsdp_sync=fsdp_sync,
+            seed=seed, version=self.version, state_precision=state_precision,
+        )
+        is_auto_ema = ema_decay is None or (isinstance(ema_decay, str) and ema_decay.strip().lower() == "auto")
+        self._validate_and_normalize_group(defaults)
+        if is_auto_ema:
+            defaults["ema_decay"] = "auto"
+
+        param_list = list(params)
+        if len(param_list) == 0:
+            raise ValueError("optimizer got an empty parameter list")
+        first = param_list[0]
+        first_p = (first.get("params") or [None])[0] if isinstance(first, dict) else first
+        if not isinstance(first_p, torch.Tensor):
+            raise TypeError(
+                "LuminaV (MI355X build) optimizes torch.Tensor parameters on ROCm devices; "
+                f"got {type(first_p).__name__}."
+            )
+        explicit_cap = bucket_cap_mb != DEFAULT_BUCKET_CAP_MB or any(
+            isinstance(g, dict) and "bucket_cap_mb" in g for g in param_list
+        )
+        self._fused_buckets: List[Dict[str, Any]] = []
+        super().__init__(param_list, defaults)
+
+        self.seed = int(defaults["seed"])
+        self.fuse_tensors: bool = bool(defaults["fuse_tensors"])
+        self.bucket_cap_mb: float = float(defaults["bucket_cap_mb"])
+        self.prewarm_jit: bool = bool(defaults["prewarm_jit"])
+        self._stepper = hip_backend.HipStepper()
+
+        if any(bool(g.get("fuse_tensors", False)) for g in self.param_groups):
+            self.fuse_tensors = True
+            warnings.warn(
+                "LuminaV: 'fuse_tensors=True' is designed for vision and image models (e.g., CNN, ViT) with "
+                "many fragmented parameter layers. If you are training large language models (LLMs), "
+                "it is recommended to keep 'fuse_tensors=False' to avoid unnecessary memory overhead.",
+                UserWarning,
+                stacklevel=2,
+            )
+            self._build_contiguous_buckets()
+        elif explicit_cap:
+            warnings.warn(
+                f"LuminaV: 'bucket_cap_mb' was explicitly specified ({self.bucket_cap_mb} MB) "
+                "but 'fuse_tensors' is False. Bounded bucket chunking only applies when parameter "
+                "coalescing is enabled via 'fuse_tensors=True'. Parameters will be updated as "
+                "standard individual tensors without chunked memory bounds.",
+                UserWarning,
+                stacklevel=2,
+            )
+
+    # ------------------------------------------------------------------ versions
+
+    def _set_version_inst(self, version: str) -> "LuminaV":
+        self.version = validate_version(version)
+        self.defaults["version"] = self.version
+        for pg in self.param_groups:
+            pg["version"] = self.version
+        return self
+
+    @classmethod
+    def _set_version_cls(cls, version: str) -> str:
+        cls._default_version = validate_version(version)
+        return cls._default_version
+
+    def _get_version_inst(self) -> str:
+        return self.version
+
+    @classmethod
+    def _get_version_cls(cls) -> str:
+        return cls._default_version
+
+    set_version = HybridVersionMethod(_set_version_inst, _set_version_cls)
+    setVersion = set_version
+    set_spec = set_version
+    setSpec = set_version
+    get_version = HybridVersionMethod(_get_version_inst, _get_version_cls)
+    getVersion = get_version
+    get_spec = get_version
+    getSpec = get_version
+    get_math_version = get_version
+    getMathVersion = get_version
+
+    @property
+    def spec(self) -> str:
+        return self.version
+
+    @property
+    def math_version(self) -> str:
+        return self.version
+
+    @classmethod
+    def _list_versions_cls(cls) -> List[str]:
+        return list(SUPPORTED_VERSIONS)
+
+    def _list_versions_inst(self) -> List[str]:
+        return list(SUPPORTED_VERSIONS)
+
+    list_versions = HybridVersionMethod(_list_versions_inst, _list_versions_cls)
+    listVersions = list_versions
+
+    @classmethod
+    def _get_capabilities_cls(cls, version: Optional[str] = None) -> Dict[str, Any]:
+        return get_capabilities(version if version is not None else cls._default_version)
+
+    def _get_capabilities_inst(self, version: Optional[str] = None) -> Dict[str, Any]:
+        return get_capabilities(version if version is not None else self.version)
+
+    get_capabilities = HybridVersionMethod(_get_capabilities_inst, _get_capabilities_cls)
+    getCapabilities = get_capabilities
+
+    # ------------------------------------------------------------------ validation
+
+    _SIG_KEYS = (
+        "lr", "betas", "eps", "weight_decay", "tau", "lam", "cautious", "cautious_clamp_min", "buffer",
+        "stochastic_rounding", "bound", "bound_type", "bound_ratio", "master_weights", "execution",
+        "fused_single_pass", "fuse_tensors", "bucket_cap_mb", "prewarm_jit", "ema_decay", "fsdp_sync", "seed",
+        "version", "state_precision",
+    )
+
+    @staticmethod
+    def _compute_group_sig(group: Dict[str, Any]) -> Tuple[Any, ...]:
+        return tuple(group.get(k) for k in LuminaV._SIG_KEYS)
+
+    @staticmethod
+    def _validate_and_normalize_group(group: Dict[str, Any]) -> None:
+        """Validates and normalises one param group in place (reference luminav.py:472-761)."""
+        lr, betas, eps = group["lr"], group["betas"], group["eps"]
+        weight_decay, tau = group["weight_decay"], group["tau"]
+        lam = group.get("lam", DEFAULT_LAM)
+        cautious = group.get("cautious", True)
+        cautious_clamp_min = group["cautious_clamp_min"]
+        buffer = group["buffer"]
+        bound = group.get("bound", True)
+        bound_type = group["bound_type"]
+        bound_ratio = group["bound_ratio"]
+        master_weights = group["master_weights"]
+        execution = group["execution"]
+        fuse_tensors = group.get("fuse_tensors", DEFAULT_FUSE_TENSORS)
+        prewarm_jit = group.get("prewarm_jit", DEFAULT_PREWARM_JIT)
+        ema_decay = group.get("ema_decay", None)
+        fsdp_sync = group.get("fsdp_sync", False)
+        seed = group["seed"]
+        state_precision = group.get("state_precision", DEFAULT_STATE_PRECISION)
+
+        if not isinstance(fuse_tensors, bool):
+            raise ValueError(f"Invalid fuse_tensors: {fuse_tensors!r}. Expected a boolean (True or False).")
+        if not isinstance(prewarm_jit, bool):
+            raise ValueError(f"Invalid prewarm_jit: {prewarm_jit!r}. Expected a boolean (True or False).")
+        if not is_valid_number(lr) or float(lr) < 0.0:
+            raise ValueError(f"Invalid lr: {lr}. Expected a finite value in range [0.0, inf).")
+        if not isinstance(betas, (tuple, list)) or len(betas) != 2:
+            raise ValueError(
+                f"Invalid betas: {betas}. Expected a 2-tuple (beta1, beta2) with values in range [0.0, 1.0)."
+            )
+        if not is_valid_number(betas[0]) or not (0.0 <= float(betas[0]) < 1.0):
+            raise ValueError(f"Invalid beta1: {betas[0]}. Expected value in range [0.0, 1.0).")
+        if not is_valid_number(betas[1]) or not (0.0 <= float(betas[1]) < 1.0):
+            raise ValueError(f"Invalid beta2: {betas[1]}. Expected value in range [0.0, 1.0).")
+        if not is_valid_number(eps) or float(eps) <= 0.0:
+            raise ValueError(f"Invalid eps: {eps}. Expected value in range (0.0, inf).")
+        if not is_valid_number(weight_decay) or float(weight_decay) < 0.0:
+            raise ValueError(f"Invalid weight_decay: {weight_decay}. Expected value in range [0.0, inf).")
+        if not is_valid_number(tau) or float(tau) <= 0.0:
+            raise ValueError(f"Invalid tau: {tau}. Expected value in range (0.0, inf).")
+        if not is_valid_number(lam) or float(lam) < 0.0:
+            raise ValueError(f"Invalid lam: {lam}. Expected value in range [0.0, inf).")
+        if not is_valid_number(cautious_clamp_min) or not (0.0 < float(cautious_clamp_min) <= 1.0):
+            raise ValueError(
+                f"Invalid cautious_clamp_min: {cautious_clamp_min}. Expected value in range (0.0, 1.0]."
+            )
+        if not is_valid_number(bound_ratio) or float(bound_ratio) <= 0.0:
+            raise ValueError(f"Invalid bound_ratio: {bound_ratio}. Expected value in range (0.0, inf).")
+        if isinstance(seed, bool) or not isinstance(seed, int) or seed < 0:
+            raise ValueError(f"Invalid seed: {seed}. Expected a non-negative integer in range [0, 4294967295].")
+
+        # buffer (luminav.py:552-587)
+        if isinstance(buffer, bool):
+            raise ValueError(f"Invalid buffer count: {buffer}. {_BUFFER_ERR}")
+        if isinstance(buffer, int):
+            if buffer not in (1, 2):
+                raise ValueError(f"Invalid buffer count: {buffer}. {_BUFFER_ERR}")
+            buf_val: Union[int, str] = int(buffer)
+        elif isinstance(buffer, str):
+            b = buffer.strip().lower()
+            if b in ("1", "tdclm", "td-clm", "single"):
+                buf_val = 1
+            elif b in ("t2", "td-t2", "t2-clm", "td-dual", "triangle2", "clm-t2", "dual-t2"):
+                buf_val = "T2"
+            elif b in ("t1", "td-t1", "t1-clm", "triangle1", "td-clm-t1", "tdclm-t1"):
+                buf_val = "T1"
+            elif b in ("2", "dual", "clm"):
+                buf_val = 2
+            else:
+                sug = suggest_closest(buffer, VALID_BUFFER_CANDIDATES, 2)
+                hint = f" Did you mean '{sug}'?" if sug is not None else ""
+                raise ValueError(f"Invalid buffer count: '{buffer}'. {_BUFFER_ERR}{hint}")
+        else:
+            raise ValueError(f"Invalid buffer count: {buffer}. {_BUFFER_ERR}")
+
+        # version gates (luminav.py:589-605)
+        gver = str(group.get("version", DEFAULT_LUMINAV_VERSION)).strip().lstrip("v")
+        if gver in ("latest", "default", "reference", "canonical", "baseline"):
+            gver = DEFAULT_LUMINAV_VERSION
+        if gver in ("1.5.3", "1.5.4", "1.5.5") and buf_val in ("T1", "T2"):
+            raise ValueError(
+                f"LuminaV algorithm specification '{gver}' does not support Triangle Family buffer='{buffer}'. "
+                f"Triangle Family tanh-free modes ('T1', 'T2') were introduced in LuminaV >= '1.6.0'. "
+                f"To use '{buffer}', upgrade to version='1.6.0' (or omit version to use the default), or set buffer=2 / buffer=1."
+            )
+        if gver in ("1.5.3", "1.5.4") and bool(fuse_tensors):
+            raise ValueError(
+                f"LuminaV algorithm specification '{gver}' does not support contiguous bucket fusion (fuse_tensors=True). "
+                f"Bucket fusion was introduced in LuminaV >= '1.5.5'. "
+                f"To use fuse_tensors=True, upgrade to version >= '1.5.5' (or omit version to use default)."
+            )
+
+        # bound_type (luminav.py:607-633)
+        if isinstance(bound_type, str):
+            bt = bound_type.strip().lower()
+            if bt in ("radial", "1"):
+                bt_val = 1
+            elif bt in ("coordinate", "2"):
+                bt_val = 2
+            elif bt in ("none", "0") and not bound:
+                bt_val = 0
+            else:
+                sug = suggest_closest(bound_type, VALID_BOUND_TYPE_CANDIDATES, 3)
+                hint = f" Did you mean '{sug}'?" if sug is not None else ""
+                raise ValueError(f"Invalid bound_type: '{bound_type}'. Expected 'coordinate' or 'radial'.{hint}")
+        elif not isinstance(bound_type, bool) and isinstance(bound_type, int):
+            if bound_type not in (0, 1, 2):
+                raise ValueError(f"Invalid bound_type: {bound_type}. Expected 'coordinate' or 'radial'.")
+            bt_val = int(bound_type)
+        else:
+            raise ValueError(f"Invalid bound_type: {bound_type!r}. Expected 'coordinate' or 'radial'.")
+
+        # master_weights (luminav.py:635-665)
+        mw_err = "Expected False, 'none', 'semi', or 'full'."
+        if isinstance(master_weights, bool):
+            mw_val = 2 if master_weights else 0
+        elif isinstance(master_weights, int):
+            if master_weights not in (0, 1, 2):
+                raise ValueError(f"Invalid master_weights: {master_weights}. {mw_err}")
+            mw_val = int(master_weights)
+        elif isinstance(master_weights, str):
+            mw = master_weights.strip().lower()
+            if mw in ("none", "false", "off", "0"):
+                mw_val = 0
+            elif mw in ("semi", "hybrid", "half", "1"):
+                mw_val = 1
+            elif mw in ("full", "true", "fp32", "masterweight", "2"):
+                mw_val = 2
+            else:
+                sug = suggest_closest(master_weights, VALID_MASTER_WEIGHTS_CANDIDATES, 3)
+                hint = f" Did you mean '{sug}'?" if sug is not None else ""
+                raise ValueError(f"Invalid master_weights: '{master_weights}'. {mw_err}{hint}")
+        else:
+            raise ValueError(f"Invalid master_weights: {master_weights!r}. {mw_err}")
+
+        # execution (luminav.py:667-701); every mode runs the HIP kernels on ROCm tensors.
+        ex_err = "Expected 'auto', 'vulkan', 'simd', or 'scalar'."
+        if isinstance(execution, str):
+            ex = execution.strip().lower()
+            table = {"auto": 0, "foreach": 0, "0": 0, "triton": 1, "1": 1, "single": 2, "2": 2, "vulkan": 3,
+                     "3": 3, "simd": 4, "4": 4, "scalar": 5, "scalar_core": 5, "5": 5}
+            if ex not in table:
+                sug = suggest_closest(execution, VALID_EXECUTION_MODE_CANDIDATES, 3)
+                hint = f" Did you mean '{sug}'?" if sug is not None else ""
+                raise ValueError(f"Invalid execution mode: '{execution}'. {ex_err}{hint}")
+            ex_val = table[ex]
+        elif not isinstance(execution, bool) and isinstance(execution, int):
+            if not 0 <= execution <= 5:
+                raise ValueError(f"Invalid execution mode: {execution}. {ex_err}")
+            ex_val = int(execution)
+        else:
+            raise ValueError(f"Invalid execution mode: {execution!r}. {ex_err}")
+
+        # ema_decay (luminav.py:703-718)
+        if ema_decay is None or (isinstance(ema_decay, str) and ema_decay.strip().lower() == "auto"):
+            ema_val = 0.95 if buf_val in (1, "T1") else 0.80
+        elif is_valid_number(ema_decay):
+            ema_val = float(ema_decay)
+            if not 0.0 < ema_val < 1.0:
+                raise ValueError(f"Invalid ema_decay: {ema_decay}. Expected value in range (0.0, 1.0).")
+        else:
+            raise ValueError(
+                f"Invalid ema_decay: {ema_decay!r}. Expected 'auto', None, or a float in range (0.0, 1.0)."
+            )
+
+        if not isinstance(state_precision, str) or state_precision.strip().lower() not in VALID_STATE_PRECISION_CANDIDATES:
+            raise ValueError(f"Invalid state_precision: {state_precision!r}. Expected 'fp32' or 'param'.")
+
+        if fsdp_sync and not (torch.distributed.is_available() and torch.distributed.is_initialized()):
+            logger.warning(
+                "LuminaV: fsdp_sync=True was specified, but torch.distributed is not initialized. "
+                "Disabling fsdp_sync to prevent collective communication errors."
+            )
+            fsdp_sync = False
+
+        raw_cap = group.get("bucket_cap_mb", DEFAULT_BUCKET_CAP_MB)
+        if raw_cap is None or not is_valid_number(raw_cap) or float(raw_cap) <= 0.0:
+            raise ValueError(f"bucket_cap_mb must be a positive number, got: {raw_cap!r}")
+
+        group.update(
+            lr=float(lr), betas=(float(betas[0]), float(betas[1])), eps=float(eps), weight_decay=float(weight_decay),
+            tau=float(tau), lam=float(lam), cautious=bool(cautious), cautious_clamp_min=float(cautious_clamp_min),
+            buffer=buf_val, stochastic_rounding=bool(group.get("stochastic_rounding", True)), bound=bool(bound),
+            bound_type=bt_val, bound_ratio=float(bound_ratio), master_weights=mw_val, execution=ex_val,
+            fused_single_pass=bool(group.get("fused_single_pass", DEFAULT_FUSED_SINGLE_PASS)),
+            fuse_tensors=bool(fuse_tensors), bucket_cap_mb=float(raw_cap), prewarm_jit=bool(prewarm_jit),
+            ema_decay=ema_val, fsdp_sync=bool(fsdp_sync), seed=int(seed),
+            state_precision=state_precision.strip().lower(),
+        )
+        group["_validated_sig"] = LuminaV._compute_group_sig(group)
+
+    # ------------------------------------------------------------------ state policy
+
+    @staticmethod
+    def _state_dtype(p_dtype: torch.dtype, master_mode: int, precision: str) -> torch.dtype:
+        if master_mode == 2 or p_dtype == torch.float32 or precision == "fp32":
+            return torch.float32
+        return p_dtype
+
+    @staticmethod
+    def _radial_active(group: Dict[str, Any]) -> bool:
+        return bool(group.get("bound", True) and group.get("bound_type", 2) in (1, "radial")
+                    and float(group.get("bound_ratio", 0.05)) > 0.0)
+
+    # ------------------------------------------------------------------ bucket fusion
+
+    @staticmethod
+    def _partition_into_bounded_chunks(indexed_params: List[Tuple[int, Any]], cap_bytes: int) -> List[List[Tuple[int, Any]]]:
+        """Sequential chunks whose param bytes stay within cap_bytes (reference luminav.py:763-786)."""
+        chunks: List[List[Tuple[int, Any]]] = []
+        cur: List[Tuple[int, Any]] = []
+        cur_bytes = 0
+        for idx, p in indexed_params:
+            nb = int(p.numel() * p.element_size())
+            if cur and cur_bytes + nb > cap_bytes:
+                chunks.append(cur)
+                cur, cur_bytes = [(idx, p)], nb
+            else:
+                cur.append((idx, p))
+                cur_bytes += nb
+        if cur:
+            chunks.append(cur)
+        return chunks
+
+    def _build_contiguous_buckets(self, force_rebuild: bool = False) -> None:
+        """One flat p/g/m/v/master allocation per (group, device, dtype) chunk; params, grads and
+        state become views into it (reference luminav.py:788-952)."""
+        if force_rebuild:
+            self._fused_buckets.clear()
+        done_groups = {id(b["group"]) for b in self._fused_buckets}
+        seen: Set[Any] = {(p.device, p.data_ptr(), int(p.numel())) for b in self._fused_buckets for p, *_ in b["slices"]}
+        for group in self.param_groups:
+            if id(group) in done_groups or not group.get("fuse_tensors", False) or group.get("fsdp_sync", False):
+                continue
+            buf_count = group["buffer"]
+            master_mode = int(group["master_weights"])
+            precision = group.get("state_precision", DEFAULT_STATE_PRECISION)
+            cap_bytes = int(float(group.get("bucket_cap_mb", DEFAULT_BUCKET_CAP_MB)) * 1024 * 1024)
+            if cap_bytes <= 0:
+                cap_bytes = int(DEFAULT_BUCKET_CAP_MB * 1024 * 1024)
+            by_key: Dict[Tuple[Any, Any], List[Tuple[int, Any]]] = {}
+            for idx, p in enumerate(group["params"]):
+                if not isinstance(p, torch.Tensor) or not p.requires_grad:
+                    continue
+                validate_supported_dtype(p, "param")
+                if p.numel() == 0:
+                    continue
+                ident = (p.device, p.data_ptr(), int(p.numel()))
+                if id(p) in seen or ident in seen:
+                    continue  # tied weights: the first occurrence owns the slice
+                seen.add(id(p))
+                seen.add(ident)
+                by_key.setdefault((p.device, p.dtype), []).append((idx, p))
+
+            for (dev, dt), indexed in by_key.items():
+                for chunk in self._partition_into_bounded_chunks(indexed, cap_bytes):
+                    total = sum(int(p.numel()) for _, p in chunk)
+                    if total == 0:
+                        continue
+                    sdt = self._state_dtype(dt, master_mode, precision)
+                    has_master = master_mode > 0 and dt in (torch.float16, torch.bfloat16)
+                    flat_p = torch.empty(total, dtype=dt, device=dev)
+                    flat_g = torch.zeros(total, dtype=dt, device=dev)
+                    flat_m = torch.zeros(total, dtype=sdt, device=dev)
+                    flat_v = torch.zeros(total, dtype=sdt, device=dev) if buf_count in (2, "T2") else None
+                    flat_mp = torch.empty(total, dtype=torch.float32, device=dev) if has_master else None
+                    scratch = _new_scratch(dev)
+                    off = 0
+                    slices = []
+                    bucket_step = 0
+                    for idx, p in chunk:
+                        n = int(p.numel())
+                        p_sl = flat_p[off:off + n].view(p.shape)
+                        g_sl = flat_g[off:off + n].view(p.shape)
+                        m_sl = flat_m[off:off + n].view(p.shape)
+                        v_sl = flat_v[off:off + n].view(p.shape) if flat_v is not None else None
+                        mp_sl = flat_mp[off:off + n].view(p.shape) if flat_mp is not None else None
+                        p_sl.copy_(p.detach())
+                        p.data = p_sl
+                        if p.grad is not None:
+                            g_sl.copy_(p.grad.detach())
+                        p.grad = g_sl
+                        if mp_sl is not None:
+                            mp_sl.copy_(p_sl.float())
+                        st = self.state[p]
+                        if isinstance(st.get("exp_avg"), torch.Tensor) and st["exp_avg"].numel() == n:
+                            m_sl.copy_(_convert_state_buffer(st["exp_avg"], dev, sdt).view(p.shape))
+                        if v_sl is not None and isinstance(st.get("exp_avg_sq"), torch.Tensor) and st["exp_avg_sq"].numel() == n:
+                            v_sl.copy_(_convert_state_buffer(st["exp_avg_sq"], dev, sdt).view(p.shape))
+                        if mp_sl is not None and isinstance(st.get("master_param"), torch.Tensor) and st["master_param"].numel() == n:
+                            mp_sl.copy_(st["master_param"].to(device=dev, dtype=torch.float32).view(p.shape))
+                        if "step" in st:
+                            s_raw = st["step"]
+                            bucket_step = max(bucket_step, int(s_raw.item() if hasattr(s_raw, "item") else s_raw))
+                        if isinstance(st.get("scratch"), torch.Tensor) and st["scratch"].numel() >= 6:
+                            scratch.copy_(st["scratch"].to(device=dev, dtype=torch.float32)[:6])
+                        st["step"] = bucket_step
+                        st["scratch"] = scratch
+                        st["exp_avg"] = m_sl
+                        if v_sl is not None:
+                            st["exp_avg_sq"] = v_sl
+                        else:
+                            st.pop("exp_avg_sq", None)
+                        if mp_sl is not None:
+                            st["master_param"] = mp_sl
+                        else:
+                            st.pop("master_param", None)
+                        st["buf_count"] = buf_count
+                        slices.append((p, p_sl, g_sl, p_sl.data_ptr(), g_sl.data_ptr(), st, idx))
+                        off += n
+                    self._fused_buckets.append({
+                        "group": group, "device": dev, "dtype": dt, "state_dtype": sdt, "buf_count": buf_count,
+                        "master_mode": master_mode, "bucket_cap_mb": cap_bytes / (1024 * 1024),
+                        "flat_p": flat_p, "flat_g": flat_g, "flat_m": flat_m, "flat_v": flat_v, "flat_mp": flat_mp,
+                        "scratch": scratch, "slices": slices, "step": bucket_step,
+                    })
+
+    def _sync_or_rebuild_fused_buckets(self) -> None:
+        """Re-binds params/grads/state to existing buckets, or rebuilds them when the group
+        topology changed (reference luminav.py:1293-1374)."""
+        need_rebuild = False
+        bucket_groups = {id(b["group"]) for b in self._fused_buckets}
+        for group in self.param_groups:
+            if group.get("fuse_tensors", False) and not group.get("fsdp_sync", False) and id(group) not in bucket_groups:
+                need_rebuild = True
+        for b in self._fused_buckets:
+            grp = b["group"]
+            if (not grp.get("fuse_tensors", False) or grp.get("fsdp_sync", False)
+                    or grp.get("buffer", 2) != b["buf_count"] or int(grp.get("master_weights", 0)) != int(b["master_mode"])
+                    or float(grp.get("bucket_cap_mb", DEFAULT_BUCKET_CAP_MB)) != float(b["bucket_cap_mb"])):
+                need_rebuild = True
+        if need_rebuild:
+            self._build_contiguous_buckets(force_rebuild=True)
+            return
+        for b in self._fused_buckets:
+            flat_m, flat_v, flat_mp, scratch = b["flat_m"], b["flat_v"], b["flat_mp"], b["scratch"]
+            bucket_step = int(b.get("step", 0))
+            new_slices = []
+            off = 0
+            for p, p_sl, g_sl, p_ptr, g_ptr, _, idx in b["slices"]:
+                n = int(p.numel())
+                if p.data_ptr() != p_ptr:
+                    p_sl.copy_(p.detach())
+                    p.data = p_sl
+                if p.grad is not None and p.grad.data_ptr() != g_ptr:
+                    g_sl.copy_(p.grad.detach())
+                p.grad = g_sl
+                st = self.state[p]
+                if isinstance(st.get("exp_avg"), torch.Tensor):
+                    tgt = flat_m[off:off + n].view(p.shape)
+                    if st["exp_avg"].data_ptr() != tgt.data_ptr():
+                        tgt.copy_(st["exp_avg"].detach())
+                    st["exp_avg"] = tgt
+                if flat_v is not None and isinstance(st.get("exp_avg_sq"), torch.Tensor):
+                    tgt = flat_v[off:off + n].view(p.shape)
+                    if st["exp_avg_sq"].data_ptr() != tgt.data_ptr():
+                        tgt.copy_(st["exp_avg_sq"].detach())
+                    st["exp_avg_sq"] = tgt
+                if flat_mp is not None and isinstance(st.get("master_param"), torch.Tensor):
+                    tgt = flat_mp[off:off + n].view(p.shape)
+                    if st["master_param"].data_ptr() != tgt.data_ptr():
+                        tgt.copy_(st["master_param"].detach())
+                    st["master_param"] = tgt
+                if "step" in st:
+                    s_raw = st["step"]
+                    bucket_step = int(s_raw.item() if hasattr(s_raw, "item") else s_raw)
+                    st["step"] = bucket_step
+                if isinstance(st.get("scratch"), torch.Tensor) and st["scratch"].numel() >= 6:
+                    if st["scratch"].data_ptr() != scratch.data_ptr():
+                        scratch.copy_(st["scratch"][:6])
+                    st["scratch"] = scratch
+                new_slices.append((p, p_sl, g_sl, p_ptr, g_ptr, st, idx))
+                off += n
+            b["slices"] = new_slices
+            b["step"] = bucket_step
+
+    def add_param_group(self, param_group: Dict[str, Any]) -> None:
+        for name, default in self.defaults.items():
+            param_group.setdefault(name, default)
+        self._validate_and_normalize_group(param_group)
+        super().add_param_group(param_group)
+        if hasattr(self, "_stepper") and param_group.get("fuse_tensors", False):
+            self.fuse_tensors = True
+            self._build_contiguous_buckets()
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        """Fused params keep their grad views into the bucket (reference luminav.py:973-1013)."""
+        if self.fuse_tensors and self._fused_buckets:
+            with torch.no_grad():
+                fused_ids = set()
+                for b in self._fused_buckets:
+                    b["flat_g"].zero_()
+                    for p, _, g_sl, _, g_ptr, _, _ in b["slices"]:
+                        fused_ids.add(id(p))
+                        if p.grad is not g_sl and (p.grad is None or p.grad.data_ptr() != g_ptr):
+                            p.grad = g_sl
+                for group in self.param_groups:
+                    for p in group["params"]:
+                        if id(p) in fused_ids or p.grad is None:
+                            continue
+                        if set_to_none:
+                            p.grad = None
+                        else:
+                            if p.grad.grad_fn is not None:
+                                p.grad.detach_()
+                            else:
+                                p.grad.requires_grad_(False)
+                            p.grad.zero_()
+            return
+        super().zero_grad(set_to_none=set_to_none)
+
+    @staticmethod
+    def detect_hardware() -> Dict[str, Any]:
+        info = {
+            "simd_backend": None,
+            "triton_aot_available": False,
+            "triton_arch": None,
+            "vulkan_available": False,
+            "wave32_supported": False,
+            "gpu_dispatch_threshold": DEFAULT_GPU_DISPATCH_THRESHOLD,
+            "backend": "hip",
+        }
+        info.update(hip_backend.device_info())
+        return info
+
+    # ------------------------------------------------------------------ checkpoints
+
+    def state_dict(self) -> Dict[str, Any]:
+        """Torch state_dict minus transient keys; scratch accumulators zeroed; fp16 state
+        containers tagged as bf16 bits (reference luminav.py:1030-1115)."""
+        raw = super().state_dict()
+        param_ids = {id(p) for g in self.param_groups for p in g["params"]}
+        clean: Dict[Any, Any] = {}
+        for k, st in raw.get("state", {}).items():
+            if not isinstance(st, dict):
+                clean[k] = st
+                continue
+            entry: Dict[str, Any] = {}
+            has_fp16 = False
+            for sk, sv in st.items():
+                if sk in TEMP_STATE_DICT_KEYS or (sk == "master_param" and id(sv) in param_ids):
+                    continue
+                if sk == "scratch" and isinstance(sv, torch.Tensor) and sv.numel() >= 6:
+                    c = sv.detach().clone()
+                    c[:3].zero_()
+                    c[5].zero_()
+                    entry[sk] = c
+                elif isinstance(sv, torch.Tensor):
+                    if sk in ("exp_avg", "exp_avg_sq") and sv.dtype == torch.float16:
+                        has_fp16 = True
+                    entry[sk] = sv.detach().clone()
+                else:
+                    entry[sk] = sv
+            if has_fp16:
+                entry["_fp16_state_format"] = "bf16_bits"
+            clean[k] = entry
+        groups = [{gk: gv for gk, gv in g.items() if gk != "_validated_sig"} for g in raw.get("param_groups", [])]
+        return {"state": clean, "param_groups": groups}
+
+    def load_state_dict(self, state_dict: Dict[str, Any]) -> None:
+        """Loads state and re-normalises dtypes, scratch layout and buckets (reference luminav.py:1117-1292)."""
+        raw_state = state_dict.get("state", {})
+        saved_groups = state_dict.get("param_groups", [])
+        raw_param_state: Dict[Any, Dict[str, Any]] = {}
+        if len(self.param_groups) == len(saved_groups):
+            for group, sg in zip(self.param_groups, saved_groups):
+                for p, pid in zip(group["params"], sg.get("params", [])):
+                    st = raw_state.get(pid)
+                    if isinstance(st, dict):
+                        raw_param_state[p] = {k: (v.detach().clone() if isinstance(v, torch.Tensor) else v) for k, v in st.items()}
+        super().load_state_dict(state_dict)
+        for group in self.param_groups:
+            for k, v in self.defaults.items():
+                group.setdefault(k, v)
+            self._validate_and_normalize_group(group)
+            master_mode = int(group["master_weights"])
+            buf_count = group["buffer"]
+            precision = group.get("state_precision", DEFAULT_STATE_PRECISION)
+            radial = self._radial_active(group)
+            for p in group["params"]:
+                if p not in self.state:
+                    continue
+                st = self.state[p]
+                raw_st = raw_param_state.get(p, {})
+                for tk in TEMP_STATE_DICT_KEYS:
+                    st.pop(tk, None)
+                if isinstance(st.get("step"), torch.Tensor):
+                    st["step"] = int(st["step"].item())
+                src_sc = raw_st.get("scratch") if isinstance(raw_st.get("scratch"), torch.Tensor) else st.get("scratch")
+                sc = _new_scratch(p.device)
+                if isinstance(src_sc, torch.Tensor):
+                    old = src_sc.to(device=p.device, dtype=torch.float32).reshape(-1)[:6]
+                    sc[: old.numel()].copy_(old)
+                sc[:3].zero_()
+                sc[5].zero_()
+                if not group["cautious"]:
+                    sc[3] = 1.0
+                if not radial:
+                    sc[4] = 1.0
+                st["scratch"] = sc
+                if master_mode == 0 or p.dtype == torch.float32:
+                    st.pop("master_param", None)
+                else:
+                    src_mp = raw_st.get("master_param") if isinstance(raw_st.get("master_param"), torch.Tensor) else st.get("master_param")
+                    if isinstance(src_mp, torch.Tensor):
+                        st["master_param"] = src_mp.to(device=p.device, dtype=torch.float32).contiguous()
+                    else:
+                        st["master_param"] = p.detach().clone().float().contiguous()
+                target = self._state_dtype(p.dtype, master_mode, precision)
+                fp16_bits = (raw_st.get("_fp16_state_format") == "bf16_bits" or st.get("_fp16_state_format") == "bf16_bits"
+                             or "scratch" in raw_st or "buf_count" in raw_st)
+                st.pop("_fp16_state_format", None)
+                for key in ("exp_avg", "exp_avg_sq"):
+                    src = raw_st.get(key) if isinstance(raw_st.get(key), torch.Tensor) else st.get(key)
+                    if isinstance(src, torch.Tensor):
+                        st[key] = _convert_state_buffer(src, p.device, target, fp16_is_bf16_bits=fp16_bits)
+                if not isinstance(st.get("exp_avg"), torch.Tensor):
+                    st["exp_avg"] = torch.zeros_like(p, dtype=target, memory_format=torch.contiguous_format)
+                if buf_count in (1, "T1"):
+                    st.pop("exp_avg_sq", None)
+                elif not isinstance(st.get("exp_avg_sq"), torch.Tensor):
+                    st["exp_avg_sq"] = torch.zeros_like(p, dtype=target, memory_format=torch.contiguous_format)
+                st["buf_count"] = buf_count
+        self.fuse_tensors = any(bool(g.get("fuse_tensors", False)) for g in self.param_groups)
+        if self.fuse_tensors:
+            self._sync_or_rebuild_fused_buckets()
+        else:
+            self._fused_buckets.clear()
+
+    # ------------------------------------------------------------------ step
+
+    def _init_or_refresh_state(self, p: torch.Tensor, group: Dict[str, Any]) -> Dict[str, Any]:
+        """Lazy state allocation and re-normalisation (reference luminav.py:1665-1790)."""
+        buf_count = group["buffer"]
+        master_mode = int(group["master_weights"])
+        sdt = self._state_dtype(p.dtype, master_mode, group.get("state_precision", DEFAULT_STATE_PRECISION))
+        state = self.state[p]
+        if len(state) == 0:
+            state["step"] = 0
+            state["scratch"] = _new_scratch(p.device)
+            state["exp_avg"] = torch.zeros_like(p, dtype=sdt, memory_format=torch.contiguous_format)
+            if buf_count in (2, "T2"):
+                state["exp_avg_sq"] = torch.zeros_like(p, dtype=sdt, memory_format=torch.contiguous_format)
+            if master_mode > 0 and p.dtype in (torch.float16, torch.bfloat16):
+                state["master_param"] = p.detach().clone().float().contiguous()
+            state["buf_count"] = buf_count
+            return state
+        if master_mode > 0:
+            if p.dtype == torch.float32:
+                state.pop("master_param", None)
+            elif state.get("master_param") is None:
+                state["master_param"] = p.detach().clone().float().contiguous()
+            elif state["master_param"].device != p.device or state["master_param"].dtype != torch.float32:
+                state["master_param"] = state["master_param"].to(device=p.device, dtype=torch.float32)
+        else:
+            state.pop("master_param", None)
+        sc = state.get("scratch")
+        if not isinstance(sc, torch.Tensor) or sc.numel() < 6:
+            new = _new_scratch(p.device)
+            if isinstance(sc, torch.Tensor):
+                new[: sc.numel()].copy_(sc.to(device=p.device, dtype=torch.float32))
+            state["scratch"] = new
+            state["buf_count"] = buf_count
+        elif sc.device != p.device or sc.dtype != torch.float32:
+            state["scratch"] = sc.to(device=p.device, dtype=torch.float32)
+            state["buf_count"] = buf_count
+        elif state.get("buf_count", buf_count) != buf_count:
+            state["scratch"].copy_(torch.tensor(_SCRATCH_INIT, dtype=torch.float32))  # ParamState::ensure_buffer_mode
+            state["buf_count"] = buf_count
+        if "exp_avg" not in state:
+            state["exp_avg"] = torch.zeros_like(p, dtype=sdt, memory_format=torch.contiguous_format)
+        elif state["exp_avg"].device != p.device or state["exp_avg"].dtype != sdt:
+            state["exp_avg"] = _convert_state_buffer(state["exp_avg"], p.device, sdt)
+        if buf_count in (2, "T2"):
+            if "exp_avg_sq" not in state:
+                state["exp_avg_sq"] = torch.zeros_like(p, dtype=sdt, memory_format=torch.contiguous_format)
+            elif state["exp_avg_sq"].device != p.device or state["exp_avg_sq"].dtype != sdt:
+                state["exp_avg_sq"] = _convert_state_buffer(state["exp_avg_sq"], p.device, sdt)
+        else:
+            state.pop("exp_avg_sq", None)
+        return state
+
+    @torch.no_grad()
+    def step(self, closure: Optional[Callable[[], float]] = None, grads: Optional[Any] = None) -> Optional[float]:
+        """One optimizer step over every param group (reference luminav.py:1376-1966)."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group in self.param_groups:
+            if group.get("_validated_sig") != self._compute_group_sig(group):
+                self._validate_and_normalize_group(group)
+            if group.get("fsdp_sync", False):
+                raise NotImplementedError(
+                    "LuminaV (MI355X build): fsdp_sync=True (sharded scratch all-reduce) is not available in this "
+                    "single-GPU build."
+                )
+            if group.get("fuse_tensors", False):
+                buckets = [b for b in self._fused_buckets if b["group"] is group]
+                if not buckets or any(b["buf_count"] != group["buffer"] or int(b["master_mode"]) != int(group["master_weights"])
+                                      for b in buckets):
+                    self._sync_or_rebuild_fused_buckets()
+                    buckets = [b for b in self._fused_buckets if b["group"] is group]
+                if buckets:
+                    for b in buckets:
+                        self._step_bucket(group, b, grads)
+                    continue
+            self._step_unfused(group, grads)
+        return loss
+
+    def _step_bucket(self, group: Dict[str, Any], b: Dict[str, Any], grads: Optional[Any]) -> None:
+        """One bucket = one tensor with param_index 0 and bucket-global offsets; slices without a
+        grad are stepped with g=0 and restored afterwards (reference luminav.py:1426-1603)."""
+        flat_m, flat_v, flat_mp = b["flat_m"], b["flat_v"], b["flat_mp"]
+        b["step"] = int(b["step"]) + 1
+        step_t = b["step"]
+        any_grad = False
+        backups = []
+        off = 0
+        for p, p_sl, g_sl, p_ptr, g_ptr, st, idx in b["slices"]:
+            n = int(p.numel())
+            m_sl = flat_m[off:off + n].view(p.shape)
+            v_sl = flat_v[off:off + n].view(p.shape) if flat_v is not None else None
+            mp_sl = flat_mp[off:off + n].view(p.shape) if flat_mp is not None else None
+            off += n
+            if p.data_ptr() != p_ptr:
+                p_sl.copy_(p.detach())
+                p.data = p_sl
+            if grads is None:
+                g = p.grad
+            elif isinstance(grads, (list, tuple)):
+                g = grads[idx] if idx < len(grads) else None
+            elif isinstance(grads, dict):
+                g = grads.get(p)
+            else:
+                g = None
+            if g is None:
+                g_sl.zero_()
+                backups.append((p_sl, p_sl.detach().clone(), m_sl, m_sl.detach().clone(), v_sl,
+                                None if v_sl is None else v_sl.detach().clone(), mp_sl,
+                                None if mp_sl is None else mp_sl.detach().clone(), st, int(st.get("step", step_t - 1))))
+                continue
+            any_grad = True
+            if getattr(g, "is_sparse", False):
+                b["step"] = step_t - 1
+                raise RuntimeError("LuminaV does not support sparse gradients.")
+            if g is not g_sl:
+                validate_supported_dtype(g, "grad")
+                if g.data_ptr() != g_ptr:
+                    g_sl.copy_(g.detach())
+                    if grads is None:
+                        p.grad = g_sl
+            st["step"] = step_t
+        if not any_grad:
+            b["step"] = step_t - 1
+            for *_, st, _ in b["slices"]:
+                st["step"] = int(st.get("step", step_t - 1))
+            return
+        self._stepper.step(group, [b["flat_p"]], [b["flat_g"]], [flat_m], [flat_v], [flat_mp], [b["scratch"]],
+                           [step_t], [0])
+        for p_sl, p_bak, m_sl, m_bak, v_sl, v_bak, mp_sl, mp_bak, st, prev in backups:
+            p_sl.copy_(p_bak)
+            m_sl.copy_(m_bak)
+            if v_sl is not None:
+                v_sl.copy_(v_bak)
+            if mp_sl is not None:
+                mp_sl.copy_(mp_bak)
+            st["step"] = prev
+
+    def _step_unfused(self, group: Dict[str, Any], grads: Optional[Any]) -> None:
+        buf_count = group["buffer"]
+        per_device: Dict[torch.device, List[Tuple[Any, ...]]] = {}
+        for idx, p in enumerate(group["params"]):
+            g = None
+            if grads is not None:
+                if isinstance(grads, (list, tuple)) and idx < len(grads):
+                    g = grads[idx]
+                elif isinstance(grads, dict) and p in grads:
+                    g = grads[p]
+            if g is None:
+                g = p.grad
+            if g is None:
+                continue
+            if getattr(g, "is_sparse", False):
+                raise RuntimeError("LuminaV does not support sparse gradients.")
+            validate_supported_dtype(p, "param")
+            validate_supported_dtype(g, "grad")
+            if p.numel() == 0:
+                continue
+            if not g.is_contiguous():
+                g = g.contiguous()
+            if p.device.type == "cpu" and not p.is_contiguous():
+                raise ValueError(
+                    f"LuminaV requires parameters to be contiguous in memory for native zero-copy execution. Call .contiguous() on parameter {idx} before passing to optimizer."
+                )
+            p_step = p if p.is_contiguous() else p.contiguous()
+            if g.device != p.device:
+                g = g.to(p.device)
+            state = self._init_or_refresh_state(p, group)
+            state["step"] = int(state["step"]) + 1
+            per_device.setdefault(p.device, []).append((
+                p, p_step, g, state["exp_avg"], state.get("exp_avg_sq") if buf_count in (2, "T2") else None,
+                state.get("master_param"), state["scratch"], state["step"], idx,
+            ))
+        for dev, rows in per_device.items():
+            self._stepper.step(group, [r[1] for r in rows], [r[2] for r in rows], [r[3] for r in rows],
+                               [r[4] for r in rows], [r[5] for r in rows], [r[6] for r in rows],
+                               [r[7] for r in rows], [r[8] for r in rows])
+            for r in rows:
+                if r[0] is not r[1]:
+                    r[0].copy_(r[1])
