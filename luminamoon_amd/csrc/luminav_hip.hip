@@ -38,6 +38,7 @@ constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argum
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
 enum Flags : uint32_t {
+    kFDynamic = 1u << 31,  // template flag set: read the flags from the launch arguments
     kFCautious = 1u << 0,
     kFSR = 1u << 1,
     kFMaster = 1u << 2,
@@ -96,25 +97,28 @@ __device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
     return z ^ (z >> 16);
 }
 
-// prng.rs:137-160 (value form: f32 carrying the bf16 bits)
+// prng.rs:137-160 (value form: f32 carrying the bf16 bits). Branch-free: both the finite and
+// the NaN result are formed and one is selected, so a wave never splits on NaN lanes.
 __device__ __forceinline__ float sr_bf16(float v, int32_t seed, int32_t off) {
-    int32_t p = (int32_t)f_bits(v);
-    int32_t a = p & 0x7FFFFFFF;
-    if (a > 0x7F800000) return bits_f(((uint32_t)p | 0x00400000u) & 0xFFFF0000u);
-    int32_t noise = prng(seed, off) & 0xFFFF;
-    int32_t added = (int32_t)(((uint32_t)a + (uint32_t)noise) & 0xFFFF0000u);
-    int32_t r = (added > 0x7F7F0000 || added < 0) ? 0x7F7F0000 : added;
-    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
+    uint32_t p = f_bits(v);
+    uint32_t a = p & 0x7FFFFFFFu;
+    uint32_t noise = (uint32_t)prng(seed, off) & 0xFFFFu;
+    uint32_t added = (a + noise) & 0xFFFF0000u;  // a <= 0x7F800000 when used: no wrap, never "negative"
+    uint32_t r = added > 0x7F7F0000u ? 0x7F7F0000u : added;
+    uint32_t fin = (p & 0x80000000u) | r;
+    uint32_t nan = (p | 0x00400000u) & 0xFFFF0000u;
+    return bits_f(a > 0x7F800000u ? nan : fin);
 }
 
 // prng.rs:162-178
 __device__ __forceinline__ float rne_bf16(float v) {
     uint32_t b = f_bits(v);
     uint32_t a = b & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return bits_f((b | 0x00400000u) & 0xFFFF0000u);
     uint32_t r = (a + 0x7FFFu + ((a >> 16) & 1u)) & 0xFFFF0000u;
     r = r > 0x7F7F0000u ? 0x7F7F0000u : r;
-    return bits_f((b & 0x80000000u) | r);
+    uint32_t fin = (b & 0x80000000u) | r;
+    uint32_t nan = (b | 0x00400000u) & 0xFFFF0000u;
+    return bits_f(a > 0x7F800000u ? nan : fin);
 }
 
 // prng.rs:29-67
@@ -185,9 +189,15 @@ __device__ __forceinline__ float quantize(float v, int32_t seed, int32_t off, bo
     }
 }
 
-// math.rs:4-11
+// math.rs:4-11. |g| < 1e38 is false for NaN and +-inf, so one compare also covers is_finite;
+// on that path g is not NaN and med3 is exactly the clamp.
 __device__ __forceinline__ float sanitize(float g) {
-    return (__builtin_isfinite(g) && fabsf(g) < 1.0e38f) ? rclamp(g, -1.0e18f, 1.0e18f) : 0.0f;
+    return fabsf(g) < 1.0e38f ? __builtin_amdgcn_fmed3f(g, -1.0e18f, 1.0e18f) : 0.0f;
+}
+
+// math.rs:13-16 (clamp_defect): NaN passes through like Rust's f32::clamp.
+__device__ __forceinline__ float clamp_defect(float d) {
+    return __builtin_isnan(d) ? d : __builtin_amdgcn_fmed3f(d, -1.0e18f, 1.0e18f);
 }
 
 // math.rs:83-118 -- [13/6] Pade tanh, Horner with fma.
@@ -257,14 +267,14 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
     m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
     if constexpr (MODE == LV_BUFFER_DUAL) {
         float clm = __builtin_fmaf(a.b1, m_new, a.omb1 * g);
-        float diff = rclamp(g - m_new, -1.0e18f, 1.0e18f);
+        float diff = clamp_defect(g - m_new);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
         float sigma = __builtin_fmaf(__builtin_sqrtf(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
         return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
     } else if constexpr (MODE == LV_BUFFER_T2) {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
-        float diff = rclamp(g - m, -1.0e18f, 1.0e18f);
+        float diff = clamp_defect(g - m);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
         float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
@@ -274,7 +284,7 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
         return clm / env;
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
-        float diff = rclamp(g - m, -1.0e18f, 1.0e18f);
+        float diff = clamp_defect(g - m);
         float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
@@ -284,53 +294,6 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
 }
 
 // ------------------------------------------------------------------ loads / stores
-
-template <int DT>
-__device__ __forceinline__ void load8(const void *base, uint64_t i, float out[8]) {
-    if constexpr (DT == LV_DTYPE_F32) {
-        const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + i);
-        float4 x = q[0], y = q[1];
-        out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
-        out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
-    } else {
-        uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + i);
-        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if constexpr (DT == LV_DTYPE_BF16) {
-                out[2 * k] = bits_f(ws[k] << 16);
-                out[2 * k + 1] = bits_f(ws[k] & 0xFFFF0000u);
-            } else {
-                out[2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
-                out[2 * k + 1] = f16_to_f32(ws[k] >> 16);
-            }
-        }
-    }
-}
-
-template <int DT>
-__device__ __forceinline__ void store8(void *base, uint64_t i, const float in[8]) {
-    if constexpr (DT == LV_DTYPE_F32) {
-        float4 *q = reinterpret_cast<float4 *>(static_cast<float *>(base) + i);
-        q[0] = make_float4(in[0], in[1], in[2], in[3]);
-        q[1] = make_float4(in[4], in[5], in[6], in[7]);
-    } else {
-        uint32_t ws[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t lo, hi;
-            if constexpr (DT == LV_DTYPE_BF16) {
-                lo = f_bits(in[2 * k]) >> 16;  // values are already bf16-exact (worker.rs:55-63)
-                hi = f_bits(in[2 * k + 1]) & 0xFFFF0000u;
-            } else {
-                lo = f32_to_f16_rne(in[2 * k]);
-                hi = f32_to_f16_rne(in[2 * k + 1]) << 16;
-            }
-            ws[k] = lo | hi;
-        }
-        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(base) + i) = make_uint4(ws[0], ws[1], ws[2], ws[3]);
-    }
-}
 
 template <int DT>
 __device__ __forceinline__ float load1(const void *base, uint64_t i) {
@@ -354,17 +317,110 @@ __device__ __forceinline__ void store1(void *base, uint64_t i, float x) {
     }
 }
 
-__device__ __forceinline__ void load8_dyn(int dt, const void *base, uint64_t i, float out[8]) {
-    if (dt == LV_DTYPE_BF16) load8<LV_DTYPE_BF16>(base, i, out);
-    else if (dt == LV_DTYPE_F32) load8<LV_DTYPE_F32>(base, i, out);
-    else load8<LV_DTYPE_F16>(base, i, out);
-}
-
 __device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i) {
     if (dt == LV_DTYPE_BF16) return load1<LV_DTYPE_BF16>(base, i);
     if (dt == LV_DTYPE_F32) return load1<LV_DTYPE_F32>(base, i);
     return load1<LV_DTYPE_F16>(base, i);
 }
+
+// One thread's 8 elements as raw vectors, kept undecoded while the loads are in flight.
+// Vector-path loads and stores are non-temporal: the step streams every byte exactly once, so
+// nothing is worth keeping in L2 or the MALL, and streaming hints measurably raise HBM
+// throughput for this 4-read/3-write pattern.
+// Layout of a 2048-element work unit: thread t owns elements [4t, 4t+4) of each 1024-element
+// half, so every wave-wide load or store instruction covers one contiguous span (1 KiB for
+// f32, 512 B for 16-bit types). 32-bit types use `a` (first half) and `b` (second half);
+// 16-bit types pack both halves into `a` (.xy first half, .zw second half).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Raw8 {
+    u32x4 a, b;
+};
+
+constexpr uint32_t kHalf = kUnit / 2;
+
+template <int DT>
+__device__ __forceinline__ Raw8 load_raw(const void *base, uint64_t h0) {
+    Raw8 r;
+    if constexpr (DT == LV_DTYPE_F32) {
+        const float *f = static_cast<const float *>(base);
+        r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0));
+        r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + kHalf));
+    } else {
+        const uint16_t *h = static_cast<const uint16_t *>(base);
+        u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
+        u32x2 y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + kHalf));
+        r.a = u32x4{x.x, x.y, y.x, y.y};
+        r.b = u32x4{0, 0, 0, 0};
+    }
+    return r;
+}
+
+__device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t h0) {
+    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32>(base, h0);
+    return load_raw<LV_DTYPE_BF16>(base, h0);  // 16-bit types share the raw layout
+}
+
+// Stores 8 values in the same two-half layout; 16-bit values are already exact in the target
+// type (quantised), so bf16 is a truncation (worker.rs:55-63) and f16 an exact RNE encode.
+template <int DT>
+__device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        float *f = static_cast<float *>(base);
+        __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4 *>(f + h0));
+        __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + kHalf));
+    } else {
+        uint32_t ws[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t lo, hi;
+            if constexpr (DT == LV_DTYPE_BF16) {
+                lo = f_bits(in[2 * k]) >> 16;
+                hi = f_bits(in[2 * k + 1]) & 0xFFFF0000u;
+            } else {
+                lo = f32_to_f16_rne(in[2 * k]);
+                hi = f32_to_f16_rne(in[2 * k + 1]) << 16;
+            }
+            ws[k] = lo | hi;
+        }
+        uint16_t *h = static_cast<uint16_t *>(base);
+        __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
+        __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + kHalf));
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void decode_raw(const Raw8 &r, float out[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        out[0] = bits_f(r.a.x); out[1] = bits_f(r.a.y); out[2] = bits_f(r.a.z); out[3] = bits_f(r.a.w);
+        out[4] = bits_f(r.b.x); out[5] = bits_f(r.b.y); out[6] = bits_f(r.b.z); out[7] = bits_f(r.b.w);
+    } else {
+        uint32_t ws[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (DT == LV_DTYPE_BF16) {
+                out[2 * k] = bits_f(ws[k] << 16);
+                out[2 * k + 1] = bits_f(ws[k] & 0xFFFF0000u);
+            } else {
+                out[2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                out[2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void decode_raw_dyn(int dt, const Raw8 &r, float out[8]) {
+    if (dt == LV_DTYPE_BF16) decode_raw<LV_DTYPE_BF16>(r, out);
+    else if (dt == LV_DTYPE_F32) decode_raw<LV_DTYPE_F32>(r, out);
+    else decode_raw<LV_DTYPE_F16>(r, out);
+}
+
+// The loads of one work unit that are in flight while the previous unit computes.
+struct Inflight {
+    Raw8 p, g, m, v, mp;
+};
 
 // ------------------------------------------------------------------ element update
 
@@ -466,13 +522,16 @@ __device__ void flush_tensor(const Args &a, int t, uint32_t n_units, uint32_t cn
 
 // ------------------------------------------------------------------ the kernel
 
-template <int MODE, int PT, int ST, int PASS>
+// FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
+// which case every option test below folds at compile time and the per-element code is
+// straight-line.
+template <int MODE, int PT, int ST, int PASS, uint32_t FL>
 __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
     __shared__ uint32_t red[kThreads / 64];
 
-    const uint32_t flags = a.flags;
+    const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
     const int gdt = (int)((flags >> 8) & 3u);
     const bool master = flags & kFMaster;
     const uint32_t total_units = a.total_units;
@@ -485,73 +544,116 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
     Seeds sd{0, 0, 0};
     uint32_t cnt = 0, units_here = 0;
 
-    for (uint32_t unit = blockIdx.x; unit < total_units; unit += gridDim.x) {
-        if (unit >= t_end) {
-            if constexpr (kCounting) {
-                if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
-            }
-            int lo = t + 1, hi = a.ndesc - 1;  // units only grow, so search right of t
-            while (lo < hi) {
-                int mid = (lo + hi + 1) >> 1;
-                if (a.d[mid].unit_begin <= unit) lo = mid;
-                else hi = mid - 1;
-            }
-            t = lo;
-            const Desc &D = a.d[t];
-            t_begin = D.unit_begin;
-            t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : total_units;
-            n = D.n;
-            uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
-            if (kDual) al |= (uintptr_t)D.v;
-            if (master) al |= (uintptr_t)D.mp;
-            vec_ok = (al & 15u) == 0;
-            uint32_t raw = a.seed_base + D.pidx * 10007u;
-            sd.m = (int32_t)(raw & 0x7FFFFFFFu);
-            sd.p = (int32_t)(((uint32_t)sd.m + 0x55555555u) & 0x7FFFFFFFu);
-            sd.v = (int32_t)(((uint32_t)sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
-            if constexpr (PASS == kFused || PASS == kApply) {
-                cs = D.scratch[3];
-                bs = D.scratch[4];
-            }
-            if constexpr (PASS == kSingle) {
-                // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
-                // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
-                if (unit == t_begin && threadIdx.x == 0) {
-                    float *s = D.scratch;
-                    s[0] = 0.0f; s[1] = 0.0f; s[2] = 0.0f; s[3] = 1.0f; s[4] = 1.0f; s[5] = 0.0f;
-                }
-            }
-            cnt = 0;
-            units_here = 0;
+    const uint32_t stride = gridDim.x;
+    uint32_t unit = blockIdx.x;
+    while (unit < total_units) {
+        // ---- switch to the tensor that owns `unit` (units of one tensor are contiguous)
+        if constexpr (kCounting) {
+            if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
         }
+        int lo = t + 1, hi = a.ndesc - 1;  // units only grow, so search right of t
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (a.d[mid].unit_begin <= unit) lo = mid;
+            else hi = mid - 1;
+        }
+        t = lo;
         const Desc &D = a.d[t];
-        const uint64_t e0 = (uint64_t)(unit - t_begin) * kUnit + (uint64_t)threadIdx.x * kVec;
-        if (vec_ok && e0 + kVec <= n) {
-            float g[8], m[8], v[8], pin[8];
-            load8_dyn(gdt, D.g, e0, g);
-            load8<ST>(D.m, e0, m);
-            if constexpr (kDual) load8<ST>(D.v, e0, v);
-            if constexpr (PASS == kCount) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f);
-            } else {
-                if (master) load8<LV_DTYPE_F32>(D.mp, e0, pin);
-                else load8<PT>(D.p, e0, pin);
-                float pout[8], mpout[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    float vj = kDual ? v[j] : 0.0f;
-                    uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)(e0 + j), cs, bs, pin[j],
-                                                            g[j], m[j], vj, pout[j], mpout[j]);
-                    if constexpr (kDual) v[j] = vj;
-                    if constexpr (kCounting) cnt += act;
-                }
-                store8<PT>(D.p, e0, pout);
-                if (master) store8<LV_DTYPE_F32>(D.mp, e0, mpout);
-                store8<ST>(D.m, e0, m);
-                if constexpr (kDual) store8<ST>(D.v, e0, v);
+        t_begin = D.unit_begin;
+        t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : total_units;
+        n = D.n;
+        uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
+        if (kDual) al |= (uintptr_t)D.v;
+        if (master) al |= (uintptr_t)D.mp;
+        vec_ok = (al & 15u) == 0;
+        uint32_t raw = a.seed_base + D.pidx * 10007u;
+        sd.m = (int32_t)(raw & 0x7FFFFFFFu);
+        sd.p = (int32_t)(((uint32_t)sd.m + 0x55555555u) & 0x7FFFFFFFu);
+        sd.v = (int32_t)(((uint32_t)sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
+        if constexpr (PASS == kFused || PASS == kApply) {
+            cs = D.scratch[3];
+            bs = D.scratch[4];
+        }
+        if constexpr (PASS == kSingle) {
+            // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
+            // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
+            if (unit == t_begin && threadIdx.x == 0) {
+                float *sc = D.scratch;
+                sc[0] = 0.0f; sc[1] = 0.0f; sc[2] = 0.0f; sc[3] = 1.0f; sc[4] = 1.0f; sc[5] = 0.0f;
             }
-        } else if (e0 < n) {
+        }
+        cnt = 0;
+        units_here = 0;
+
+        // ---- whole, aligned units: software-pipelined vector path. The loads of the next
+        // unit are issued before the current unit is computed, so a wave always has one unit
+        // of HBM traffic in flight while it computes.
+        const uint32_t full_end = vec_ok ? t_begin + (uint32_t)(n / kUnit) : t_begin;
+        if (unit < full_end) {
+            auto issue = [&](uint32_t u) {
+                Inflight f;
+                const uint64_t e = (uint64_t)(u - t_begin) * kUnit + (uint64_t)threadIdx.x * 4u;
+                f.g = load_raw_dyn(gdt, D.g, e);
+                f.m = load_raw<ST>(D.m, e);
+                if constexpr (kDual) f.v = load_raw<ST>(D.v, e);
+                if constexpr (PASS != kCount) {
+                    if (master) f.mp = load_raw<LV_DTYPE_F32>(D.mp, e);
+                    else f.p = load_raw<PT>(D.p, e);
+                }
+                return f;
+            };
+            auto process = [&](const Inflight &cur, uint32_t u) {
+                const uint64_t e0 = (uint64_t)(u - t_begin) * kUnit + (uint64_t)threadIdx.x * 4u;
+                float g[8], m[8], v[8];
+                decode_raw_dyn(gdt, cur.g, g);
+                decode_raw<ST>(cur.m, m);
+                if constexpr (kDual) decode_raw<ST>(cur.v, v);
+                if constexpr (PASS == kCount) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f);
+                } else {
+                    float pin[8], pout[8], mpout[8];
+                    if (master) decode_raw<LV_DTYPE_F32>(cur.mp, pin);
+                    else decode_raw<PT>(cur.p, pin);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        float vj = kDual ? v[j] : 0.0f;
+                        const uint64_t ej = e0 + (j < 4 ? (uint64_t)j : (uint64_t)(kHalf + j - 4));
+                        uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)ej, cs, bs,
+                                                                pin[j], g[j], m[j], vj, pout[j], mpout[j]);
+                        if constexpr (kDual) v[j] = vj;
+                        if constexpr (kCounting) cnt += act;
+                    }
+                    store_raw<PT>(D.p, e0, pout);
+                    if (master) store_raw<LV_DTYPE_F32>(D.mp, e0, mpout);
+                    store_raw<ST>(D.m, e0, m);
+                    if constexpr (kDual) store_raw<ST>(D.v, e0, v);
+                }
+                units_here++;
+            };
+            // Two register buffers in ping-pong. The prefetch is unconditional (the last one of
+            // a run re-reads the current unit, in bounds and unused) so the wait counts are the
+            // same on every path and the compiler never has to drain the prefetch early.
+            Inflight A = issue(unit);
+            for (;;) {
+                uint32_t next = unit + stride;
+                bool more = next < full_end;
+                Inflight B = issue(more ? next : unit);
+                process(A, unit);
+                unit = next;
+                if (!more) break;
+                next = unit + stride;
+                more = next < full_end;
+                A = issue(more ? next : unit);
+                process(B, unit);
+                unit = next;
+                if (!more) break;
+            }
+        }
+
+        // ---- the partial last unit and unaligned tensors: per-element path
+        for (; unit < t_end; unit += stride) {
+            const uint64_t e0 = (uint64_t)(unit - t_begin) * kUnit + (uint64_t)threadIdx.x * kVec;
             const uint64_t e1 = (e0 + kVec < n) ? e0 + kVec : n;
             for (uint64_t i = e0; i < e1; i++) {
                 float g = load1_dyn(gdt, D.g, i);
@@ -571,8 +673,8 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                     if constexpr (kCounting) cnt += act;
                 }
             }
+            units_here++;
         }
-        units_here++;
     }
     if constexpr (kCounting) {
         if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
@@ -583,36 +685,52 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
 
 using KernelFn = void (*)(Args);
 
+// Flag word of the specialised ("static") instantiation: the reference defaults (cautious in
+// the counting passes, stochastic rounding, weight decay, coordinate bound, no master, grad
+// dtype = param dtype, v clamp for fp16 params).
+constexpr uint32_t static_flags(int PT, int PASS) {
+    return (PASS != kSingle ? (uint32_t)kFCautious : 0u) | (uint32_t)kFSR | (uint32_t)kFWeightDecay |
+           (uint32_t)kFCoordinate | (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8);
+}
+
+template <int MODE, int PT, int ST, int PASS>
+KernelFn pick_flags(uint32_t flags) {
+    constexpr uint32_t kStatic = static_flags(PT, PASS);
+    if (flags == kStatic) return step_kernel<MODE, PT, ST, PASS, kStatic>;
+    return step_kernel<MODE, PT, ST, PASS, kFDynamic>;
+}
+
 template <int MODE, int PT, int ST>
-KernelFn pick_pass(int pass) {
+KernelFn pick_pass(int pass, uint32_t flags) {
     switch (pass) {
-    case kSingle: return step_kernel<MODE, PT, ST, kSingle>;
-    case kFused: return step_kernel<MODE, PT, ST, kFused>;
-    case kCount: return step_kernel<MODE, PT, ST, kCount>;
-    default: return step_kernel<MODE, PT, ST, kApply>;
+    case kSingle: return pick_flags<MODE, PT, ST, kSingle>(flags);
+    case kFused: return pick_flags<MODE, PT, ST, kFused>(flags);
+    case kCount: return pick_flags<MODE, PT, ST, kCount>(flags);
+    default: return pick_flags<MODE, PT, ST, kApply>(flags);
     }
 }
 
 template <int MODE, int PT>
-KernelFn pick_state(int st, int pass) {
-    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass) : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass);
+KernelFn pick_state(int st, int pass, uint32_t flags) {
+    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass, flags)
+                              : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass, flags);
 }
 
 template <int MODE>
-KernelFn pick_param(int pt, int st, int pass) {
+KernelFn pick_param(int pt, int st, int pass, uint32_t flags) {
     switch (pt) {
-    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass);
-    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass);
-    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass);
+    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass, flags);
+    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass, flags);
+    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass, flags);
     }
 }
 
-static KernelFn pick_kernel(int mode, int pt, int st, int pass) {
+static KernelFn pick_kernel(int mode, int pt, int st, int pass, uint32_t flags) {
     switch (mode) {
-    case LV_BUFFER_TDCLM: return pick_param<LV_BUFFER_TDCLM>(pt, st, pass);
-    case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass);
-    case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass);
-    default: return pick_param<LV_BUFFER_T2>(pt, st, pass);
+    case LV_BUFFER_TDCLM: return pick_param<LV_BUFFER_TDCLM>(pt, st, pass, flags);
+    case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass, flags);
+    case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass, flags);
+    default: return pick_param<LV_BUFFER_T2>(pt, st, pass, flags);
     }
 }
 
@@ -685,21 +803,35 @@ static int validate_config(const lv_config *c) {
     return LV_STATUS_SUCCESS;
 }
 
-static int blocks_per_launch_cap() {
-    static int cap[64] = {0};
+// Persistent grid: exactly the blocks that can be resident at once (CUs x occupancy), so no
+// block waits for another to finish and the grid-stride loop has no tail round.
+static uint32_t resident_blocks(KernelFn fn) {
+    struct Entry {
+        int dev;
+        KernelFn fn;
+        uint32_t blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 2048;
-    if (cap[dev] == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-        int per_cu = 8;
-        if (const char *e = std::getenv("LV_BLOCKS_PER_CU")) {
-            int v = std::atoi(e);
-            if (v > 0 && v <= 64) per_cu = v;
-        }
-        cap[dev] = cus * per_cu;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const Entry &e : cache)
+        if (e.dev == dev && e.fn == fn) return e.blocks;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), kThreads, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = 4;
+    if (const char *e = std::getenv("LV_BLOCKS_PER_CU")) {
+        int v = std::atoi(e);
+        if (v > 0 && v <= 64) per_cu = v;
     }
-    return cap[dev];
+    uint32_t blocks = (uint32_t)cus * (uint32_t)per_cu;
+    cache.push_back({dev, fn, blocks});
+    return blocks;
 }
 
 struct Item {
@@ -712,8 +844,8 @@ struct Item {
 };
 
 static int launch(const Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
-    KernelFn fn = pick_kernel(mode, pt, st, pass);
-    uint32_t grid = std::min<uint32_t>(args.total_units, (uint32_t)blocks_per_launch_cap());
+    KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags);
+    uint32_t grid = std::min<uint32_t>(args.total_units, resident_blocks(fn));
     if (grid == 0) return LV_STATUS_SUCCESS;
     void *kargs[] = {const_cast<Args *>(&args)};
     hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(grid), dim3(kThreads), kargs, 0, stream);
