@@ -76,6 +76,10 @@ typedef struct lv_tensor {
     int32_t grad_dtype;
     int32_t state_dtype;
     int32_t reserved;
+    /* Element i uses stochastic-rounding offset (int32)(index_base + i). 0 for a whole tensor
+     * (the reference's `idx as i32`, reference_cpu/dual.rs:54); a shard of a larger tensor passes
+     * its global start so its bits equal the unsharded step. */
+    uint64_t index_base;
 } lv_tensor;
 
 /* Library version, major*10000 + minor*100 + patch. */

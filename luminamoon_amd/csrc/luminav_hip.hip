@@ -33,7 +33,7 @@ namespace lv {
 constexpr int kThreads = 256;
 constexpr int kVec = 8;
 constexpr uint32_t kUnit = kThreads * kVec;  // elements per work unit
-constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table)
+constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
@@ -48,7 +48,7 @@ enum Flags : uint32_t {
     kFCoordinate = 1u << 6,
 };
 
-// One tensor of a launch (64 bytes, lives in the kernel argument segment).
+// One tensor of a launch (72 bytes, lives in the kernel argument segment).
 struct Desc {
     void *p;
     const void *g;
@@ -59,6 +59,8 @@ struct Desc {
     uint64_t n;
     uint32_t unit_begin;  // first work unit of this tensor in the launch's unit space
     uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
+    uint32_t ibase;       // low 32 bits of index_base (the SR offset is taken mod 2^32)
+    uint32_t pad;
 };
 
 // Launch-uniform constants: hyper-parameters, per-step coefficients, tensor table.
@@ -542,6 +544,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
     bool vec_ok = false;
     float cs = 1.0f, bs = 1.0f;
     Seeds sd{0, 0, 0};
+    uint32_t ibase = 0;
     uint32_t cnt = 0, units_here = 0;
 
     const uint32_t stride = gridDim.x;
@@ -566,6 +569,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
         if (kDual) al |= (uintptr_t)D.v;
         if (master) al |= (uintptr_t)D.mp;
         vec_ok = (al & 15u) == 0;
+        ibase = D.ibase;
         uint32_t raw = a.seed_base + D.pidx * 10007u;
         sd.m = (int32_t)(raw & 0x7FFFFFFFu);
         sd.p = (int32_t)(((uint32_t)sd.m + 0x55555555u) & 0x7FFFFFFFu);
@@ -619,7 +623,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                     for (int j = 0; j < 8; j++) {
                         float vj = kDual ? v[j] : 0.0f;
                         const uint64_t ej = e0 + (j < 4 ? (uint64_t)j : (uint64_t)(kHalf + j - 4));
-                        uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)ej, cs, bs,
+                        uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)((uint32_t)ej + ibase), cs, bs,
                                                                 pin[j], g[j], m[j], vj, pout[j], mpout[j]);
                         if constexpr (kDual) v[j] = vj;
                         if constexpr (kCounting) cnt += act;
@@ -664,7 +668,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                 } else {
                     float pin = master ? D.mp[i] : load1<PT>(D.p, i);
                     float pout, mpout;
-                    uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)(uint32_t)i, cs, bs, pin, g, m, v,
+                    uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)((uint32_t)i + ibase), cs, bs, pin, g, m, v,
                                                             pout, mpout);
                     store1<PT>(D.p, i, pout);
                     if (master) D.mp[i] = mpout;
@@ -995,6 +999,7 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             D.n = T.numel;
             D.unit_begin = (uint32_t)units;
             D.pidx = (uint32_t)T.param_index;
+            D.ibase = (uint32_t)T.index_base;
             units += (T.numel + kUnit - 1) / kUnit;
         }
         if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");

@@ -62,6 +62,7 @@ class LvTensor(ctypes.Structure):
         ("grad_dtype", ctypes.c_int32),
         ("state_dtype", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("index_base", ctypes.c_uint64),
     ]
 
 
@@ -151,7 +152,10 @@ class HipStepper:
         scratches: Sequence[torch.Tensor],
         steps: Sequence[int],
         param_indices: Sequence[int],
+        index_bases: Optional[Sequence[int]] = None,
     ) -> None:
+        """index_bases: global element offset of each tensor when it is a shard of a larger
+        tensor (stochastic-rounding offsets continue from there); None = all 0."""
         n = len(params)
         if n == 0:
             return
@@ -205,6 +209,7 @@ class HipStepper:
             items[i] = LvTensor(
                 p.data_ptr(), g.data_ptr(), m.data_ptr(), vp, mpp, sc.data_ptr(), numel, int(steps[i]),
                 int(param_indices[i]), DTYPE_CODES[p.dtype], DTYPE_CODES[g.dtype], DTYPE_CODES[m.dtype], 0,
+                int(index_bases[i]) if index_bases is not None else 0,
             )
         cfg = make_config(group)
         ws = self.workspace.get(device, n)

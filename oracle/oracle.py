@@ -16,7 +16,8 @@ from typing import Optional, Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "libluminav_oracle.so")
+# LVO_LIB_OVERRIDE lets the mutation test point the pins at a deliberately broken build.
+_LIB_PATH = os.environ.get("LVO_LIB_OVERRIDE") or os.path.join(_HERE, "_build", "libluminav_oracle.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 BUFFER_CODES = {1: 1, 2: 2, "T1": 3, "T2": 4}
@@ -69,6 +70,8 @@ _lib: Optional[ctypes.CDLL] = None
 
 def build() -> str:
     """Compile the oracle with its Makefile (gcc); returns the library path."""
+    if os.environ.get("LVO_LIB_OVERRIDE"):
+        return _LIB_PATH
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
     return _LIB_PATH
 

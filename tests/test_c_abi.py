@@ -1,0 +1,96 @@
+"""The C ABI library loads here (no GPU), exports every function include/luminav_hip.h declares,
+and rejects bad calls on the host before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from luminamoon_amd.optimizer import hip_backend as H
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "luminav_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(lv_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(H.LIB_PATH):
+        from luminamoon_amd import build_ext
+
+        build_ext.build()
+    return H.load_library()
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted(H.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_workspace(lib):
+    assert lib.lv_version() >= 100
+    assert lib.lv_workspace_bytes(1) >= 16 and lib.lv_workspace_bytes(1) % 256 == 0
+    assert lib.lv_workspace_bytes(1000) >= 16 * 1000
+
+
+def test_struct_layouts_match_header():
+    # lv_config: 10 floats + 8 int32 = 72 bytes; lv_tensor: 6 pointers + 3 u64 + 4 i32 + u64 = 96 bytes
+    assert ctypes.sizeof(H.LvConfig) == 72
+    assert ctypes.sizeof(H.LvTensor) == 96
+
+
+def _cfg(**kw):
+    from tests.parity_util import group_dict
+
+    return H.make_config(group_dict(**kw))
+
+
+def test_host_side_rejections_without_device(lib):
+    cfg = _cfg(buffer="T2")
+    ws = (ctypes.c_uint8 * 4096)()
+    t = H.LvTensor()
+    assert lib.lv_step_multi(None, ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 0, ws, 4096, None) == 0  # nothing to do
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 1, ws, 4096, None) == -1
+    bad = _cfg(buffer="T2")
+    bad.lr = float("nan")
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, 4096, None) == -3
+    assert b"learning rate" in lib.lv_last_error()
+    bad = _cfg(buffer="T2")
+    bad.beta2 = 1.0
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, 4096, None) == -3
+    # a tensor with numel but no pointers
+    t.numel, t.step = 10, 1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert b"null" in lib.lv_last_error()
+    # missing exp_avg_sq in a dual-state mode, missing master for bf16 with master weights
+    t.param = t.grad = t.exp_avg = t.scratch = 0x1000
+    t.param_dtype = t.grad_dtype = 1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert b"exp_avg_sq" in lib.lv_last_error()
+    t.exp_avg_sq = 0x2000
+    mcfg = _cfg(buffer="T2", master_weights="full")
+    assert lib.lv_step_multi(ctypes.byref(mcfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert b"master_param" in lib.lv_last_error()
+    # step 0, a too-small workspace, grad aliasing param
+    t.step = 0
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -3
+    t.step = 1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 8, None) == -3
+    t.grad = t.param
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -3
+    # radial bound is rejected by this build
+    rcfg = _cfg(buffer="T2", bound_type="radial")
+    t.grad = 0x3000
+    assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, 4096, None) == -3
