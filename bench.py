@@ -43,6 +43,29 @@ WORKLOADS = {
 }
 
 
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes over this script
+#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o fetch -- python -u bench.py --steps 2 --warmup 1 --no-cpu-baseline
+#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir> -o write -- python -u bench.py --steps 2 --warmup 1 --no-cpu-baseline
+# (KiB per dispatch), each scaled by what the same counter reads for the copy probe below: the
+# 4 GiB negate runs as two dispatches of 2 GiB in + 2 GiB out each (torch splits it for 32-bit
+# indexing). On gfx950 FETCH_SIZE counts each 128-byte read request as 64 bytes (probe factor
+# 2.0) and WRITE_SIZE is exact (factor 1.0); TCC_EA0_RDREQ_DRAM_32B / TCC_EA0_WRREQ_WRITE_DRAM_32B
+# give the same byte totals for this kernel.
+PMC_TRAFFIC = {
+    5: dict(kernel="lv::step_kernel<4, 1, 0, 1, 331u>", fetch_kib=39493071.0, write_kib=65805580.84,
+            probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0),
+}
+
+
+def pmc_traffic_bytes(config: int):
+    t = PMC_TRAFFIC.get(config)
+    if t is None:
+        return None
+    read_factor = t["probe_bytes"] / (t["probe_fetch_kib"] * 1024.0)
+    write_factor = t["probe_bytes"] / (t["probe_write_kib"] * 1024.0)
+    return t["fetch_kib"] * 1024.0 * read_factor + t["write_kib"] * 1024.0 * write_factor
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -70,6 +93,29 @@ def fill_inputs(torch, n: int, pdt, grad_kind: str, seed: int = 1234):
         g[s:e].copy_(z.mul_(1e-3))
         del z
     return p, g
+
+
+def copy_probe(torch, n_floats: int = 1 << 30, reps: int = 5) -> float:
+    """A plain streaming kernel of known traffic: y = -x over n_floats fp32 values (4 GiB read +
+    4 GiB written, far above the 256 MB last-level cache; torch runs it as two 2 GiB dispatches).
+    It is the calibration kernel for the HBM byte counters (FETCH_SIZE / WRITE_SIZE) and a
+    reference bandwidth for the step kernel. Returns GB/s (read + write) of the median call."""
+    x = torch.empty(n_floats, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.neg(x, out=y)
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        torch.neg(x, out=y)
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    times.sort()
+    ms = times[len(times) // 2]
+    del x, y
+    return 8.0 * n_floats / (ms / 1e3) / 1e9
 
 
 def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
@@ -213,6 +259,8 @@ def main() -> int:
         return 1
     del opt, p, p_data, g_data
     torch.cuda.empty_cache()
+    copy_gbs = copy_probe(torch)
+    log(f"copy probe (fp32 negate, 4 GiB in + 4 GiB out): {copy_gbs:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -244,13 +292,14 @@ def main() -> int:
         },
         "achieved_gb_per_s": achieved,
         "hbm_frac": achieved / HBM_PEAK_GBS,
+        "copy_probe_gb_per_s": copy_gbs,
         "roofline": {
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": pmc_traffic_bytes(args.config),
         },
         "cpu_baseline": cpu,
     }
