@@ -8,6 +8,14 @@
 // last block of each tensor -- found with a per-tensor ticket -- finalises the 6-float scratch
 // on the device, so a step needs no host synchronisation and no extra launch.
 //
+// Radial bound: the squared-norm sums sum(u_eff^2) and sum(p^2) are accumulated from the f32
+// squares in f64 (per thread, then a fixed-order wave/block reduction), each block stores its
+// partial in a workspace slot, and the finalising block folds the slots in block order. The
+// result (rounded to f32 once) is the exactly rounded sum up to f64 rounding, and bitwise
+// deterministic for a given grid. The reference's own f32 sums depend on its CPU backend
+// (16-lane order in reference_cpu/dual.rs:134-253 vs. AVX-512 reductions in avx512/dual.rs),
+// so radial results match it to its cross-backend tolerance, not bit for bit.
+//
 // Per-element arithmetic follows the reference's scalar core operation for operation
 // (optimizer/crates/luminav-core/src/reference_cpu/dual.rs, reference_cpu/tdclm.rs,
 // math.rs, prng.rs): explicit fmaf exactly where the Rust code calls mul_add, separately
@@ -34,6 +42,7 @@ constexpr int kThreads = 256;
 constexpr int kVec = 8;
 constexpr uint32_t kUnit = kThreads * kVec;  // elements per work unit
 constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
+constexpr uint32_t kRadialMaxBlocks = 2048;  // grid cap of radial launches (workspace partial slots)
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
@@ -72,6 +81,7 @@ struct Args {
     uint32_t total_units;
     int32_t ndesc;
     unsigned long long *counters;  // 2 per tensor: cautious mask count, finished-unit ticket
+    double *partials;              // radial: [tensor][block] pairs (sum u_eff^2, sum p^2)
     Desc d[kMaxDesc];
 };
 
@@ -247,6 +257,24 @@ __device__ __forceinline__ float fp16_safety_bound(float step, float p_init) {
 __device__ __forceinline__ float cautious_scale(float mask_sum, float total, float clamp_min) {
     float denom = __builtin_fmaxf(total, 1.0f);
     return 1.0f / rclamp(mask_sum / denom, clamp_min, 1.0f);
+}
+
+// math.rs:127-160: radial trust-region scale from the squared norms. TRI selects the rational
+// form of the triangle family (T1/T2), otherwise tanh(r)/r.
+template <bool TRI>
+__device__ __forceinline__ float radial_scale(float u_sq, float p_sq, float cs, float lr, float ratio) {
+    float norm_p = __builtin_sqrtf(__builtin_fmaxf(p_sq, 0.0f));
+    float norm_d = __builtin_sqrtf(__builtin_fmaxf(u_sq, 0.0f)) * cs;
+    float radius = ratio * __builtin_fmaxf(norm_p, 1.0f);
+    if constexpr (TRI) {
+        float r = (lr * norm_d) / __builtin_fmaxf(radius, 1.0e-12f);
+        float one_plus_r = 1.0f + r;
+        return one_plus_r / __builtin_fmaf(r, r, one_plus_r);
+    } else {
+        float r = (lr * norm_d) / radius;
+        if (r < 1.0e-4f) return 1.0f;
+        return tanh_pade(r) / __builtin_fmaxf(r, 1.0e-8f);
+    }
 }
 
 // Round-to-nearest-even u64 -> f32 (Rust `as f32`), exact integer algorithm.
@@ -431,11 +459,12 @@ struct Seeds {
 };
 
 // Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
-// Returns the cautious mask bit.
+// Returns the cautious mask bit; u_eff is the (masked) direction whose square feeds the radial
+// norm (dual.rs:176-180).
 template <int MODE, int PT, int ST>
 __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const Seeds &sd, int32_t off,
                                                float cs, float bs, float p_init, float g_raw, float &m_io,
-                                               float &v_io, float &p_out, float &mp_out) {
+                                               float &v_io, float &p_out, float &mp_out, float &u_eff) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     const bool sr = flags & kFSR;
@@ -446,7 +475,8 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
     float m_mask = active ? 1.0f : 0.0f;
     m_io = quantize<ST>(m_new, sd.m, off, sr);
     if constexpr (kDual) v_io = quantize<ST>(v_new, sd.v, off, sr);
-    float delta = (flags & kFCautious) ? (u * m_mask) * cs : u;
+    u_eff = (flags & kFCautious) ? u * m_mask : u;
+    float delta = (flags & kFCautious) ? u_eff * cs : u;
     float step = a.lr * delta;
     if (flags & kFRadial) step *= bs;
     else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio);
@@ -464,57 +494,139 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
 
 // Counting path for one element (dual.rs:279-303, dual.rs:720-746, tdclm.rs:232-248).
 template <int MODE>
-__device__ __forceinline__ uint32_t count_elem(const Args &a, uint32_t flags, float g_raw, float m, float v) {
+__device__ __forceinline__ uint32_t count_elem(const Args &a, uint32_t flags, float g_raw, float m, float v,
+                                               float &u_eff) {
     float g = sanitize(g_raw);
     float m_new, v_new;
     float u = compute_u<MODE>(a, flags & kFClampV, g, m, v, m_new, v_new);
-    return (u * g) > 0.0f ? 1u : 0u;
+    bool active = (u * g) > 0.0f;
+    u_eff = (flags & kFCautious) ? u * (active ? 1.0f : 0.0f) : u;
+    return active ? 1u : 0u;
 }
 
 // ------------------------------------------------------------------ scratch finalisation
 
 // Last block of tensor t: dual.rs:255-259 + math.rs:188-239 (fused), dual.rs:330-351 +
-// dual.rs:436-438 (two-pass count).  Thread 0 only.
-template <int PASS>
-__device__ void finalize_scratch(const Args &a, const Desc &D, unsigned long long mask_count) {
+// dual.rs:436-438 (two-pass count).  Thread 0 only. Slots 3/4 end at 1.0 when cautious /
+// radial is off, the value the reference's host layer forces before every step
+// (luminav.py:1748-1751).
+template <int MODE, int PASS>
+__device__ void finalize_scratch(const Args &a, bool radial, const Desc &D, unsigned long long mask_count,
+                                 float u_sq, float p_sq) {
+    constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
     float *s = D.scratch;
     const bool cautious = a.flags & kFCautious;
     float mask_sum = u64_to_f32_rn(mask_count);
     float total = u64_to_f32_rn(D.n);
-    float s3;
+    float s3, s4 = 1.0f;
     if constexpr (PASS == kFused) {
         s3 = cautious ? __builtin_fmaf(a.ema, s[3], a.ema_c * cautious_scale(mask_sum, total, a.clamp_min)) : 1.0f;
+        if (radial)
+            s4 = __builtin_fmaf(a.ema, s[4], a.ema_c * radial_scale<kTri>(u_sq, p_sq, s3, a.lr, a.ratio));
     } else {
         s3 = cautious ? cautious_scale(mask_sum, total, a.clamp_min) : 1.0f;
+        if (radial) s4 = radial_scale<kTri>(u_sq, p_sq, s3, a.lr, a.ratio);
     }
     s[0] = 0.0f;
     s[1] = 0.0f;
     s[2] = 0.0f;
     s[3] = s3;
-    s[4] = 1.0f;
+    s[4] = s4;
     s[5] = 0.0f;
 }
 
-// Block-wide sum of the per-thread mask counts, then the per-tensor ticket.
-template <int PASS>
-__device__ void flush_tensor(const Args &a, int t, uint32_t n_units, uint32_t cnt, uint32_t units_here,
-                             uint32_t *red) {
+struct BlockShared {
+    uint32_t cnt[kThreads / 64];
+    double su[kThreads / 64];
+    double sp[kThreads / 64];
+    uint32_t last;
+};
+
+// Butterfly sum over the 64 lanes; every lane ends with the same, order-fixed value.
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+__device__ __forceinline__ double load_partial(const double *p) {
+    uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __longlong_as_double((long long)b);
+}
+
+// End of a block's run over tensor t: block sums of the mask count (and of the radial squares),
+// then the per-tensor ticket; the block that completes the tensor folds the radial partials of
+// all blocks in block order and finalises the scratch.
+template <int MODE, int PASS>
+__device__ void flush_tensor(const Args &a, bool radial, int t, uint32_t t_begin, uint32_t n_units, uint32_t cnt,
+                             double su, double sp, uint32_t units_here, BlockShared &sh) {
+    const int w = threadIdx.x >> 6;
+    const bool lane0 = (threadIdx.x & 63) == 0;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = cnt;
+    if (radial) {
+        su = wave_sum(su);
+        sp = wave_sum(sp);
+    }
+    if (lane0) {
+        sh.cnt[w] = cnt;
+        sh.su[w] = su;
+        sh.sp[w] = sp;
+    }
     __syncthreads();
+    unsigned long long *ctr = a.counters + 2 * t;
     if (threadIdx.x == 0) {
         uint32_t tot = 0;
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; w++) tot += red[w];
-        unsigned long long *ctr = a.counters + 2 * t;
+        for (int k = 0; k < kThreads / 64; k++) tot += sh.cnt[k];
         if (tot) atomicAdd(&ctr[0], (unsigned long long)tot);
+        if (radial) {
+            double bu = 0.0, bp = 0.0;
+#pragma unroll
+            for (int k = 0; k < kThreads / 64; k++) {
+                bu += sh.su[k];
+                bp += sh.sp[k];
+            }
+            double *slot = a.partials + 2 * ((size_t)t * gridDim.x + blockIdx.x);
+            slot[0] = bu;
+            slot[1] = bp;
+        }
         __threadfence();
         unsigned long long prev = atomicAdd(&ctr[1], (unsigned long long)units_here);
-        if (prev + units_here == (unsigned long long)n_units) {
-            __threadfence();
+        sh.last = (prev + units_here == (unsigned long long)n_units) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (sh.last) {  // block-uniform
+        __threadfence();
+        double fu = 0.0, fp = 0.0;
+        if (radial) {
+            // Unit u is processed by block u % G, so the blocks that visited t are those of its
+            // first min(n_units, G) units.
+            const uint32_t G = gridDim.x;
+            const uint32_t nb = n_units < G ? n_units : G;
+            for (uint32_t k = threadIdx.x; k < nb; k += kThreads) {
+                const double *slot = a.partials + 2 * ((size_t)t * G + (t_begin + k) % G);
+                fu += load_partial(slot);
+                fp += load_partial(slot + 1);
+            }
+            fu = wave_sum(fu);
+            fp = wave_sum(fp);
+            if (lane0) {  // thread 0 finished reading sh.su / sh.sp before the barrier above
+                sh.su[w] = fu;
+                sh.sp[w] = fp;
+            }
+            __syncthreads();
+            fu = 0.0;
+            fp = 0.0;
+#pragma unroll
+            for (int k = 0; k < kThreads / 64; k++) {
+                fu += sh.su[k];
+                fp += sh.sp[k];
+            }
+        }
+        if (threadIdx.x == 0) {
             unsigned long long total = atomicAdd(&ctr[0], 0ull);
-            finalize_scratch<PASS>(a, a.d[t], total);
+            finalize_scratch<MODE, PASS>(a, radial, a.d[t], total, (float)fu, (float)fp);
             atomicExch(&ctr[0], 0ull);
             atomicExch(&ctr[1], 0ull);
         }
@@ -531,11 +643,12 @@ template <int MODE, int PT, int ST, int PASS, uint32_t FL>
 __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
-    __shared__ uint32_t red[kThreads / 64];
+    __shared__ BlockShared sh;
 
     const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
     const int gdt = (int)((flags >> 8) & 3u);
     const bool master = flags & kFMaster;
+    const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
     const uint32_t total_units = a.total_units;
 
     int t = -1;
@@ -546,13 +659,14 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
     Seeds sd{0, 0, 0};
     uint32_t ibase = 0;
     uint32_t cnt = 0, units_here = 0;
+    double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
 
     const uint32_t stride = gridDim.x;
     uint32_t unit = blockIdx.x;
     while (unit < total_units) {
         // ---- switch to the tensor that owns `unit` (units of one tensor are contiguous)
         if constexpr (kCounting) {
-            if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
+            if (t >= 0) flush_tensor<MODE, PASS>(a, radial, t, t_begin, t_end - t_begin, cnt, su, sp, units_here, sh);
         }
         int lo = t + 1, hi = a.ndesc - 1;  // units only grow, so search right of t
         while (lo < hi) {
@@ -588,6 +702,8 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
         }
         cnt = 0;
         units_here = 0;
+        su = 0.0;
+        sp = 0.0;
 
         // ---- whole, aligned units: software-pipelined vector path. The loads of the next
         // unit are issued before the current unit is computed, so a wave always has one unit
@@ -600,7 +716,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                 f.g = load_raw_dyn(gdt, D.g, e);
                 f.m = load_raw<ST>(D.m, e);
                 if constexpr (kDual) f.v = load_raw<ST>(D.v, e);
-                if constexpr (PASS != kCount) {
+                if (PASS != kCount || radial) {  // the count pass reads p only for the radial norm
                     if (master) f.mp = load_raw<LV_DTYPE_F32>(D.mp, e);
                     else f.p = load_raw<PT>(D.p, e);
                 }
@@ -613,8 +729,20 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                 decode_raw<ST>(cur.m, m);
                 if constexpr (kDual) decode_raw<ST>(cur.v, v);
                 if constexpr (PASS == kCount) {
+                    float pin[8];
+                    if (radial) {
+                        if (master) decode_raw<LV_DTYPE_F32>(cur.mp, pin);
+                        else decode_raw<PT>(cur.p, pin);
+                    }
 #pragma unroll
-                    for (int j = 0; j < 8; j++) cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f);
+                    for (int j = 0; j < 8; j++) {
+                        float ue;
+                        cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
+                        if (radial) {
+                            su += (double)(ue * ue);
+                            sp += (double)(pin[j] * pin[j]);
+                        }
+                    }
                 } else {
                     float pin[8], pout[8], mpout[8];
                     if (master) decode_raw<LV_DTYPE_F32>(cur.mp, pin);
@@ -622,11 +750,18 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         float vj = kDual ? v[j] : 0.0f;
+                        float ue;
                         const uint64_t ej = e0 + (j < 4 ? (uint64_t)j : (uint64_t)(kHalf + j - 4));
                         uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)((uint32_t)ej + ibase), cs, bs,
-                                                                pin[j], g[j], m[j], vj, pout[j], mpout[j]);
+                                                                pin[j], g[j], m[j], vj, pout[j], mpout[j], ue);
                         if constexpr (kDual) v[j] = vj;
-                        if constexpr (kCounting) cnt += act;
+                        if constexpr (kCounting) {
+                            cnt += act;
+                            if (radial) {
+                                su += (double)(ue * ue);
+                                sp += (double)(pin[j] * pin[j]);
+                            }
+                        }
                     }
                     store_raw<PT>(D.p, e0, pout);
                     if (master) store_raw<LV_DTYPE_F32>(D.mp, e0, mpout);
@@ -664,24 +799,36 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
                 float m = load1<ST>(D.m, i);
                 float v = kDual ? load1<ST>(D.v, i) : 0.0f;
                 if constexpr (PASS == kCount) {
-                    cnt += count_elem<MODE>(a, flags, g, m, v);
+                    float ue;
+                    cnt += count_elem<MODE>(a, flags, g, m, v, ue);
+                    if (radial) {
+                        float pin = master ? D.mp[i] : load1<PT>(D.p, i);
+                        su += (double)(ue * ue);
+                        sp += (double)(pin * pin);
+                    }
                 } else {
                     float pin = master ? D.mp[i] : load1<PT>(D.p, i);
-                    float pout, mpout;
+                    float pout, mpout, ue;
                     uint32_t act = apply_elem<MODE, PT, ST>(a, flags, sd, (int32_t)((uint32_t)i + ibase), cs, bs, pin, g, m, v,
-                                                            pout, mpout);
+                                                            pout, mpout, ue);
                     store1<PT>(D.p, i, pout);
                     if (master) D.mp[i] = mpout;
                     store1<ST>(D.m, i, m);
                     if constexpr (kDual) store1<ST>(D.v, i, v);
-                    if constexpr (kCounting) cnt += act;
+                    if constexpr (kCounting) {
+                        cnt += act;
+                        if (radial) {
+                            su += (double)(ue * ue);
+                            sp += (double)(pin * pin);
+                        }
+                    }
                 }
             }
             units_here++;
         }
     }
     if constexpr (kCounting) {
-        if (t >= 0) flush_tensor<PASS>(a, t, t_end - t_begin, cnt, units_here, red);
+        if (t >= 0) flush_tensor<MODE, PASS>(a, radial, t, t_begin, t_end - t_begin, cnt, su, sp, units_here, sh);
     }
 }
 
@@ -850,6 +997,7 @@ struct Item {
 static int launch(const Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
     KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags);
     uint32_t grid = std::min<uint32_t>(args.total_units, resident_blocks(fn));
+    if (args.flags & kFRadial) grid = std::min<uint32_t>(grid, kRadialMaxBlocks);  // partial slots per tensor
     if (grid == 0) return LV_STATUS_SUCCESS;
     void *kargs[] = {const_cast<Args *>(&args)};
     hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(grid), dim3(kThreads), kargs, 0, stream);
@@ -865,10 +1013,16 @@ extern "C" {
 
 int lv_version(void) { return 100; }
 
-size_t lv_workspace_bytes(int n_tensors) {
-    if (n_tensors < 1) n_tensors = 1;
+// Layout: [2 u64 counters per tensor, padded to 256 B][radial partials: kMaxDesc x
+// kRadialMaxBlocks x 2 doubles, reused by every launch of a call (stream-ordered)].
+static size_t counter_bytes(int n_tensors) {
     size_t b = (size_t)n_tensors * 2 * sizeof(unsigned long long);
     return (b + 255) & ~(size_t)255;
+}
+
+size_t lv_workspace_bytes(int n_tensors) {
+    if (n_tensors < 1) n_tensors = 1;
+    return counter_bytes(n_tensors) + (size_t)lv::kMaxDesc * lv::kRadialMaxBlocks * 2 * sizeof(double);
 }
 
 const char *lv_last_error(void) { return lv::g_err; }
@@ -884,8 +1038,6 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     int rc = validate_config(cfg);
     if (rc != LV_STATUS_SUCCESS) return rc;
     const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;  // config.rs:368-375
-    if (bound == LV_BOUND_RADIAL)
-        return fail(LV_STATUS_INVALID_CONFIG, "bound_type='radial' is not supported by this build of the HIP backend");
     const bool dual = cfg->buffer == LV_BUFFER_DUAL || cfg->buffer == LV_BUFFER_T2;
     const bool cautious = cfg->cautious != 0;
     if (!workspace) return fail(LV_STATUS_NULL_POINTER, "workspace is NULL");
@@ -983,6 +1135,7 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
         if (cfg->weight_decay != 0.0f) flags |= kFWeightDecay;
         if (h.clampv) flags |= kFClampV;
         if (bound == LV_BOUND_COORDINATE) flags |= kFCoordinate;
+        if (bound == LV_BOUND_RADIAL) flags |= kFRadial;
         flags |= (uint32_t)h.gt << 8;
         args.flags = flags;
         uint64_t units = 0;
@@ -1005,6 +1158,7 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
         if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
         args.total_units = (uint32_t)units;
         args.counters = ctr + 2 * begin;  // slots [begin, end) of this call's workspace
+        args.partials = reinterpret_cast<double *>(static_cast<char *>(workspace) + counter_bytes(count));
         if (h.pass == kCount) {
             rc = launch(args, cfg->buffer, h.pt, h.st, kCount, stream);
             if (rc == LV_STATUS_SUCCESS) rc = launch(args, cfg->buffer, h.pt, h.st, kApply, stream);

@@ -476,12 +476,20 @@ static inline int count_elem(const coef_t *k, const view_t *w, uint64_t idx, flo
 typedef struct {
     uint64_t mask;
     float u_sq, p_sq;
+    double du, dp; /* f64 sum mode */
 } chunk_metrics;
+
+/* Radial sum mode (checker option, not a reference behaviour): 0 = the scalar core's f32 lane
+ * and chunk order (default); 1 = every f32 square added in f64, rounded to f32 once -- the
+ * order-independent sum the HIP kernels compute, so they can be compared bit for bit. */
+static int g_radial_sum_f64 = 0;
+void lvo_set_radial_sum_mode(int32_t mode) { g_radial_sum_f64 = mode ? 1 : 0; }
+int32_t lvo_radial_sum_mode(void) { return g_radial_sum_f64; }
 
 /* One 2,097,152-element chunk of a counting pass: lane sums exactly as the scalar core. */
 static chunk_metrics run_chunk(const coef_t *k, const view_t *w, uint64_t start, uint64_t end,
                                int apply, float cs, float bs) {
-    chunk_metrics cm = {0, 0.0f, 0.0f};
+    chunk_metrics cm = {0, 0.0f, 0.0f, 0.0, 0.0};
     uint64_t len = end - start;
     uint64_t simd_len = len & ~15ull;
     float ul[16] = {0}, pl[16] = {0};
@@ -494,7 +502,8 @@ static chunk_metrics run_chunk(const coef_t *k, const view_t *w, uint64_t start,
                         : count_elem(k, w, idx, radial ? &usq : NULL, &psq);
         if (k->cautious && act) cm.mask += 1;
         if (radial) {
-            if (li < simd_len) { ul[li & 15] += usq; pl[li & 15] += psq; }
+            if (g_radial_sum_f64) { cm.du += (double)usq; cm.dp += (double)psq; }
+            else if (li < simd_len) { ul[li & 15] += usq; pl[li & 15] += psq; }
             else { ut += usq; pt += psq; }
         }
     }
@@ -509,7 +518,7 @@ static chunk_metrics run_chunk(const coef_t *k, const view_t *w, uint64_t start,
 static chunk_metrics run_counting(const coef_t *k, const view_t *w, uint64_t n, int apply,
                                   float cs, float bs, int threads) {
     uint64_t nchunks = (n + LVO_ELEM_CHUNK_SIZE - 1) / LVO_ELEM_CHUNK_SIZE;
-    chunk_metrics tot = {0, 0.0f, 0.0f};
+    chunk_metrics tot = {0, 0.0f, 0.0f, 0.0, 0.0};
     if (threads > 1 && nchunks > 1) {
         chunk_metrics *parts = (chunk_metrics *)malloc(nchunks * sizeof(chunk_metrics));
 #pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
@@ -522,6 +531,8 @@ static chunk_metrics run_counting(const coef_t *k, const view_t *w, uint64_t n, 
             tot.mask += parts[c].mask;
             tot.u_sq += parts[c].u_sq;
             tot.p_sq += parts[c].p_sq;
+            tot.du += parts[c].du;
+            tot.dp += parts[c].dp;
         }
         free(parts);
     } else {
@@ -532,7 +543,13 @@ static chunk_metrics run_counting(const coef_t *k, const view_t *w, uint64_t n, 
             tot.mask += cm.mask;
             tot.u_sq += cm.u_sq;
             tot.p_sq += cm.p_sq;
+            tot.du += cm.du;
+            tot.dp += cm.dp;
         }
+    }
+    if (g_radial_sum_f64) {
+        tot.u_sq = (float)tot.du;
+        tot.p_sq = (float)tot.dp;
     }
     return tot;
 }

@@ -93,6 +93,12 @@ float lvo_fp16_safety_bound_t2(float step, float p_init);
 void lvo_update_post_step_ema(float *scratch, float total, const lvo_config *cfg, int32_t triangle);
 float lvo_u64_to_f32(uint64_t x);
 
+/* Radial-bound sum mode (checker option): 0 (default) = the scalar core's f32 16-lane / chunk
+ * order (reference_cpu/dual.rs:134-253, parallel/dual.rs:192-200); 1 = each f32 square added
+ * in f64 and rounded to f32 once (the HIP kernels' order-independent sum). Process-global. */
+void lvo_set_radial_sum_mode(int32_t mode);
+int32_t lvo_radial_sum_mode(void);
+
 /* Validate like LuminaVConfig::validate (config.rs:329-366). Returns LVO_OK or LVO_ERR_CONFIG. */
 int lvo_validate_config(const lvo_config *cfg);
 

@@ -8,6 +8,7 @@ luminav_oracle.c for the per-function citations.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import subprocess
@@ -111,6 +112,8 @@ def lib() -> ctypes.CDLL:
             "lvo_fp16_safety_bound_t2": (f, [f, f]),
             "lvo_update_post_step_ema": (None, [ctypes.POINTER(f), f, ctypes.POINTER(LvoConfig), i32]),
             "lvo_u64_to_f32": (f, [u64]),
+            "lvo_set_radial_sum_mode": (None, [i32]),
+            "lvo_radial_sum_mode": (i32, []),
             "lvo_validate_config": (ctypes.c_int, [ctypes.POINTER(LvoConfig)]),
             "lvo_step_multi": (ctypes.c_int, [ctypes.POINTER(LvoConfig), ctypes.POINTER(LvoTensor), ctypes.c_int, ctypes.c_int]),
             "lvo_last_error": (ctypes.c_char_p, []),
@@ -122,6 +125,19 @@ def lib() -> ctypes.CDLL:
         _ = P
         _lib = L
     return _lib
+
+
+@contextlib.contextmanager
+def radial_sum_f64():
+    """Inside the block the oracle adds the radial squares in f64 and rounds to f32 once (the
+    HIP kernels' order-independent sum) instead of the scalar core's f32 lane order."""
+    L = lib()
+    old = L.lvo_radial_sum_mode()
+    L.lvo_set_radial_sum_mode(1)
+    try:
+        yield
+    finally:
+        L.lvo_set_radial_sum_mode(old)
 
 
 def make_config(

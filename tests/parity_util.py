@@ -20,6 +20,25 @@ def seeded_tensor(n: int, seed: int, scale: float, dtype: torch.dtype, zero_frac
     return torch.from_numpy(x).to(dtype)
 
 
+def prng_np(seed: int, idx: np.ndarray) -> np.ndarray:
+    """_prng (prng.rs:21-26) vectorised with the arithmetic of the reference's NumPy restatement
+    (validation.py:73-77); tests compare it with the oracle's lvo_prng."""
+    z = (idx.astype(np.int64) + int(seed) - 1640531527).astype(np.int32)
+    z = (((z ^ (z >> 16)).astype(np.int64) * -2048173461) & 0xFFFFFFFF).astype(np.int32)
+    z = (((z ^ (z >> 13)).astype(np.int64) * -1028477387) & 0xFFFFFFFF).astype(np.int32)
+    return (z ^ (z >> 16)).astype(np.int32)
+
+
+def reference_pseudo_random(n: int, seed: int, scale: float, dtype: torch.dtype) -> torch.Tensor:
+    """The inputs of the reference's differential-parity tests
+    (luminav-simd/tests/differential_parity.rs:18-27): unit = f32(prng / i32::MAX), val = unit *
+    scale in f32, rounded to the dtype (RNE, no noise)."""
+    r = prng_np(seed, np.arange(n, dtype=np.int64))
+    unit = (r.astype(np.float64) / float(2 ** 31 - 1)).astype(np.float32)
+    val = unit * np.float32(scale)
+    return torch.from_numpy(val).to(dtype)
+
+
 def bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().contiguous().cpu()
     if t.dtype in (torch.bfloat16, torch.float16):

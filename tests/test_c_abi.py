@@ -42,6 +42,8 @@ def test_version_and_workspace(lib):
     assert lib.lv_version() >= 100
     assert lib.lv_workspace_bytes(1) >= 16 and lib.lv_workspace_bytes(1) % 256 == 0
     assert lib.lv_workspace_bytes(1000) >= 16 * 1000
+    # counters (16 B per tensor) plus the radial partial slots (48 tensors x 2048 blocks x 16 B)
+    assert lib.lv_workspace_bytes(1) >= 48 * 2048 * 16
 
 
 def test_struct_layouts_match_header():
@@ -58,39 +60,40 @@ def _cfg(**kw):
 
 def test_host_side_rejections_without_device(lib):
     cfg = _cfg(buffer="T2")
-    ws = (ctypes.c_uint8 * 4096)()
+    WS = lib.lv_workspace_bytes(1)
+    ws = (ctypes.c_uint8 * WS)()
     t = H.LvTensor()
-    assert lib.lv_step_multi(None, ctypes.byref(t), 1, ws, 4096, None) == -1
-    assert lib.lv_step_multi(ctypes.byref(cfg), None, 0, ws, 4096, None) == 0  # nothing to do
-    assert lib.lv_step_multi(ctypes.byref(cfg), None, 1, ws, 4096, None) == -1
+    assert lib.lv_step_multi(None, ctypes.byref(t), 1, ws, WS, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 0, ws, WS, None) == 0  # nothing to do
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 1, ws, WS, None) == -1
     bad = _cfg(buffer="T2")
     bad.lr = float("nan")
-    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, 4096, None) == -3
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, WS, None) == -3
     assert b"learning rate" in lib.lv_last_error()
     bad = _cfg(buffer="T2")
     bad.beta2 = 1.0
-    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, 4096, None) == -3
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, WS, None) == -3
     # a tensor with numel but no pointers
     t.numel, t.step = 10, 1
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
     assert b"null" in lib.lv_last_error()
     # missing exp_avg_sq in a dual-state mode, missing master for bf16 with master weights
     t.param = t.grad = t.exp_avg = t.scratch = 0x1000
     t.param_dtype = t.grad_dtype = 1
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
     assert b"exp_avg_sq" in lib.lv_last_error()
     t.exp_avg_sq = 0x2000
     mcfg = _cfg(buffer="T2", master_weights="full")
-    assert lib.lv_step_multi(ctypes.byref(mcfg), ctypes.byref(t), 1, ws, 4096, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(mcfg), ctypes.byref(t), 1, ws, WS, None) == -1
     assert b"master_param" in lib.lv_last_error()
     # step 0, a too-small workspace, grad aliasing param
     t.step = 0
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -3
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -3
     t.step = 1
     assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 8, None) == -3
     t.grad = t.param
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 4096, None) == -3
-    # radial bound is rejected by this build
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -3
+    # radial: same host checks (the call is never launched here)
     rcfg = _cfg(buffer="T2", bound_type="radial")
-    t.grad = 0x3000
-    assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, 4096, None) == -3
+    assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, WS, None) == -3
+    assert b"aliases" in lib.lv_last_error()

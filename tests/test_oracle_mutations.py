@@ -30,6 +30,9 @@ MUTATIONS = {
     "cautious_scale_no_clamp": ("float m_bar = rclamp(mask_sum / denom, clamp_min, 1.0f);", "float m_bar = mask_sum / denom; (void)clamp_min;"),
     "weight_decay_sign": ("fmaf(-k->lr_wd, p_init, p_init)", "fmaf(k->lr_wd, p_init, p_init)"),
     "sanitize_keeps_inf": ("if (isfinite(g) && fabsf(g) < 1.0e38f)", "if (!isnan(g))"),
+    "radial_norm_ignores_cautious_mask": ("float u_eff = k->cautious ? u * (active ? 1.0f : 0.0f) : u;",
+                                          "float u_eff = u; (void)active;"),
+    "radial_norm_uses_updated_param": ("*p_sq_out = p_init * p_init;", "*p_sq_out = p_upd * p_upd;"),
 }
 
 

@@ -259,6 +259,96 @@ def test_cautious_scale_and_ema_known_answer(oracle_mod):
     assert s[0] == s[1] == s[2] == 0.0
 
 
+def _t1_radial_expectation(p, g, m, lr, lam, ratio, eps):
+    """Closed form of the radial inputs for T1 (no bias correction, no v): u, the cautious mask
+    u*g > 0, and the squared norms sum((u*mask)^2), sum(p^2), evaluated in float64 from the f32
+    inputs and the f32-rounded coefficients (tdclm.rs:102-109, dual.rs:176-180)."""
+    b1sq = np.float32(np.float32(0.9) * np.float32(0.9))
+    omb1sq = np.float32(1.0) - b1sq
+    p64, g64, m64 = (x.astype(np.float64) for x in (p, g, m))
+    u = (float(b1sq) * m64 + float(omb1sq) * g64) / (
+        float(b1sq) * np.abs(m64) + float(np.float32(eps)) + float(omb1sq) * np.abs(g64)
+        + float(np.float32(lam)) * np.abs(g64 - m64))
+    active = u * g64 > 0
+    count = int(active.sum())
+    return float(np.sum((u * active) ** 2)), float(np.sum(p64 ** 2)), count
+
+
+def _t1_radial_target(u_sq, p_sq, cs, lr, ratio):
+    r = lr * math.sqrt(u_sq) * cs / (ratio * max(math.sqrt(p_sq), 1.0))
+    return (1.0 + r) / (1.0 + r + r * r)
+
+
+@pytest.mark.parametrize("f64_sums", [False, True])
+def test_radial_norms_two_pass_and_fused(oracle_mod, f64_sums):
+    """The radial scale is built from sum((u*mask)^2) over the cautious mask and sum(p_init^2)
+    (dual.rs:279-320 two-pass, dual.rs:176-190 fused + math.rs:188-239 EMA). Checked against the
+    closed form from the inputs, with the initial m chosen so that about a third of the mask is off.
+    The f64 sum mode must land within 1e-6; the scalar core's f32 lane order within its own
+    first-order summation bound, (adds per lane) x 2^-24 (|d ln bs / d ln r| < 1, r ~ sqrt(U/P))."""
+    O = oracle_mod
+    n = 100_003
+    rng = np.random.default_rng(21)
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    g[::33] = 0.0
+    m0 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    lr, lam, ratio, eps = 1e-2, 0.3, 0.05, 1e-8
+    u_sq, p_sq, count = _t1_radial_expectation(p0, g, m0, lr, lam, ratio, eps)
+    assert 0.55 * n < count < 0.8 * n  # the mask matters
+    cfg = O.make_config(buffer="T1", lr=lr, lam=lam, bound_type=1, bound_ratio=ratio, eps=eps, ema_decay=0.8,
+                        weight_decay=0.0)
+    import contextlib
+
+    ctx = O.radial_sum_f64() if f64_sums else contextlib.nullcontext()
+    tol = 1e-6 if f64_sums else (n // 16 + 1) * 2.0 ** -24
+    with ctx:
+        # step 1: two passes, scale from this step's norms
+        p, m, sc = p0.copy(), m0.copy(), np.array([0, 0, 0, 1, 1, 0], np.float32)
+        O.step(cfg, [p], [g], [m], [None], [None], [sc], [1], [0])
+        cs = 1.0 / min(max(count / n, 0.5), 1.0)
+        want = _t1_radial_target(u_sq, p_sq, cs, lr, ratio)
+        assert 0.05 < want < 0.95
+        assert abs(sc[4] - want) <= tol * want, (sc[4], want)
+        assert sc[3] == np.float32(cs) or abs(sc[3] - cs) <= 1e-6 * cs
+        # step 2 from the same inputs: fused pass with lagged scales, EMA of both
+        p, m, sc = p0.copy(), m0.copy(), np.array([0, 0, 0, 1.25, 0.8, 0], np.float32)
+        O.step(cfg, [p], [g], [m], [None], [None], [sc], [2], [0])
+        cs_new = 0.8 * 1.25 + 0.2 * cs
+        want2 = 0.8 * 0.8 + 0.2 * _t1_radial_target(u_sq, p_sq, cs_new, lr, ratio)
+        assert abs(sc[3] - cs_new) <= 1e-6 * cs_new
+        assert abs(sc[4] - want2) <= tol * want2, (sc[4], want2)
+        assert sc[0] == sc[1] == sc[2] == sc[5] == 0.0
+
+
+def test_radial_sum_modes_agree_to_f32_summation_error(oracle_mod):
+    """The f64 sum mode (what the HIP kernels compute) and the scalar core's f32 lane order give
+    the same bound scale up to the f32 summation bound (131,072 sequential adds per lane in a
+    2,097,152-element chunk, then the chunk fold: gamma = 131,074 x 2^-24 = 7.8e-3), on a tensor
+    spanning two chunks; m and v never see the scale and stay bitwise equal."""
+    O = oracle_mod
+    n = 2097152 + 777_777
+    rng = np.random.default_rng(22)
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    cfg = O.make_config(buffer="T2", lr=3e-3, bound_type=1)
+    res = []
+    for mode in (0, 1):
+        O.lib().lvo_set_radial_sum_mode(mode)
+        try:
+            p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+            sc = np.array([0, 0, 0, 1, 1, 0], np.float32)
+            O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=4)
+            res.append((sc.copy(), p, m, v))
+        finally:
+            O.lib().lvo_set_radial_sum_mode(0)
+    (s0, p_a, m_a, v_a), (s1, p_b, m_b, v_b) = res
+    assert np.array_equal(m_a, m_b) and np.array_equal(v_a, v_b)  # the scale never feeds m, v
+    gamma = (2097152 // 16 + 2) * 2.0 ** -24
+    assert abs(s0[4] - s1[4]) <= gamma * s1[4] and s1[4] < 0.999
+    assert np.max(np.abs(p_a - p_b)) <= 1.5e-6  # differential_parity.rs:16 TOLERANCE
+
+
 def test_radial_scale_properties(oracle_mod):
     L = oracle_mod.lib()
     assert L.lvo_radial_scale(1e-12, 1.0, 1.0, 1e-3, 0.05) == 1.0  # r < 1e-4
