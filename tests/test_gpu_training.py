@@ -1,0 +1,175 @@
+"""The drop-in optimizer in training loops on the GPU: the reference's own behavioural tests,
+restated for ROCm tensors.
+
+* bit-exact resume after state_dict / torch.save / load_state_dict for fp32 and bf16 models, all
+  four buffer modes and master weights off / semi / full (eval/modules/checkpoint_test.py:12-88),
+  unfused and with fused buckets;
+* fused buckets equal unfused tensors with cautious and stochastic rounding off (the reference
+  asserts allclose, test_end_to_end_training.py:339-395; here the bits are equal), and zero_grad
+  keeps the grad views into the bucket;
+* small bucket caps split into several buckets and still track the unfused run
+  (test_end_to_end_training.py:437-462);
+* tied weights are stepped once and a grad=None parameter inside a bucket is left untouched
+  (test_end_to_end_training.py:464-482).
+"""
+from __future__ import annotations
+
+import copy
+import io
+
+import pytest
+import torch
+import torch.nn as nn
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+
+
+def _model(dtype):
+    return nn.Sequential(nn.Linear(10, 20), nn.ReLU(), nn.Linear(20, 2)).to(dtype=dtype, device="cuda")
+
+
+@pytest.mark.parametrize("fuse", [False, True], ids=["unfused", "fused"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_checkpoint_bit_exact_resume(dtype, fuse):
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+    from luminamoon_amd.optimizer.constants import TEMP_STATE_DICT_KEYS
+
+    torch.manual_seed(42)
+    for buf in (1, 2, "T1", "T2"):
+        for mw in (False, "semi", "full"):
+            print(f"[case] resume dtype={dtype} buffer={buf} master={mw} fuse={fuse}", flush=True)
+            model_cont = _model(dtype)
+            model_res = copy.deepcopy(model_cont)
+            kw = dict(lr=1e-3, buffer=buf, bound=True, master_weights=mw, fuse_tensors=fuse)
+            opt_cont = LuminaV(model_cont.parameters(), **kw)
+            opt_res = LuminaV(model_res.parameters(), **kw)
+            batches = [(torch.randn(4, 10, dtype=dtype, device="cuda"), torch.tensor([0, 1, 0, 1], device="cuda"))
+                       for _ in range(6)]
+            for i in range(5):
+                x, y = batches[i]
+                for m, opt in ((model_cont, opt_cont), (model_res, opt_res)):
+                    loss = nn.CrossEntropyLoss()(m(x).float(), y)
+                    opt.zero_grad()
+                    loss.backward()
+                    opt.step()
+            buf_io = io.BytesIO()
+            torch.save(opt_res.state_dict(), buf_io)
+            buf_io.seek(0)
+            opt_loaded = LuminaV(model_res.parameters(), **kw)
+            loaded = torch.load(buf_io, weights_only=True)
+            opt_loaded.load_state_dict(loaded)
+            for st in loaded["state"].values():
+                assert not (set(st) & set(TEMP_STATE_DICT_KEYS))
+                sc = st["scratch"]
+                assert float(sc[0]) == float(sc[1]) == float(sc[2]) == float(sc[5]) == 0.0
+            for p in model_res.parameters():
+                st = opt_loaded.state[p]
+                assert st["scratch"].dtype == torch.float32
+                if "master_param" in st:
+                    assert st["master_param"].dtype == torch.float32
+            x, y = batches[5]
+            for m, opt in ((model_cont, opt_cont), (model_res, opt_loaded)):
+                loss = nn.CrossEntropyLoss()(m(x).float(), y)
+                opt.zero_grad()
+                loss.backward()
+                opt.step()
+            torch.cuda.synchronize()
+            for p_c, p_r in zip(model_cont.parameters(), model_res.parameters()):
+                assert torch.equal(p_c.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                                   p_r.view(torch.int16 if dtype == torch.bfloat16 else torch.int32)), (buf, mw)
+            for p_c, p_r in zip(model_cont.parameters(), model_res.parameters()):
+                assert torch.equal(opt_cont.state[p_c]["exp_avg"], opt_loaded.state[p_r]["exp_avg"]), (buf, mw)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("buf", [1, 2, "T1", "T2"])
+def test_fused_bucket_equals_unfused_without_cautious_and_sr(buf, dt):
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    torch.manual_seed(100)
+    shapes = [(16, 8), (16,), (32, 16), (32,), (8, 32)]
+    pu_list = [nn.Parameter(torch.randn(s, dtype=dt, device="cuda")) for s in shapes]
+    pf_list = [nn.Parameter(p.detach().clone()) for p in pu_list]
+    kw = dict(lr=2e-3, buffer=buf, cautious=False, bound=True, bound_type="coordinate", stochastic_rounding=False)
+    opt_u = LuminaV(pu_list, fuse_tensors=False, **kw)
+    opt_f = LuminaV(pf_list, fuse_tensors=True, **kw)
+    assert len(opt_f._fused_buckets) == 1
+    bucket = opt_f._fused_buckets[0]
+    assert bucket["flat_p"].numel() == sum(p.numel() for p in pf_list)
+    opt_f.zero_grad(set_to_none=True)
+    for p, _, g_slice, _, g_ptr, _, _ in bucket["slices"]:
+        assert p.grad is g_slice and p.grad.data_ptr() == g_ptr
+    for _ in range(4):
+        opt_u.zero_grad(set_to_none=True)
+        opt_f.zero_grad(set_to_none=True)
+        for pu, pf in zip(pu_list, pf_list):
+            g = torch.randn_like(pu) * 0.05
+            pu.grad = g.clone()
+            pf.grad.copy_(g)
+        opt_u.step()
+        opt_f.step()
+    torch.cuda.synchronize()
+    iv = torch.int32 if dt == torch.float32 else torch.int16
+    for pu, pf in zip(pu_list, pf_list):
+        assert torch.equal(pu.detach().view(iv), pf.detach().view(iv)), f"buffer={buf} dtype={dt}"
+
+
+def test_small_bucket_cap_splits_and_tracks_unfused():
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    torch.manual_seed(7)
+    shapes = [(32, 16), (16,), (64, 32), (32,), (128, 64)]
+    pu_list = [nn.Parameter(torch.randn(s, device="cuda")) for s in shapes]
+    pc_list = [nn.Parameter(p.detach().clone()) for p in pu_list]
+    opt_u = LuminaV(pu_list, lr=1e-3, buffer=1, fuse_tensors=False)
+    opt_c = LuminaV(pc_list, lr=1e-3, buffer=1, fuse_tensors=True, bucket_cap_mb=0.004)
+    assert len(opt_c._fused_buckets) >= 2
+    for _ in range(5):
+        opt_u.zero_grad(set_to_none=True)
+        opt_c.zero_grad(set_to_none=True)
+        for pu, pc in zip(pu_list, pc_list):
+            g = torch.randn_like(pu) * 0.01
+            pu.grad = g.clone()
+            pc.grad.copy_(g)
+        opt_u.step()
+        opt_c.step()
+    torch.cuda.synchronize()
+    for pu, pc in zip(pu_list, pc_list):
+        # per-bucket vs per-tensor cautious scale: close, not equal (the reference's own tolerance)
+        assert torch.allclose(pu, pc, atol=1e-5, rtol=1e-4)
+    sd = opt_c.state_dict()
+    reload = [nn.Parameter(p.detach().clone()) for p in pc_list]
+    opt_r = LuminaV(reload, lr=1e-3, buffer=1, fuse_tensors=True, bucket_cap_mb=0.004)
+    opt_r.load_state_dict(sd)
+    assert len(opt_r._fused_buckets) == len(opt_c._fused_buckets)
+
+
+def test_tied_weights_and_grad_none_isolation_in_bucket():
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    p_shared = nn.Parameter(torch.ones(16, device="cuda"))
+    p_frozen = nn.Parameter(torch.full((16,), 2.0, device="cuda"))
+    p_active = nn.Parameter(torch.full((16,), 3.0, device="cuda"))
+    opt = LuminaV([p_shared, p_shared, p_frozen, p_active], lr=1e-2, weight_decay=0.1, buffer=2, fuse_tensors=True)
+    assert len(opt._fused_buckets[0]["slices"]) == 3
+    p_shared.grad = torch.ones_like(p_shared) * 0.5
+    p_frozen.grad = None
+    p_active.grad = torch.ones_like(p_active) * 0.5
+    for _ in range(3):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(p_frozen, torch.full((16,), 2.0, device="cuda")), "grad=None param was mutated"
+    assert opt.state[p_frozen]["step"] == 0
+    assert opt.state[p_active]["step"] == 3
+    assert not torch.equal(p_active, torch.full((16,), 3.0, device="cuda"))
+    m_frozen = opt.state[p_frozen]["exp_avg"]
+    assert torch.count_nonzero(m_frozen) == 0
