@@ -39,8 +39,9 @@
 namespace lv {
 
 constexpr int kThreads = 256;
-constexpr int kVec = 8;
-constexpr uint32_t kUnit = kThreads * kVec;  // elements per work unit
+constexpr uint32_t kHalf = kThreads * 4;     // a thread owns 4 consecutive elements of each half
+constexpr int kUnitHalves = 1;               // halves per work unit of a unit launch (1024 elements)
+constexpr int kPersistHalves = 2;            // halves per work unit of a persistent launch (2048)
 constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
 constexpr uint32_t kRadialMaxBlocks = 2048;  // grid cap of radial launches (workspace partial slots)
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
@@ -359,11 +360,11 @@ __device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i)
     return load1<LV_DTYPE_F16>(base, i);
 }
 
-// One thread's 8 elements as raw vectors, kept undecoded while the loads are in flight.
+// One thread's 4 or 8 elements as raw vectors, kept undecoded while the loads are in flight.
 // Vector-path loads and stores are non-temporal: the step streams every byte exactly once, so
 // nothing is worth keeping in L2 or the MALL, and streaming hints measurably raise HBM
 // throughput for this 4-read/3-write pattern.
-// Layout of a 2048-element work unit: thread t owns elements [4t, 4t+4) of each 1024-element
+// Layout of a work unit of H 1024-element halves: thread t owns elements [4t, 4t+4) of each
 // half, so every wave-wide load or store instruction covers one contiguous span (1 KiB for
 // f32, 512 B for 16-bit types). 32-bit types use `a` (first half) and `b` (second half);
 // 16-bit types pack both halves into `a` (.xy first half, .zw second half).
@@ -375,42 +376,45 @@ struct Raw8 {
     u32x4 a, b;
 };
 
-constexpr uint32_t kHalf = kUnit / 2;
-
-template <int DT>
+// H (1 or 2) is the number of 1024-element halves in the unit: a thread moves 4 * H elements.
+template <int DT, int H>
 __device__ __forceinline__ Raw8 load_raw(const void *base, uint64_t h0) {
     Raw8 r;
     if constexpr (DT == LV_DTYPE_F32) {
         const float *f = static_cast<const float *>(base);
         r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0));
-        r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + kHalf));
+        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + kHalf));
+        else r.b = u32x4{0, 0, 0, 0};
     } else {
         const uint16_t *h = static_cast<const uint16_t *>(base);
         u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
-        u32x2 y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + kHalf));
+        u32x2 y = u32x2{0, 0};
+        if constexpr (H == 2) y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + kHalf));
         r.a = u32x4{x.x, x.y, y.x, y.y};
         r.b = u32x4{0, 0, 0, 0};
     }
     return r;
 }
 
+template <int H>
 __device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t h0) {
-    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32>(base, h0);
-    return load_raw<LV_DTYPE_BF16>(base, h0);  // 16-bit types share the raw layout
+    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32, H>(base, h0);
+    return load_raw<LV_DTYPE_BF16, H>(base, h0);  // 16-bit types share the raw layout
 }
 
-// Stores 8 values in the same two-half layout; 16-bit values are already exact in the target
+// Stores 4 * H values in the same layout; 16-bit values are already exact in the target
 // type (quantised), so bf16 is a truncation (worker.rs:55-63) and f16 an exact RNE encode.
-template <int DT>
+template <int DT, int H>
 __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
     if constexpr (DT == LV_DTYPE_F32) {
         float *f = static_cast<float *>(base);
         __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4 *>(f + h0));
-        __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + kHalf));
+        if constexpr (H == 2)
+            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + kHalf));
     } else {
         uint32_t ws[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 2 * H; k++) {
             uint32_t lo, hi;
             if constexpr (DT == LV_DTYPE_BF16) {
                 lo = f_bits(in[2 * k]) >> 16;
@@ -423,19 +427,21 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
         }
         uint16_t *h = static_cast<uint16_t *>(base);
         __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
-        __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + kHalf));
+        if constexpr (H == 2) __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + kHalf));
     }
 }
 
-template <int DT>
+template <int DT, int H>
 __device__ __forceinline__ void decode_raw(const Raw8 &r, float out[8]) {
     if constexpr (DT == LV_DTYPE_F32) {
         out[0] = bits_f(r.a.x); out[1] = bits_f(r.a.y); out[2] = bits_f(r.a.z); out[3] = bits_f(r.a.w);
-        out[4] = bits_f(r.b.x); out[5] = bits_f(r.b.y); out[6] = bits_f(r.b.z); out[7] = bits_f(r.b.w);
+        if constexpr (H == 2) {
+            out[4] = bits_f(r.b.x); out[5] = bits_f(r.b.y); out[6] = bits_f(r.b.z); out[7] = bits_f(r.b.w);
+        }
     } else {
         uint32_t ws[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 2 * H; k++) {
             if constexpr (DT == LV_DTYPE_BF16) {
                 out[2 * k] = bits_f(ws[k] << 16);
                 out[2 * k + 1] = bits_f(ws[k] & 0xFFFF0000u);
@@ -447,10 +453,11 @@ __device__ __forceinline__ void decode_raw(const Raw8 &r, float out[8]) {
     }
 }
 
+template <int H>
 __device__ __forceinline__ void decode_raw_dyn(int dt, const Raw8 &r, float out[8]) {
-    if (dt == LV_DTYPE_BF16) decode_raw<LV_DTYPE_BF16>(r, out);
-    else if (dt == LV_DTYPE_F32) decode_raw<LV_DTYPE_F32>(r, out);
-    else decode_raw<LV_DTYPE_F16>(r, out);
+    if (dt == LV_DTYPE_BF16) decode_raw<LV_DTYPE_BF16, H>(r, out);
+    else if (dt == LV_DTYPE_F32) decode_raw<LV_DTYPE_F32, H>(r, out);
+    else decode_raw<LV_DTYPE_F16, H>(r, out);
 }
 
 // The loads of one work unit that are in flight while the previous unit computes.
@@ -686,43 +693,43 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
 }
 
 // Vector loads of one whole, aligned unit.
-template <int MODE, int PT, int ST, int PASS>
+template <int MODE, int PT, int ST, int PASS, int H>
 __device__ __forceinline__ Inflight issue_unit(const Desc &D, const View &tv, uint32_t flags, bool radial, uint32_t u) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     const int gdt = (int)((flags >> 8) & 3u);
     Inflight f;
-    const uint64_t e = (uint64_t)(u - tv.t_begin) * kUnit + (uint64_t)threadIdx.x * 4u;
-    f.g = load_raw_dyn(gdt, D.g, e);
-    f.m = load_raw<ST>(D.m, e);
-    if constexpr (kDual) f.v = load_raw<ST>(D.v, e);
+    const uint64_t e = (uint64_t)(u - tv.t_begin) * (kHalf * H) + (uint64_t)threadIdx.x * 4u;
+    f.g = load_raw_dyn<H>(gdt, D.g, e);
+    f.m = load_raw<ST, H>(D.m, e);
+    if constexpr (kDual) f.v = load_raw<ST, H>(D.v, e);
     if (PASS != kCount || radial) {  // the count pass reads p only for the radial norm
-        if (flags & kFMaster) f.mp = load_raw<LV_DTYPE_F32>(D.mp, e);
-        else f.p = load_raw<PT>(D.p, e);
+        if (flags & kFMaster) f.mp = load_raw<LV_DTYPE_F32, H>(D.mp, e);
+        else f.p = load_raw<PT, H>(D.p, e);
     }
     return f;
 }
 
 // Update (or count) one whole, aligned unit from its loaded vectors and store it.
-template <int MODE, int PT, int ST, int PASS>
+template <int MODE, int PT, int ST, int PASS, int H>
 __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
                                              const Inflight &cur, uint32_t u, uint32_t &cnt, double &su, double &sp) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
     const int gdt = (int)((flags >> 8) & 3u);
     const bool master = flags & kFMaster;
-    const uint64_t e0 = (uint64_t)(u - tv.t_begin) * kUnit + (uint64_t)threadIdx.x * 4u;
+    const uint64_t e0 = (uint64_t)(u - tv.t_begin) * (kHalf * H) + (uint64_t)threadIdx.x * 4u;
     float g[8], m[8], v[8];
-    decode_raw_dyn(gdt, cur.g, g);
-    decode_raw<ST>(cur.m, m);
-    if constexpr (kDual) decode_raw<ST>(cur.v, v);
+    decode_raw_dyn<H>(gdt, cur.g, g);
+    decode_raw<ST, H>(cur.m, m);
+    if constexpr (kDual) decode_raw<ST, H>(cur.v, v);
     if constexpr (PASS == kCount) {
         float pin[8];
         if (radial) {
-            if (master) decode_raw<LV_DTYPE_F32>(cur.mp, pin);
-            else decode_raw<PT>(cur.p, pin);
+            if (master) decode_raw<LV_DTYPE_F32, H>(cur.mp, pin);
+            else decode_raw<PT, H>(cur.p, pin);
         }
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < 4 * H; j++) {
             float ue;
             cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
             if (radial) {
@@ -732,10 +739,10 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
         }
     } else {
         float pin[8], pout[8], mpout[8];
-        if (master) decode_raw<LV_DTYPE_F32>(cur.mp, pin);
-        else decode_raw<PT>(cur.p, pin);
+        if (master) decode_raw<LV_DTYPE_F32, H>(cur.mp, pin);
+        else decode_raw<PT, H>(cur.p, pin);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
             float ue;
             const uint64_t ej = e0 + (j < 4 ? (uint64_t)j : (uint64_t)(kHalf + j - 4));
@@ -750,23 +757,24 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
                 }
             }
         }
-        store_raw<PT>(D.p, e0, pout);
-        if (master) store_raw<LV_DTYPE_F32>(D.mp, e0, mpout);
-        store_raw<ST>(D.m, e0, m);
-        if constexpr (kDual) store_raw<ST>(D.v, e0, v);
+        store_raw<PT, H>(D.p, e0, pout);
+        if (master) store_raw<LV_DTYPE_F32, H>(D.mp, e0, mpout);
+        store_raw<ST, H>(D.m, e0, m);
+        if constexpr (kDual) store_raw<ST, H>(D.v, e0, v);
     }
 }
 
 // Per-element path for one unit: the partial last unit of a tensor and unaligned tensors.
-template <int MODE, int PT, int ST, int PASS>
+template <int MODE, int PT, int ST, int PASS, int H>
 __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
                                             uint32_t u, uint32_t &cnt, double &su, double &sp) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    constexpr uint64_t kPer = 4 * H;  // consecutive elements per thread
     const int gdt = (int)((flags >> 8) & 3u);
     const bool master = flags & kFMaster;
-    const uint64_t e0 = (uint64_t)(u - tv.t_begin) * kUnit + (uint64_t)threadIdx.x * kVec;
-    const uint64_t e1 = (e0 + kVec < tv.n) ? e0 + kVec : tv.n;
+    const uint64_t e0 = (uint64_t)(u - tv.t_begin) * (kHalf * H) + (uint64_t)threadIdx.x * kPer;
+    const uint64_t e1 = (e0 + kPer < tv.n) ? e0 + kPer : tv.n;
     for (uint64_t i = e0; i < e1; i++) {
         float g = load1_dyn(gdt, D.g, i);
         float m = load1<ST>(D.m, i);
@@ -812,13 +820,14 @@ __device__ __forceinline__ int find_tensor(const Args &a, int lo, uint32_t unit)
 
 // ------------------------------------------------------------------ the kernels
 
-// Unit launch: block b updates exactly one 2048-element work unit (unit_base + b) and exits.
+// Unit launch: each block updates exactly one 1024-element work unit and exits.
 // The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
 // arithmetic of others without a software pipeline; on MI355X this launch shape streams HBM
-// faster than any persistent grid-stride loop over the same buffers (measured: 23.8 vs 26.5 ms
-// for the 6.7e9-element T2 step). Counting passes add each block's exact mask count into one of
-// the tensor's kSlots u64 slots (relaxed integer atomics: exact in any order, no fence per
-// block); finalize_kernel folds the slots after the launch. Never used for radial counting.
+// faster than any persistent grid-stride loop over the same buffers (measured: 23.4 vs 26.5 ms
+// for the 6.7e9-element T2 step; 2048-element units: 23.7 ms). Counting passes add each block's
+// exact mask count into one of the tensor's kSlots u64 slots (relaxed integer atomics: exact in
+// any order, no fence per block); finalize_kernel folds the slots after the launch. Never used
+// for radial counting.
 // FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
 // which case every option test folds at compile time and the per-element code is straight-line.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL>
@@ -837,11 +846,12 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const View tv = open_view<MODE, PASS>(a, D, t, flags, unit);
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // unused: radial sums run in step_kernel
-    if (tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / kUnit)) {
-        const Inflight f = issue_unit<MODE, PT, ST, PASS>(D, tv, flags, false, unit);
-        process_unit<MODE, PT, ST, PASS>(a, D, tv, flags, false, f, unit, cnt, su, sp);
+    constexpr int H = kUnitHalves;
+    if (tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
+        const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, false, unit);
+        process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, f, unit, cnt, su, sp);
     } else {
-        scalar_unit<MODE, PT, ST, PASS>(a, D, tv, flags, false, unit, cnt, su, sp);
+        scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, unit, cnt, su, sp);
     }
     if constexpr (kCounting) {
 #pragma unroll
@@ -916,24 +926,25 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
         // ---- whole, aligned units: software-pipelined vector path. The loads of the next
         // unit are issued before the current unit is computed, so a wave always has one unit
         // of HBM traffic in flight while it computes.
-        const uint32_t full_end = tv.vec_ok ? tv.t_begin + (uint32_t)(tv.n / kUnit) : tv.t_begin;
+        constexpr int H = kPersistHalves;
+        const uint32_t full_end = tv.vec_ok ? tv.t_begin + (uint32_t)(tv.n / (kHalf * H)) : tv.t_begin;
         if (unit < full_end) {
             // Two register buffers in ping-pong. The prefetch is unconditional (the last one of
             // a run re-reads the current unit, in bounds and unused) so the wait counts are the
             // same on every path and the compiler never has to drain the prefetch early.
-            Inflight A = issue_unit<MODE, PT, ST, PASS>(D, tv, flags, radial, unit);
+            Inflight A = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, unit);
             for (;;) {
                 uint32_t next = unit + stride;
                 bool more = next < full_end;
-                Inflight B = issue_unit<MODE, PT, ST, PASS>(D, tv, flags, radial, more ? next : unit);
-                process_unit<MODE, PT, ST, PASS>(a, D, tv, flags, radial, A, unit, cnt, su, sp);
+                Inflight B = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, more ? next : unit);
+                process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, A, unit, cnt, su, sp);
                 units_here++;
                 unit = next;
                 if (!more) break;
                 next = unit + stride;
                 more = next < full_end;
-                A = issue_unit<MODE, PT, ST, PASS>(D, tv, flags, radial, more ? next : unit);
-                process_unit<MODE, PT, ST, PASS>(a, D, tv, flags, radial, B, unit, cnt, su, sp);
+                A = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, more ? next : unit);
+                process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, B, unit, cnt, su, sp);
                 units_here++;
                 unit = next;
                 if (!more) break;
@@ -942,7 +953,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
 
         // ---- the partial last unit and unaligned tensors: per-element path
         for (; unit < tv.t_end; unit += stride) {
-            scalar_unit<MODE, PT, ST, PASS>(a, D, tv, flags, radial, unit, cnt, su, sp);
+            scalar_unit<MODE, PT, ST, PASS, kPersistHalves>(a, D, tv, flags, radial, unit, cnt, su, sp);
             units_here++;
         }
     }
@@ -1154,11 +1165,26 @@ static int launch_one(KernelFn fn, const Args &args, uint32_t grid, uint32_t thr
     return LV_STATUS_SUCCESS;
 }
 
+// Gives the tensors of a launch consecutive ranges of units of `unit_elems` elements.
+static int assign_units(Args &args, uint32_t unit_elems) {
+    uint64_t units = 0;
+    for (int k = 0; k < args.ndesc; k++) {
+        args.d[k].unit_begin = (uint32_t)units;
+        units += (args.d[k].n + unit_elems - 1) / unit_elems;
+        if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
+    }
+    args.total_units = (uint32_t)units;
+    return LV_STATUS_SUCCESS;
+}
+
 static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
-    if (args.total_units == 0) return LV_STATUS_SUCCESS;
     KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags);
     const bool counting = pass == kFused || pass == kCount;
-    if (counting && (args.flags & kFRadial)) {
+    const bool persistent = counting && (args.flags & kFRadial);
+    int rc = assign_units(args, kHalf * (persistent ? kPersistHalves : kUnitHalves));
+    if (rc != LV_STATUS_SUCCESS) return rc;
+    if (args.total_units == 0) return LV_STATUS_SUCCESS;
+    if (persistent) {
         // persistent: at most kRadialMaxBlocks blocks (the partial slots per tensor)
         uint32_t grid = std::min<uint32_t>(args.total_units, resident_blocks(fn));
         grid = std::min<uint32_t>(grid, kRadialMaxBlocks);
@@ -1169,7 +1195,7 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
     args.xcds = device_xcds();
     for (uint32_t ub = 0; ub < args.total_units; ub += std::min<uint32_t>(kMaxGrid, args.total_units - ub)) {
         args.unit_base = ub;
-        int rc = launch_one(fn, args, std::min<uint32_t>(kMaxGrid, args.total_units - ub), kThreads, stream);
+        rc = launch_one(fn, args, std::min<uint32_t>(kMaxGrid, args.total_units - ub), kThreads, stream);
         if (rc != LV_STATUS_SUCCESS) return rc;
     }
     args.unit_base = 0;
@@ -1233,7 +1259,7 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             T.state_dtype > 2)
             return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: invalid dtype code", i);
         if (T.step == 0) return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: step must be >= 1", i);
-        if (T.numel > (uint64_t)0xFFFFFFFFull * kUnit)
+        if (T.numel > (uint64_t)0xFFFFFFFFull * kHalf)
             return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many elements", i);
         // worker.rs:95-98 and worker.rs:153-156: an fp32 param aliasing its master has none.
         bool mp_present = T.master_param && !(T.param_dtype == LV_DTYPE_F32 && (void *)T.master_param == T.param);
@@ -1313,7 +1339,6 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
         if (bound == LV_BOUND_RADIAL) flags |= kFRadial;
         flags |= (uint32_t)h.gt << 8;
         args.flags = flags;
-        uint64_t units = 0;
         args.ndesc = (int32_t)(end - begin);
         for (size_t k = begin; k < end; k++) {
             const lv_tensor &T = tensors[items[k].idx];
@@ -1325,13 +1350,10 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             D.mp = items[k].master ? T.master_param : nullptr;
             D.scratch = T.scratch;
             D.n = T.numel;
-            D.unit_begin = (uint32_t)units;
+            D.unit_begin = 0;  // set per launch (the unit size depends on the launch shape)
             D.pidx = (uint32_t)T.param_index;
             D.ibase = (uint32_t)T.index_base;
-            units += (T.numel + kUnit - 1) / kUnit;
         }
-        if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
-        args.total_units = (uint32_t)units;
         args.counters = ctr + 2 * begin;  // slots [begin, end) of this call's workspace
         args.slots = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace) + counter_bytes(count));
         args.partials = reinterpret_cast<double *>(static_cast<char *>(workspace) + counter_bytes(count) + kSlotBytes);
