@@ -80,6 +80,15 @@ typedef struct lv_tensor {
      * (the reference's `idx as i32`, reference_cpu/dual.rs:54); a shard of a larger tensor passes
      * its global start so its bits equal the unsharded step. */
     uint64_t index_base;
+    /* Optional inactive element ranges: `inactive` points to 2 x n_inactive uint64 values in
+     * device memory, sorted and disjoint [begin, end) pairs of element indices of this tensor.
+     * Their elements count in the cautious / radial statistics as if their gradient were zero,
+     * but are never written (param, state and master keep their values) and their grad is not
+     * read. This is the reference's grad=None slice of a fused bucket -- zero the grad slice,
+     * step the whole bucket, restore the slice (python/luminamoon/optimizer/luminav.py:1466-1531,
+     * luminav.py:1585-1603) -- without the copies. NULL / 0: every element is active. */
+    const uint64_t *inactive;
+    uint64_t n_inactive;
 } lv_tensor;
 
 /* Library version, major*10000 + minor*100 + patch. */

@@ -61,7 +61,7 @@ enum Flags : uint32_t {
     kFCoordinate = 1u << 6,
 };
 
-// One tensor of a launch (72 bytes, lives in the kernel argument segment).
+// One tensor of a launch (80 bytes, lives in the kernel argument segment).
 struct Desc {
     void *p;
     const void *g;
@@ -73,7 +73,8 @@ struct Desc {
     uint32_t unit_begin;  // first work unit of this tensor in the launch's unit space
     uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
     uint32_t ibase;       // low 32 bits of index_base (the SR offset is taken mod 2^32)
-    uint32_t pad;
+    uint32_t nskip;       // inactive [begin, end) ranges in `skip` (sorted, disjoint)
+    const uint64_t *skip;
 };
 
 // Launch-uniform constants: hyper-parameters, per-step coefficients, tensor table.
@@ -91,6 +92,9 @@ struct Args {
     double *partials;              // radial: [tensor][block] pairs (sum u_eff^2, sum p^2)
     Desc d[kMaxDesc];
 };
+
+static_assert(sizeof(Desc) == 80, "descriptor layout");
+static_assert(sizeof(Args) <= 4096, "kernel arguments must fit in 4 KiB");
 
 // ------------------------------------------------------------------ device math
 
@@ -765,9 +769,13 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
 }
 
 // Per-element path for one unit: the partial last unit of a tensor and unaligned tensors.
+// nskip > 0: the unit overlaps the tensor's inactive ranges, `first` is the first range that ends
+// after the unit's first element. Inactive elements are computed with a zero gradient (they count
+// in the statistics) and not stored.
 template <int MODE, int PT, int ST, int PASS, int H>
 __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
-                                            uint32_t u, uint32_t &cnt, double &su, double &sp) {
+                                            uint32_t u, uint32_t &cnt, double &su, double &sp, uint32_t nskip = 0,
+                                            uint32_t first = 0) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
     constexpr uint64_t kPer = 4 * H;  // consecutive elements per thread
@@ -775,8 +783,14 @@ __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const 
     const bool master = flags & kFMaster;
     const uint64_t e0 = (uint64_t)(u - tv.t_begin) * (kHalf * H) + (uint64_t)threadIdx.x * kPer;
     const uint64_t e1 = (e0 + kPer < tv.n) ? e0 + kPer : tv.n;
+    uint32_t r = first;
     for (uint64_t i = e0; i < e1; i++) {
-        float g = load1_dyn(gdt, D.g, i);
+        bool inactive = false;
+        if (nskip) {
+            while (r < nskip && D.skip[2 * r + 1] <= i) r++;
+            inactive = r < nskip && D.skip[2 * r] <= i;
+        }
+        float g = inactive ? 0.0f : load1_dyn(gdt, D.g, i);
         float m = load1<ST>(D.m, i);
         float v = kDual ? load1<ST>(D.v, i) : 0.0f;
         if constexpr (PASS == kCount) {
@@ -792,10 +806,12 @@ __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const 
             float pout, mpout, ue;
             uint32_t act = apply_elem<MODE, PT, ST>(a, flags, tv.sd, (int32_t)((uint32_t)i + tv.ibase), tv.cs, tv.bs, pin,
                                                     g, m, v, pout, mpout, ue);
-            store1<PT>(D.p, i, pout);
-            if (master) D.mp[i] = mpout;
-            store1<ST>(D.m, i, m);
-            if constexpr (kDual) store1<ST>(D.v, i, v);
+            if (!inactive) {
+                store1<PT>(D.p, i, pout);
+                if (master) D.mp[i] = mpout;
+                store1<ST>(D.m, i, m);
+                if constexpr (kDual) store1<ST>(D.v, i, v);
+            }
             if constexpr (kCounting) {
                 cnt += act;
                 if (radial) {
@@ -805,6 +821,22 @@ __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const 
             }
         }
     }
+}
+
+// How the tensor's inactive ranges cover the elements [e0, e1): 0 not at all, 1 partly, 2 fully.
+// `first` receives the first range that ends after e0. Block-uniform.
+__device__ __forceinline__ int inactive_cover(const Desc &D, uint64_t e0, uint64_t e1, uint32_t &first) {
+    uint32_t lo = 0, hi = D.nskip;
+    while (lo < hi) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (D.skip[2 * mid + 1] <= e0) lo = mid + 1;
+        else hi = mid;
+    }
+    first = lo;
+    if (lo == D.nskip) return 0;
+    const uint64_t b = D.skip[2 * lo], e = D.skip[2 * lo + 1];
+    if (b >= e1) return 0;
+    return (b <= e0 && e >= e1) ? 2 : 1;
 }
 
 // Index of the tensor that owns `unit`: binary search of the unit ranges, right of `lo`.
@@ -847,14 +879,22 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // unused: radial sums run in step_kernel
     constexpr int H = kUnitHalves;
-    if (tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
+    int cover = 0;
+    uint32_t first = 0;
+    if (D.nskip) {
+        const uint64_t e0 = (uint64_t)(unit - tv.t_begin) * (kHalf * H);
+        cover = inactive_cover(D, e0, e0 + kHalf * H < tv.n ? e0 + kHalf * H : tv.n, first);
+        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing.
+        if (cover == 2) return;
+    }
+    if (cover == 0 && tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
         const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, false, unit);
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
         process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, f, unit, cnt, su, sp);
     } else {
-        scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, unit, cnt, su, sp);
+        scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, unit, cnt, su, sp, cover ? D.nskip : 0, first);
     }
     if constexpr (kCounting) {
 #pragma unroll
@@ -930,7 +970,8 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
         // unit are issued before the current unit is computed, so a wave always has one unit
         // of HBM traffic in flight while it computes.
         constexpr int H = kPersistHalves;
-        const uint32_t full_end = tv.vec_ok ? tv.t_begin + (uint32_t)(tv.n / (kHalf * H)) : tv.t_begin;
+        // tensors with inactive ranges take the per-element path (their elements still count)
+        const uint32_t full_end = (tv.vec_ok && D.nskip == 0) ? tv.t_begin + (uint32_t)(tv.n / (kHalf * H)) : tv.t_begin;
         if (unit < full_end) {
             // Two register buffers in ping-pong. The prefetch is unconditional (the last one of
             // a run re-reads the current unit, in bounds and unused) so the wait counts are the
@@ -956,7 +997,14 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
 
         // ---- the partial last unit and unaligned tensors: per-element path
         for (; unit < tv.t_end; unit += stride) {
-            scalar_unit<MODE, PT, ST, PASS, kPersistHalves>(a, D, tv, flags, radial, unit, cnt, su, sp);
+            uint32_t first = 0;
+            int cover = 0;
+            if (D.nskip) {
+                const uint64_t e0 = (uint64_t)(unit - tv.t_begin) * (kHalf * kPersistHalves);
+                cover = inactive_cover(D, e0, e0 + kHalf * kPersistHalves < tv.n ? e0 + kHalf * kPersistHalves : tv.n, first);
+            }
+            scalar_unit<MODE, PT, ST, PASS, kPersistHalves>(a, D, tv, flags, radial, unit, cnt, su, sp,
+                                                            cover ? D.nskip : 0, first);
             units_here++;
         }
     }
@@ -1271,6 +1319,8 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             return fail(LV_STATUS_NULL_POINTER, "tensor %d: Master weight mode requires an initialized master_param buffer", i);
         if (T.grad == T.param || T.grad == T.exp_avg)
             return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: grad aliases mutable state", i);  // mod.rs:310-318
+        if (T.n_inactive && !T.inactive) return fail(LV_STATUS_NULL_POINTER, "tensor %d: inactive ranges pointer is NULL", i);
+        if (T.n_inactive > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many inactive ranges", i);
         Item it;
         it.idx = i;
         it.pt = T.param_dtype;
@@ -1356,6 +1406,8 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             D.unit_begin = 0;  // set per launch (the unit size depends on the launch shape)
             D.pidx = (uint32_t)T.param_index;
             D.ibase = (uint32_t)T.index_base;
+            D.nskip = (uint32_t)T.n_inactive;
+            D.skip = T.n_inactive ? T.inactive : nullptr;
         }
         args.counters = ctr + 2 * begin;  // slots [begin, end) of this call's workspace
         args.slots = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace) + counter_bytes(count));

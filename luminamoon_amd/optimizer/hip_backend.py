@@ -63,6 +63,8 @@ class LvTensor(ctypes.Structure):
         ("state_dtype", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
         ("index_base", ctypes.c_uint64),
+        ("inactive", ctypes.c_void_p),
+        ("n_inactive", ctypes.c_uint64),
     ]
 
 
@@ -153,9 +155,13 @@ class HipStepper:
         steps: Sequence[int],
         param_indices: Sequence[int],
         index_bases: Optional[Sequence[int]] = None,
+        inactive: Optional[Sequence[Optional[torch.Tensor]]] = None,
     ) -> None:
         """index_bases: global element offset of each tensor when it is a shard of a larger
-        tensor (stochastic-rounding offsets continue from there); None = all 0."""
+        tensor (stochastic-rounding offsets continue from there); None = all 0.
+        inactive: per tensor, None or an int64 device tensor of shape [k, 2] holding sorted,
+        disjoint [begin, end) element ranges whose elements count in the statistics with a zero
+        gradient but are not written (a fused bucket's grad=None slices)."""
         n = len(params)
         if n == 0:
             return
@@ -206,10 +212,18 @@ class HipStepper:
                 if mp.device != device or not mp.is_contiguous():
                     raise ValueError(f"LuminaV: master_param of param index {param_indices[i]} must be contiguous on {device}.")
                 mpp = mp.data_ptr()
+            ip, ni = 0, 0
+            rng = inactive[i] if inactive is not None else None
+            if rng is not None and rng.numel() > 0:
+                if rng.dtype != torch.int64 or rng.dim() != 2 or rng.shape[1] != 2 or not rng.is_contiguous():
+                    raise ValueError("LuminaV: inactive ranges must be a contiguous int64 tensor of shape [k, 2].")
+                if rng.device != device:
+                    raise ValueError(f"LuminaV: inactive ranges of param index {param_indices[i]} must be on {device}.")
+                ip, ni = rng.data_ptr(), int(rng.shape[0])
             items[i] = LvTensor(
                 p.data_ptr(), g.data_ptr(), m.data_ptr(), vp, mpp, sc.data_ptr(), numel, int(steps[i]),
                 int(param_indices[i]), DTYPE_CODES[p.dtype], DTYPE_CODES[g.dtype], DTYPE_CODES[m.dtype], 0,
-                int(index_bases[i]) if index_bases is not None else 0,
+                int(index_bases[i]) if index_bases is not None else 0, ip, ni,
             )
         cfg = make_config(group)
         ws = self.workspace.get(device, n)

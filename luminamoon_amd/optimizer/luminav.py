@@ -894,19 +894,20 @@ class LuminaV(Optimizer):
         return loss
 
     def _step_bucket(self, group: Dict[str, Any], b: Dict[str, Any], grads: Optional[Any]) -> None:
-        """One bucket = one tensor with param_index 0 and bucket-global offsets; slices without a
-        grad are stepped with g=0 and restored afterwards (reference luminav.py:1426-1603)."""
+        """One bucket = one tensor with param_index 0 and bucket-global offsets. A slice whose
+        param has no grad stays in the bucket's statistics with a zero gradient and is not
+        written: it goes to the kernel as an inactive element range. The reference zeroes the grad
+        slice, steps the whole bucket and copies the slice's param/state back
+        (luminav.py:1426-1603); the result is the same without the copies."""
         flat_m, flat_v, flat_mp = b["flat_m"], b["flat_v"], b["flat_mp"]
         b["step"] = int(b["step"]) + 1
         step_t = b["step"]
         any_grad = False
-        backups = []
+        inactive: List[Tuple[int, int]] = []  # merged [begin, end) element ranges
         off = 0
         for p, p_sl, g_sl, p_ptr, g_ptr, st, idx in b["slices"]:
             n = int(p.numel())
-            m_sl = flat_m[off:off + n].view(p.shape)
-            v_sl = flat_v[off:off + n].view(p.shape) if flat_v is not None else None
-            mp_sl = flat_mp[off:off + n].view(p.shape) if flat_mp is not None else None
+            begin = off
             off += n
             if p.data_ptr() != p_ptr:
                 p_sl.copy_(p.detach())
@@ -920,10 +921,11 @@ class LuminaV(Optimizer):
             else:
                 g = None
             if g is None:
-                g_sl.zero_()
-                backups.append((p_sl, p_sl.detach().clone(), m_sl, m_sl.detach().clone(), v_sl,
-                                None if v_sl is None else v_sl.detach().clone(), mp_sl,
-                                None if mp_sl is None else mp_sl.detach().clone(), st, int(st.get("step", step_t - 1))))
+                if n > 0:
+                    if inactive and inactive[-1][1] == begin:
+                        inactive[-1] = (inactive[-1][0], begin + n)
+                    else:
+                        inactive.append((begin, begin + n))
                 continue
             any_grad = True
             if getattr(g, "is_sparse", False):
@@ -941,16 +943,15 @@ class LuminaV(Optimizer):
             for *_, st, _ in b["slices"]:
                 st["step"] = int(st.get("step", step_t - 1))
             return
+        table = None
+        if inactive:
+            key = tuple(inactive)
+            if b.get("inactive_key") != key:  # uploaded only when the set of grad=None params changes
+                b["inactive_table"] = torch.tensor(inactive, dtype=torch.int64, device=b["flat_p"].device)
+                b["inactive_key"] = key
+            table = b["inactive_table"]
         self._stepper.step(group, [b["flat_p"]], [b["flat_g"]], [flat_m], [flat_v], [flat_mp], [b["scratch"]],
-                           [step_t], [0])
-        for p_sl, p_bak, m_sl, m_bak, v_sl, v_bak, mp_sl, mp_bak, st, prev in backups:
-            p_sl.copy_(p_bak)
-            m_sl.copy_(m_bak)
-            if v_sl is not None:
-                v_sl.copy_(v_bak)
-            if mp_sl is not None:
-                mp_sl.copy_(mp_bak)
-            st["step"] = prev
+                           [step_t], [0], inactive=[table])
 
     def _step_unfused(self, group: Dict[str, Any], grads: Optional[Any]) -> None:
         buf_count = group["buffer"]

@@ -5,6 +5,8 @@ from __future__ import annotations
 import ctypes
 import os
 import re
+import shutil
+import subprocess
 
 import pytest
 
@@ -46,10 +48,28 @@ def test_version_and_workspace(lib):
     assert lib.lv_workspace_bytes(1) >= 48 * 2048 * 16
 
 
-def test_struct_layouts_match_header():
-    # lv_config: 10 floats + 8 int32 = 72 bytes; lv_tensor: 6 pointers + 3 u64 + 4 i32 + u64 = 96 bytes
-    assert ctypes.sizeof(H.LvConfig) == 72
-    assert ctypes.sizeof(H.LvTensor) == 96
+def _c_layout(struct, fields, tmp_path):
+    """sizeof and offsetof of `struct` as gcc lays out include/luminav_hip.h."""
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "luminav_hip.h"', "int main(void) {",
+             f'  printf("%zu\\n", sizeof({struct}));']
+    lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    return int(out[0]), [int(x) for x in out[1:]]
+
+
+@pytest.mark.parametrize("ctype,cname", [(H.LvConfig, "lv_config"), (H.LvTensor, "lv_tensor")])
+def test_struct_layouts_match_header(ctype, cname, tmp_path):
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    names = [f[0] for f in ctype._fields_]
+    size, offsets = _c_layout(cname, names, tmp_path)
+    assert ctypes.sizeof(ctype) == size
+    assert [getattr(ctype, f).offset for f in names] == offsets
 
 
 def _cfg(**kw):
@@ -93,6 +113,13 @@ def test_host_side_rejections_without_device(lib):
     assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 8, None) == -3
     t.grad = t.param
     assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -3
+    # inactive ranges: a count without a table
+    t.grad = 0x3000
+    t.n_inactive = 2
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
+    assert b"inactive" in lib.lv_last_error()
+    t.n_inactive = 0
+    t.grad = t.param
     # radial: same host checks (the call is never launched here)
     rcfg = _cfg(buffer="T2", bound_type="radial")
     assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, WS, None) == -3
