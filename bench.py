@@ -30,6 +30,14 @@ N5 = 32 * (4 * 4096 * 4096 + 3 * 4096 * 11008 + 2 * 4096) + 2 * 32000 * 4096 + 4
 N4 = 16 * (4 * 2048 * 2048 + 3 * 2048 * 5632 + 2 * 2048) + 2 * 32000 * 2048 + 2048
 N3 = 12 * (768 * 2304 + 768 * 768 + 768 * 3072 + 3072 * 768) + 50 * 768 + 50257 * 768
 
+def cfg2_sizes(count: int = 64, seed: int = 2):
+    """64 ragged tensor sizes, log-uniform in [1, 2^20]: floor(exp(U(0, ln 2^20))) + 1, seeded."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return [int(math.floor(math.exp(rng.uniform(0.0, math.log(2.0 ** 20))))) + 1 for _ in range(count)]
+
+
 # Algorithmic bytes per parameter per steady-state step: every buffer read once, written once.
 #   T2/CLM bf16 p,g + f32 m,v: p 2+2, g 2, m 4+4, v 4+4 = 22
 #   T1/TD-CLM bf16 p,g + f32 m: p 2+2, g 2, m 4+4 = 14
@@ -41,6 +49,8 @@ WORKLOADS = {
             n=N4, buffer="T1", pdt="bf16", cautious=True, bytes_per_param=14, grad="normal"),
     3: dict(name="cfg3: LuminaV buffer=2 cautious, fp32, one 123,570,432-elem bucket (GPT-2 small)",
             n=N3, buffer=2, pdt="f32", cautious=True, bytes_per_param=28, grad="normal"),
+    2: dict(name="cfg2: LuminaV buffer=1 (TD-CLM, lam=0.3) cautious, fp32, 64 ragged unfused tensors",
+            sizes=cfg2_sizes(), buffer=1, pdt="f32", cautious=True, bytes_per_param=20, grad="normal_zeros"),
 }
 
 
@@ -84,6 +94,8 @@ def fill_inputs(torch, n: int, pdt, grad_kind: str, seed: int = 1234):
         z = torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
         p[s:e].copy_(z.mul_(0.02))
         z = torch.randn(k, generator=gen, device="cuda", dtype=torch.float32)
+        if grad_kind == "normal_zeros":  # 5% exact zeros
+            z.masked_fill_(torch.rand(k, generator=gen, device="cuda") < 0.05, 0.0)
         if grad_kind == "student_t3":
             chi2 = torch.zeros(k, device="cuda", dtype=torch.float32)
             for _ in range(3):
@@ -133,14 +145,35 @@ def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
     cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"])
     dual = workload["buffer"] in (2, "T2")
 
-    def make(n):
-        rng = np.random.default_rng(5)
+    def make(n, seed=5):
+        rng = np.random.default_rng(seed)
         p = torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)).to(pdt)
         g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(pdt)
         m = torch.zeros(n)
         v = torch.zeros(n) if dual else None
         sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
         return p, g, m, v, sc
+
+    if "sizes" in workload:
+        # a multi-tensor workload small enough to time whole: every tensor, one call per step
+        sizes = workload["sizes"]
+        k = len(sizes)
+        P, G, M, V, S = map(list, zip(*[make(sz, seed=5 + i) for i, sz in enumerate(sizes)]))
+        idx = list(range(k))
+        O.step(cfg, P, G, M, V, [None] * k, S, [1] * k, idx, threads=threads)  # step 1 (two-pass), untimed
+        times = []
+        for s in range(2, 12):
+            t0 = time.perf_counter()
+            O.step(cfg, P, G, M, V, [None] * k, S, [s] * k, idx, threads=threads)
+            times.append(time.perf_counter() - t0)
+        t = float(np.median(times))
+        n = sum(sizes)
+        return {
+            "value": n / t, "unit": "params/s", "cores": threads, "kind": "port",
+            "sample": f"the whole workload: {k} tensors, {n} elements (median of 10 steady steps, "
+                      f"{t * 1e3:.2f} ms/step), {threads} threads",
+            "gb_per_s": n * workload["bytes_per_param"] / t / 1e9,
+        }
 
     # calibrate on a small sample, then size the timed sample to ~target_s over 3 steps
     n_cal = 1 << 22
@@ -206,7 +239,8 @@ def main() -> int:
         return 1
     wl = WORKLOADS[args.config]
     pdt = torch.bfloat16 if wl["pdt"] == "bf16" else torch.float32
-    n = wl["n"]
+    sizes = wl.get("sizes", [wl.get("n", 0)])
+    n = sum(sizes)
     free, total = torch.cuda.mem_get_info()
     state_b = 4 * n * (2 if wl["buffer"] in (2, "T2") else 1)
     need = n * (2 if pdt == torch.bfloat16 else 4) * 2 + state_b
@@ -215,20 +249,25 @@ def main() -> int:
         log("not enough HBM for this workload")
         return 1
 
-    # Reserve-and-release most of HBM once before allocating the workload. On a freshly booted
-    # box the first large allocations of the first process are mapped such that this streaming
-    # step runs ~15% slower for the whole process lifetime (30.5 vs 26.5 ms on cfg5 measured on
-    # the same box); one allocate/free cycle (no writes, ~0.02 s) avoids that. Untimed.
+    # Reserve-and-release most of HBM once before allocating the workload (untimed, no writes,
+    # ~0.02 s). On a freshly booted box the first large allocations of the first process could
+    # land where this streaming step ran ~15% slower for the whole process lifetime; one
+    # allocate/free cycle avoided that. Placement still moves the step by about +-3% between
+    # processes (the driver chooses the physical pages).
     if not args.no_reserve:
         reserve = torch.empty(int(min(args.reserve_gb * (1 << 30), free * 0.9)), dtype=torch.uint8, device="cuda")
         del reserve
         torch.cuda.empty_cache()
 
     t0 = time.perf_counter()
-    p_data, g_data = fill_inputs(torch, n, pdt, wl["grad"])
-    p = torch.nn.Parameter(p_data, requires_grad=True)
-    p.grad = g_data
-    opt = LuminaV([p], lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"])
+    params = []
+    for i, size in enumerate(sizes):
+        p_data, g_data = fill_inputs(torch, size, pdt, wl["grad"], seed=1234 + i)
+        p = torch.nn.Parameter(p_data, requires_grad=True)
+        p.grad = g_data
+        params.append(p)
+    del p_data, g_data
+    opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"])
     torch.cuda.synchronize()
     log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
 
@@ -253,12 +292,13 @@ def main() -> int:
     bytes_launch = n * wl["bytes_per_param"]
     achieved = bytes_launch / (ms_avg / 1e3) / 1e9
     log(f"per-step event ms: min {min(per_step_ms):.3f} avg {ms_avg:.3f} max {max(per_step_ms):.3f}; wall {ms_wall:.3f}")
-    sc = opt.state[p]["scratch"].tolist()
-    log(f"scratch after {args.warmup + args.steps} steps: {sc}")
-    if not all(math.isfinite(x) for x in sc):
-        log("non-finite scratch")
-        return 1
-    del opt, p, p_data, g_data
+    for q in params:
+        sc = opt.state[q]["scratch"].tolist()
+        if not all(math.isfinite(x) for x in sc):
+            log(f"non-finite scratch {sc}")
+            return 1
+    log(f"scratch of the last tensor after {args.warmup + args.steps} steps: {sc}")
+    del opt, params, p
     torch.cuda.empty_cache()
     copy_gbs = copy_probe(torch)
     log(f"copy probe (fp32 negate, 4 GiB in + 4 GiB out): {copy_gbs:.0f} GB/s")
@@ -286,6 +326,7 @@ def main() -> int:
             "workload": wl["name"],
             "buffer": wl["buffer"],
             "params": n,
+            "tensors": len(sizes),
             "param_dtype": wl["pdt"],
             "state_dtype": "f32",
             "cautious": wl["cautious"],

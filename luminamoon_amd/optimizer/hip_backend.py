@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 from typing import Any, Dict, List, Optional, Sequence
 
@@ -137,15 +138,50 @@ class _Workspace:
         return buf
 
 
+# lv_tensor packed little-endian: 6 pointers, numel, step, param_index, 4 x int32, index_base,
+# inactive, n_inactive (layout checked against the header by tests/test_c_abi.py).
+_TENSOR = struct.Struct("<6Q3Q4i3Q")
+_STEP_OFFSET = 7 * 8   # byte offset of lv_tensor.step
+_GRAD_OFFSET = 1 * 8   # byte offset of lv_tensor.grad
+_OK_DTYPES = frozenset(DTYPE_CODES)
+
+
+class PreparedStep:
+    """Validated, packed descriptors for one lv_step_multi call. Between steps the caller may
+    swap a tensor's grad (same shape/dtype/device, contiguous; checked) and set step counters;
+    everything else stays as validated."""
+
+    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index")
+
+    def __init__(self, buf: bytearray, n: int, device: torch.device, numels: List[int], gdtypes: List[Any]):
+        self.buf = buf
+        self.items = (LvTensor * n).from_buffer(buf) if n else None
+        self.n = n
+        self.device = device
+        self.numels = numels
+        self.gdtypes = gdtypes
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+
+    def set_grad(self, i: int, g: torch.Tensor) -> bool:
+        """Point descriptor i at grad g; False (nothing changed) if g does not fit it."""
+        if (g.dtype is not self.gdtypes[i] or not g.is_cuda or g.get_device() != self.index
+                or g.numel() != self.numels[i] or not g.is_contiguous()):
+            return False
+        struct.pack_into("<Q", self.buf, i * _TENSOR.size + _GRAD_OFFSET, g.data_ptr())
+        return True
+
+    def set_step(self, i: int, step: int) -> None:
+        struct.pack_into("<Q", self.buf, i * _TENSOR.size + _STEP_OFFSET, int(step))
+
+
 class HipStepper:
     """Runs one optimizer step for a list of same-device tensors through lv_step_multi."""
 
     def __init__(self) -> None:
         self.workspace = _Workspace()
 
-    def step(
+    def prepare(
         self,
-        group: Dict[str, Any],
         params: Sequence[torch.Tensor],
         grads: Sequence[torch.Tensor],
         exp_avgs: Sequence[torch.Tensor],
@@ -156,23 +192,20 @@ class HipStepper:
         param_indices: Sequence[int],
         index_bases: Optional[Sequence[int]] = None,
         inactive: Optional[Sequence[Optional[torch.Tensor]]] = None,
-    ) -> None:
-        """index_bases: global element offset of each tensor when it is a shard of a larger
-        tensor (stochastic-rounding offsets continue from there); None = all 0.
-        inactive: per tensor, None or an int64 device tensor of shape [k, 2] holding sorted,
-        disjoint [begin, end) element ranges whose elements count in the statistics with a zero
-        gradient but are not written (a fused bucket's grad=None slices)."""
+    ) -> Optional[PreparedStep]:
+        """Validates every tensor and packs the lv_tensor descriptors (see step())."""
         n = len(params)
         if n == 0:
-            return
-        lib = load_library()
+            return None
         device = params[0].device
         if device.type != "cuda":
             raise RuntimeError(
                 "LuminaV (MI355X build) steps ROCm device tensors only; got a tensor on "
                 f"'{device}'. Move the model to the GPU before calling step()."
             )
-        items = (LvTensor * n)()
+        buf = bytearray(n * _TENSOR.size)
+        numels: List[int] = []
+        gdtypes: List[Any] = []
         for i in range(n):
             p, g, m = params[i], grads[i], exp_avgs[i]
             v, mp, sc = exp_avg_sqs[i], master_params[i], scratches[i]
@@ -181,6 +214,9 @@ class HipStepper:
                     raise ValueError(f"LuminaV: {name} of param index {param_indices[i]} is on {t.device}, expected {device}.")
                 if not t.is_contiguous():
                     raise ValueError(f"LuminaV: {name} of param index {param_indices[i]} must be contiguous.")
+            for name, t in (("param", p), ("grad", g), ("exp_avg", m)):
+                if t.dtype not in _OK_DTYPES:
+                    raise ValueError(f"LuminaV: unsupported dtype {t.dtype} for {name} of param index {param_indices[i]}.")
             numel = p.numel()
             if g.numel() != numel or m.numel() != numel:
                 raise ValueError(
@@ -220,21 +256,53 @@ class HipStepper:
                 if rng.device != device:
                     raise ValueError(f"LuminaV: inactive ranges of param index {param_indices[i]} must be on {device}.")
                 ip, ni = rng.data_ptr(), int(rng.shape[0])
-            items[i] = LvTensor(
-                p.data_ptr(), g.data_ptr(), m.data_ptr(), vp, mpp, sc.data_ptr(), numel, int(steps[i]),
-                int(param_indices[i]), DTYPE_CODES[p.dtype], DTYPE_CODES[g.dtype], DTYPE_CODES[m.dtype], 0,
+            _TENSOR.pack_into(
+                buf, i * _TENSOR.size, p.data_ptr(), g.data_ptr(), m.data_ptr(), vp, mpp, sc.data_ptr(), numel,
+                int(steps[i]), int(param_indices[i]), DTYPE_CODES[p.dtype], DTYPE_CODES[g.dtype], DTYPE_CODES[m.dtype], 0,
                 int(index_bases[i]) if index_bases is not None else 0, ip, ni,
             )
+            numels.append(numel)
+            gdtypes.append(g.dtype)
+        return PreparedStep(buf, n, device, numels, gdtypes)
+
+    def launch(self, group: Dict[str, Any], prep: Optional[PreparedStep]) -> None:
+        """One lv_step_multi call over prepared descriptors, on the device's current stream."""
+        if prep is None or prep.n == 0:
+            return
+        lib = load_library()
         cfg = make_config(group)
-        ws = self.workspace.get(device, n)
-        with torch.cuda.device(device):
-            stream = torch.cuda.current_stream(device).cuda_stream
-            rc = lib.lv_step_multi(ctypes.byref(cfg), items, n, ws.data_ptr(), ws.numel(), stream)
+        ws = self.workspace.get(prep.device, prep.n)
+        with torch.cuda.device(prep.device):
+            stream = torch.cuda.current_stream(prep.device).cuda_stream
+            rc = lib.lv_step_multi(ctypes.byref(cfg), prep.items, prep.n, ws.data_ptr(), ws.numel(), stream)
         if rc != 0:
             msg = lib.lv_last_error().decode(errors="replace")
             if rc in (-1, -3):
                 raise ValueError(f"LuminaV HIP step rejected the call ({STATUS_NAMES.get(rc, rc)}): {msg}")
             raise RuntimeError(f"LuminaV HIP step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
+
+    def step(
+        self,
+        group: Dict[str, Any],
+        params: Sequence[torch.Tensor],
+        grads: Sequence[torch.Tensor],
+        exp_avgs: Sequence[torch.Tensor],
+        exp_avg_sqs: Sequence[Optional[torch.Tensor]],
+        master_params: Sequence[Optional[torch.Tensor]],
+        scratches: Sequence[torch.Tensor],
+        steps: Sequence[int],
+        param_indices: Sequence[int],
+        index_bases: Optional[Sequence[int]] = None,
+        inactive: Optional[Sequence[Optional[torch.Tensor]]] = None,
+    ) -> None:
+        """index_bases: global element offset of each tensor when it is a shard of a larger
+        tensor (stochastic-rounding offsets continue from there); None = all 0.
+        inactive: per tensor, None or an int64 device tensor of shape [k, 2] holding sorted,
+        disjoint [begin, end) element ranges whose elements count in the statistics with a zero
+        gradient but are not written (a fused bucket's grad=None slices)."""
+        load_library()
+        self.launch(group, self.prepare(params, grads, exp_avgs, exp_avg_sqs, master_params, scratches, steps,
+                                        param_indices, index_bases, inactive))
 
 
 def device_info() -> Dict[str, Any]:

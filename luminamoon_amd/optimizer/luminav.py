@@ -20,6 +20,7 @@ from __future__ import annotations
 import logging
 import math
 import warnings
+import weakref
 from typing import Any, Callable, Dict, List, Optional, Set, Tuple, Union
 
 import torch
@@ -188,6 +189,10 @@ class LuminaV(Optimizer):
         self.bucket_cap_mb: float = float(defaults["bucket_cap_mb"])
         self.prewarm_jit: bool = bool(defaults["prewarm_jit"])
         self._stepper = hip_backend.HipStepper()
+        # Packed descriptors of each unfused param group, reused while nothing but grads and step
+        # counters changed (see _step_unfused); any state/param-group change bumps the epoch.
+        self._unfused_plans: Dict[int, Dict[str, Any]] = {}
+        self._plan_epoch = 0
 
         if any(bool(g.get("fuse_tensors", False)) for g in self.param_groups):
             self.fuse_tensors = True
@@ -270,6 +275,10 @@ class LuminaV(Optimizer):
     getCapabilities = get_capabilities
 
     # ------------------------------------------------------------------ validation
+
+    # Group keys that decide which state tensors a param has (and so the descriptors' pointers);
+    # every other option is read into the launch config at each step.
+    _LAYOUT_KEYS = ("buffer", "master_weights", "state_precision", "fuse_tensors", "fsdp_sync")
 
     _SIG_KEYS = (
         "lr", "betas", "eps", "weight_decay", "tau", "lam", "cautious", "cautious_clamp_min", "buffer",
@@ -659,7 +668,13 @@ class LuminaV(Optimizer):
             b["slices"] = new_slices
             b["step"] = bucket_step
 
+    def _invalidate_plans(self) -> None:
+        if hasattr(self, "_unfused_plans"):
+            self._unfused_plans.clear()
+            self._plan_epoch += 1
+
     def add_param_group(self, param_group: Dict[str, Any]) -> None:
+        self._invalidate_plans()
         for name, default in self.defaults.items():
             param_group.setdefault(name, default)
         self._validate_and_normalize_group(param_group)
@@ -744,6 +759,7 @@ class LuminaV(Optimizer):
 
     def load_state_dict(self, state_dict: Dict[str, Any]) -> None:
         """Loads state and re-normalises dtypes, scratch layout and buckets (reference luminav.py:1117-1292)."""
+        self._invalidate_plans()
         raw_state = state_dict.get("state", {})
         saved_groups = state_dict.get("param_groups", [])
         raw_param_state: Dict[Any, Dict[str, Any]] = {}
@@ -954,8 +970,15 @@ class LuminaV(Optimizer):
                            [step_t], [0], inactive=[table])
 
     def _step_unfused(self, group: Dict[str, Any], grads: Optional[Any]) -> None:
+        """Unfused params: one C-ABI call per device over every param that has a grad
+        (reference luminav.py:1932-1960 steps them one Triton launch at a time)."""
+        if grads is None and self._run_unfused_plan(group):
+            return
+        self._unfused_plans.pop(id(group), None)
         buf_count = group["buffer"]
         per_device: Dict[torch.device, List[Tuple[Any, ...]]] = {}
+        plannable = grads is None
+        active: List[bool] = []
         for idx, p in enumerate(group["params"]):
             g = None
             if grads is not None:
@@ -965,6 +988,7 @@ class LuminaV(Optimizer):
                     g = grads[p]
             if g is None:
                 g = p.grad
+            active.append(g is not None)
             if g is None:
                 continue
             if getattr(g, "is_sparse", False):
@@ -975,23 +999,75 @@ class LuminaV(Optimizer):
                 continue
             if not g.is_contiguous():
                 g = g.contiguous()
+                plannable = False
             if p.device.type == "cpu" and not p.is_contiguous():
                 raise ValueError(
                     f"LuminaV requires parameters to be contiguous in memory for native zero-copy execution. Call .contiguous() on parameter {idx} before passing to optimizer."
                 )
             p_step = p if p.is_contiguous() else p.contiguous()
+            if p_step is not p:
+                plannable = False
             if g.device != p.device:
                 g = g.to(p.device)
+                plannable = False
             state = self._init_or_refresh_state(p, group)
             state["step"] = int(state["step"]) + 1
             per_device.setdefault(p.device, []).append((
                 p, p_step, g, state["exp_avg"], state.get("exp_avg_sq") if buf_count in (2, "T2") else None,
-                state.get("master_param"), state["scratch"], state["step"], idx,
+                state.get("master_param"), state["scratch"], state["step"], idx, state,
             ))
         for dev, rows in per_device.items():
-            self._stepper.step(group, [r[1] for r in rows], [r[2] for r in rows], [r[3] for r in rows],
-                               [r[4] for r in rows], [r[5] for r in rows], [r[6] for r in rows],
-                               [r[7] for r in rows], [r[8] for r in rows])
+            prep = self._stepper.prepare([r[1] for r in rows], [r[2] for r in rows], [r[3] for r in rows],
+                                         [r[4] for r in rows], [r[5] for r in rows], [r[6] for r in rows],
+                                         [r[7] for r in rows], [r[8] for r in rows])
+            self._stepper.launch(group, prep)
             for r in rows:
                 if r[0] is not r[1]:
                     r[0].copy_(r[1])
+        if plannable and len(per_device) == 1:
+            rows = next(iter(per_device.values()))
+            # grads are held weakly: the plan must not keep last step's grads alive
+            self._unfused_plans[id(group)] = {
+                "epoch": self._plan_epoch, "group": group, "layout": tuple(group.get(k) for k in self._LAYOUT_KEYS),
+                "ids": [id(p) for p in group["params"]], "active": active,
+                "entries": [[r[0], r[0].data_ptr(), weakref.ref(r[2]), r[9], r[2].data_ptr()] for r in rows],
+                "prep": prep,
+            }
+
+    def _run_unfused_plan(self, group: Dict[str, Any]) -> bool:
+        """Steps `group` from its packed descriptors when only grads and step counters changed:
+        the same params carry a grad, param storage is where it was and no state was replaced
+        (load_state_dict and add_param_group bump the epoch; a changed buffer count, master mode or
+        state precision changes the recorded layout). Returns False, having changed nothing
+        the slow path relies on, when anything else changed."""
+        plan = self._unfused_plans.get(id(group))
+        if plan is None or plan["epoch"] != self._plan_epoch or plan["group"] is not group:
+            return False
+        if plan["layout"] != tuple(group.get(k) for k in self._LAYOUT_KEYS):
+            return False
+        params = group["params"]
+        ids, active = plan["ids"], plan["active"]
+        if len(params) != len(ids):
+            return False
+        for i, p in enumerate(params):
+            if id(p) != ids[i] or (p.grad is not None) != active[i]:
+                return False
+        prep = plan["prep"]
+        entries = plan["entries"]
+        for k, e in enumerate(entries):
+            p = e[0]
+            if p.data_ptr() != e[1]:
+                return False
+            g = p.grad
+            if g is not e[2]() or g.data_ptr() != e[4]:
+                if g.is_sparse or not prep.set_grad(k, g):
+                    return False
+                e[2] = weakref.ref(g)
+                e[4] = g.data_ptr()
+        for k, e in enumerate(entries):
+            st = e[3]
+            s = int(st["step"]) + 1
+            st["step"] = s
+            prep.set_step(k, s)
+        self._stepper.launch(group, prep)
+        return True

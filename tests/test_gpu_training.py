@@ -173,3 +173,87 @@ def test_tied_weights_and_grad_none_isolation_in_bucket():
     assert not torch.equal(p_active, torch.full((16,), 3.0, device="cuda"))
     m_frozen = opt.state[p_frozen]["exp_avg"]
     assert torch.count_nonzero(m_frozen) == 0
+
+
+def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
+    """Unfused groups reuse their packed descriptors while only grads and step counters change.
+    Every way the plan can go stale is driven here -- grads updated in place, new grad tensors,
+    a param losing and regaining its grad, param storage replaced, load_state_dict, a changed
+    hyper-parameter -- and each step is compared bit for bit with the oracle."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+    from tests.parity_util import TensorSet, assert_bitwise, oracle_config, seeded_tensor
+
+    O = oracle_mod
+    sizes = [4099, 1, 2048, 70_001]
+    host = TensorSet(sizes, "bf16", "bf16", "f32", True, False, seed=11)
+    params = [torch.nn.Parameter(t.clone().cuda()) for t in host.p]
+    opt = LuminaV(params, lr=3e-3, buffer="T2")
+    used = {"fast": 0}
+    real = opt._run_unfused_plan
+
+    def spy(group):
+        ok = real(group)
+        used["fast"] += int(ok)
+        return ok
+
+    opt._run_unfused_plan = spy
+    host_steps = [0] * len(sizes)
+
+    def run(s, mode, expect_fast):
+        grads = [seeded_tensor(n, 900 + 10 * s + i, 1e-3, torch.bfloat16) for i, n in enumerate(sizes)]
+        active = [True] * len(sizes)
+        if mode == "drop1":
+            active[1] = False
+        for i, p in enumerate(params):
+            if not active[i]:
+                p.grad = None
+            elif mode == "inplace" and p.grad is not None:
+                p.grad.copy_(grads[i].cuda())
+            else:
+                p.grad = grads[i].cuda()
+        before = used["fast"]
+        opt.step()
+        torch.cuda.synchronize()
+        assert used["fast"] - before == int(expect_fast), f"step {s} ({mode}): plan used {used['fast'] - before}"
+        group = opt.param_groups[0]
+        cfg = oracle_config(O, group)
+        for i in range(len(sizes)):
+            if not active[i]:
+                continue
+            host_steps[i] += 1
+            if group["master_weights"] and host.mp[i] is None:  # master weights switched on
+                host.mp[i] = host.p[i].float().clone()
+            if not group["cautious"]:  # the host layer's scratch forcing (reference luminav.py:1748-1749)
+                host.sc[i][3] = 1.0
+            O.step(cfg, [host.p[i]], [grads[i]], [host.m[i]], [host.v[i]], [host.mp[i]], [host.sc[i]],
+                   [host_steps[i]], [i])
+        for i, p in enumerate(params):
+            st = opt.state[p]
+            if host.mp[i] is not None:
+                assert_bitwise(st["master_param"], host.mp[i], f"step {s} ({mode}) mp[{i}]")
+            assert_bitwise(p.detach(), host.p[i], f"step {s} ({mode}) p[{i}]")
+            assert_bitwise(st["exp_avg"], host.m[i], f"step {s} ({mode}) m[{i}]")
+            assert_bitwise(st["exp_avg_sq"], host.v[i], f"step {s} ({mode}) v[{i}]")
+            assert_bitwise(st["scratch"], host.sc[i], f"step {s} ({mode}) scratch[{i}]")
+            assert int(st["step"]) == host_steps[i]
+
+    run(1, "new", False)      # builds the plan
+    run(2, "new", True)       # new grad tensors: pointers refreshed
+    run(3, "inplace", True)   # same grad tensors updated in place
+    run(4, "drop1", False)    # a param without a grad: slow path, new plan
+    run(5, "drop1", True)
+    run(6, "new", False)      # it has a grad again
+    run(7, "new", True)
+    params[2].data = params[2].data.clone()  # param storage moved
+    run(8, "new", False)
+    run(9, "new", True)
+    opt.load_state_dict(opt.state_dict())    # state tensors replaced
+    run(10, "new", False)
+    run(11, "new", True)
+    opt.param_groups[0]["lr"] = 1e-3         # options are read into every launch: the plan stays
+    opt.param_groups[0]["cautious"] = False
+    run(12, "new", True)
+    opt.param_groups[0]["master_weights"] = "full"  # the state layout changes: slow path, new plan
+    run(13, "new", False)
+    run(14, "new", True)
