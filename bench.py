@@ -321,7 +321,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (p ~ N(0,0.02), g = 1e-3*t(df=3) for cfg5 else 1e-3*N(0,1); generated on the GPU)",
+        "data": "synthetic (p ~ N(0,0.02), g = 1e-3*t(df=3) for cfg5 else 1e-3*N(0,1), 5% exact zeros for cfg2; "
+                "generated on the GPU)",
         "config": {
             "workload": wl["name"],
             "buffer": wl["buffer"],
