@@ -1252,11 +1252,17 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
         args.unit_base = 0;
         return launch_one(fn, args, grid, kThreads, stream);
     }
-    // unit launches, in pieces of at most kMaxGrid blocks, then the slot fold
+    // unit launches, in pieces of at most kMaxGrid blocks (LV_MAX_GRID_BLOCKS lowers the cap, so
+    // tests can split small launches), then the slot fold
     args.xcds = device_xcds();
-    for (uint32_t ub = 0; ub < args.total_units; ub += std::min<uint32_t>(kMaxGrid, args.total_units - ub)) {
+    uint32_t max_grid = kMaxGrid;
+    if (const char *e = std::getenv("LV_MAX_GRID_BLOCKS")) {
+        long v = std::atol(e);
+        if (v > 0 && (uint32_t)v < kMaxGrid) max_grid = (uint32_t)v;
+    }
+    for (uint32_t ub = 0; ub < args.total_units; ub += std::min<uint32_t>(max_grid, args.total_units - ub)) {
         args.unit_base = ub;
-        rc = launch_one(fn, args, std::min<uint32_t>(kMaxGrid, args.total_units - ub), kThreads, stream);
+        rc = launch_one(fn, args, std::min<uint32_t>(max_grid, args.total_units - ub), kThreads, stream);
         if (rc != LV_STATUS_SUCCESS) return rc;
     }
     args.unit_base = 0;

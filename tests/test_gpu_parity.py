@@ -249,3 +249,28 @@ def test_mask_count_exact_above_2_pow_24(oracle_mod):
 
 if __name__ == "__main__":
     sys.exit(pytest.main([__file__, "-v"]))
+
+
+@pytest.mark.parametrize("buffer,pdt,sdt", [("T2", "bf16", "f32"), ("T1", "bf16", "f32"), (2, "f32", "f32")])
+def test_unit_launch_split_into_pieces(oracle_mod, monkeypatch, buffer, pdt, sdt):
+    """A unit launch larger than the per-launch block cap runs as several pieces (unit_base);
+    LV_MAX_GRID_BLOCKS lowers the cap so small tensors exercise it: pieces of 7 blocks (fewer
+    than the 8 XCDs) and of 37 blocks, cutting across tensor boundaries, equal the oracle."""
+    _need_gpu()
+    O = oracle_mod
+    group = group_dict(buffer=buffer)
+    dual = group["buffer"] in (2, "T2")
+    sizes = [100_003, 5, 66_000, 2048, 1]
+    for cap in ("7", "37"):
+        monkeypatch.setenv("LV_MAX_GRID_BLOCKS", cap)
+        host = TensorSet(sizes, pdt, pdt, sdt, dual, False, seed=19, m_scale=1e-3)
+        dev = host.to("cuda")
+        cfg = oracle_config(O, group)
+        st = _stepper()
+        print(f"[case] split launch cap={cap} buffer={buffer} {pdt}", flush=True)
+        for s in range(1, 4):
+            grads = host.grads(s, seed=23)
+            host.oracle_step(O, cfg, grads, s)
+            dev.hip_step(st, group, [g.cuda() for g in grads], s)
+            torch.cuda.synchronize()
+            host.assert_equal(dev, f"cap {cap} step {s}")
