@@ -124,3 +124,24 @@ def test_host_side_rejections_without_device(lib):
     rcfg = _cfg(buffer="T2", bound_type="radial")
     assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, WS, None) == -3
     assert b"aliases" in lib.lv_last_error()
+
+
+def test_xcd_block_mapping_is_exact_and_bijective():
+    """Unit launches send block b to XCD x = b mod X and give each XCD one contiguous range of
+    units: unit = x * (G div X) + min(x, G mod X) + b div X. The kernel takes b div X as
+    (b * (floor(2^40 / X) + 1)) >> 40 (no integer division in the block prologue): exact for every
+    b below the 2^23-block launch cap and X <= 64, and the mapping is a permutation of the grid."""
+    import numpy as np
+
+    b = np.arange(1 << 23, dtype=np.uint64)
+    for X in range(1, 65):
+        recip = np.uint64((1 << 40) // X + 1)
+        assert np.array_equal((b * recip) >> np.uint64(40), b // np.uint64(X)), X
+    for X in (1, 3, 8, 12):
+        for G in list(range(1, 40)) + [1023, 6_580_484]:
+            bb = np.arange(G, dtype=np.int64)
+            i = (bb.astype(np.uint64) * np.uint64((1 << 40) // X + 1)) >> np.uint64(40)
+            x = bb - i.astype(np.int64) * X
+            q, r = G // X, G % X
+            unit = x * q + np.minimum(x, r) + i.astype(np.int64)
+            assert np.array_equal(np.sort(unit), bb), (X, G)
