@@ -95,8 +95,8 @@ typedef struct lv_tensor {
 int lv_version(void);
 
 /* Bytes of device workspace lv_step_multi needs for n_tensors tensors: 16 bytes of counters per
- * tensor (rounded up to 256), a fixed 192 KiB of cautious mask-count slots (48 tensors per
- * launch x 64 slots x 64 bytes) and a fixed 1.5 MiB of radial-bound partial sums (48 tensors per
+ * tensor (rounded up to 256), a fixed 195 KiB of cautious mask-count words (48 tensors per
+ * launch x 65 words x 64 bytes) and a fixed 1.5 MiB of radial-bound partial sums (48 tensors per
  * launch x 2048 blocks x 2 doubles). The caller allocates it once, zero-filled; the kernels
  * leave the counters and count slots zeroed again after every call (the partial slots need no
  * clearing), so it is reused from step to step. Calls that share one workspace must not

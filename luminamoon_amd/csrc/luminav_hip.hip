@@ -1,20 +1,23 @@
 // MI355X (gfx950) LuminaV optimizer step: HIP kernels + C ABI (include/luminav_hip.h).
 //
-// One fused, grid-stride, multi-tensor pass per (dtype, step, pass) class.  Each work unit is
-// 256 threads x 8 contiguous elements; a thread moves its 8 elements with 16-byte vector
-// loads/stores (one dwordx4 for bf16/f16, two for f32) and falls back to per-element access
-// for ragged tails and for tensors whose pointers are not 16-byte aligned.  The cautious mask
-// is counted exactly (per-thread integer counts, one u64 atomic per block and tensor), and the
-// last block of each tensor -- found with a per-tensor ticket -- finalises the 6-float scratch
-// on the device, so a step needs no host synchronisation and no extra launch.
+// One multi-tensor launch per (pass, step, dtype) class of tensors. Each tensor is cut into work
+// units of 1024 elements (2048 with 16-bit state); every block of a unit launch updates exactly
+// one unit and exits. A thread moves 4 consecutive elements of each 1024-element half with
+// vector loads/stores (16 bytes for f32, 8 for 16-bit types) and falls back to per-element
+// access for the partial last unit and for tensors whose pointers are not 16-byte aligned.
+// The cautious mask is counted exactly: each block reports its integer count and its completion
+// in one atomic on one of 64 spread u64 slot words per tensor; the block that completes the
+// tensor holds the exact total and finalises the 6-float scratch on the device, so a steady step
+// is one launch and needs no host synchronisation.
 //
-// Radial bound: the squared-norm sums sum(u_eff^2) and sum(p^2) are accumulated from the f32
-// squares in f64 (per thread, then a fixed-order wave/block reduction), each block stores its
-// partial in a workspace slot, and the finalising block folds the slots in block order. The
-// result (rounded to f32 once) is the exactly rounded sum up to f64 rounding, and bitwise
-// deterministic for a given grid. The reference's own f32 sums depend on its CPU backend
-// (16-lane order in reference_cpu/dual.rs:134-253 vs. AVX-512 reductions in avx512/dual.rs),
-// so radial results match it to its cross-backend tolerance, not bit for bit.
+// Radial bound (counting passes only): a persistent grid walks the units grid-stride; the
+// squared-norm sums sum(u_eff^2) and sum(p^2) are accumulated from the f32 squares in f64 (per
+// thread, then a fixed-order wave/block reduction), each block stores its partial in a
+// workspace slot, and the block that completes a tensor (per-tensor ticket) folds the slots in
+// block order. The result (rounded to f32 once) is the exactly rounded sum up to f64 rounding,
+// and bitwise deterministic for a given grid. The reference's own f32 sums depend on its CPU
+// backend (16-lane order in reference_cpu/dual.rs:134-253 vs. AVX-512 reductions in
+// avx512/dual.rs), so radial results match it to its cross-backend tolerance, not bit for bit.
 //
 // Per-element arithmetic follows the reference's scalar core operation for operation
 // (optimizer/crates/luminav-core/src/reference_cpu/dual.rs, reference_cpu/tdclm.rs,
@@ -42,19 +45,26 @@ constexpr int kThreads = 256;
 constexpr uint32_t kHalf = kThreads * 4;     // a thread owns 4 consecutive elements of each half
 constexpr int kPersistHalves = 2;            // halves per work unit of a persistent launch (2048)
 
-// Halves per work unit of a unit launch: blocks that move about 20-28 KB of HBM traffic stream
-// best on MI355X (measured: 1024-element units for 22 and 28 B/element, 2048 for 14 B/element,
-// 5.7% apart on the 14 B/element T1 step).
+// Halves per work unit of a unit launch. With f32 state the step is HBM-bound and 1024-element
+// units stream best (measured in one process: T2 bf16/f32 23.2 vs 23.6 ms, T1 bf16/f32 2.17 vs
+// 2.25 ms, CLM and TD-CLM f32 0.58 vs 0.63 ms and 0.41 vs 0.44 ms for 1024 vs 2048). With 16-bit
+// state, stochastic rounding of m (and v) makes the step VALU-bound and 2048-element units are
+// faster (T2 bf16/bf16 3.05 vs 3.40 ms, T1 bf16/bf16 2.22 vs 2.49 ms).
 constexpr int unit_halves(int mode, int pt, int st) {
-    const int ps = pt == LV_DTYPE_F32 ? 4 : 2, ss = st == LV_DTYPE_F32 ? 4 : 2;
-    const bool dual = mode == LV_BUFFER_DUAL || mode == LV_BUFFER_T2;
-    const int bytes = 3 * ps + 2 * ss * (dual ? 2 : 1);  // p read+write, g read, state read+write
-    return bytes < 18 ? 2 : 1;
+    (void)mode;
+    (void)pt;
+    return st == LV_DTYPE_F32 ? 1 : 2;
 }
 constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
 constexpr uint32_t kRadialMaxBlocks = 2048;  // grid cap of radial launches (workspace partial slots)
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
+constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
 constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-byte segment
+// Slot word: mask count << kTicketBits | blocks that reported. A tensor has < 2^32 units of
+// >= 1024 elements and at most 2^42 elements, so a slot sees <= 2^26 blocks (27 bits) and
+// counts <= 2^36 elements (37 bits). Fold word: count << 7 | slots completed (<= 64).
+constexpr int kTicketBits = 27;
+constexpr int kFoldBits = 7;
 constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
@@ -99,7 +109,7 @@ struct Args {
     int32_t ndesc;
     uint64_t xcd_recip;  // unit launches: floor(2^40 / xcds) + 1, so b / xcds == (b * xcd_recip) >> 40
     unsigned long long *counters;  // persistent launches: 2 per tensor (mask count, finished-unit ticket)
-    unsigned long long *slots;     // unit launches: kSlots mask-count slots per tensor
+    unsigned long long *slots;     // unit launches: kSlotWords count words per tensor
     double *partials;              // radial: [tensor][block] pairs (sum u_eff^2, sum p^2)
     Desc d[kMaxDesc];
 };
@@ -863,15 +873,47 @@ __device__ __forceinline__ int find_tensor(const Args &a, int lo, uint32_t unit)
 
 // ------------------------------------------------------------------ the kernels
 
+// Counting unit launches: thread 0 of every block reports its exact mask count and the block's
+// completion in ONE 64-bit atomic (count << kTicketBits | 1) on one of the tensor's kSlots slot
+// words (slot = unit index in the tensor mod kSlots, 64 B apart, so the atomics spread over
+// L2 channels). The block whose report completes a slot (its ticket reaches the slot's block
+// count) holds that slot's whole count in the value its own atomic returned, re-zeroes the slot
+// and reports count << kFoldBits | 1 on the tensor's fold word; the block that completes the
+// fold word holds the tensor's exact count and finalises the scratch. Every decision reads only
+// the value returned by an atomic on that same word, so no fence is needed (a device-scope
+// release fence per block measured 7x slower); integer sums are exact in any order, so the
+// result is deterministic. Wholly inactive units report a zero count.
+template <int MODE, int PASS>
+__device__ __forceinline__ void report_count(const Args &a, int t, const View &tv, uint32_t unit, uint32_t count) {
+    const uint32_t n_units = tv.t_end - tv.t_begin;
+    const uint32_t k = unit - tv.t_begin;
+    const uint32_t s = k % kSlots;
+    unsigned long long *words = a.slots + (size_t)t * kSlotWords * kSlotStride;
+    unsigned long long *slot = words + (size_t)s * kSlotStride;
+    constexpr unsigned long long kTicketMask = (1ull << kTicketBits) - 1ull;
+    const unsigned long long old = __hip_atomic_fetch_add(slot, ((unsigned long long)count << kTicketBits) | 1ull,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t expect = n_units / kSlots + (s < n_units % kSlots ? 1u : 0u);
+    if ((uint32_t)(old & kTicketMask) + 1u != expect) return;
+    const unsigned long long slot_count = (old >> kTicketBits) + count;
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long *fold = words + (size_t)kSlots * kSlotStride;
+    const unsigned long long prev = __hip_atomic_fetch_add(fold, (slot_count << kFoldBits) | 1ull, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t nslots = n_units < kSlots ? n_units : kSlots;
+    if ((uint32_t)(prev & ((1ull << kFoldBits) - 1ull)) + 1u != nslots) return;
+    __hip_atomic_store(fold, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finalize_scratch<MODE, PASS>(a, false, a.d[t], (prev >> kFoldBits) + slot_count, 0.0f, 0.0f);
+}
+
 // Unit launch: each block updates exactly one work unit (1024 or 2048 elements, unit_halves) and
 // exits.
 // The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
 // arithmetic of others without a software pipeline; on MI355X this launch shape streams HBM
 // faster than any persistent grid-stride loop over the same buffers (measured: 23.4 vs 26.5 ms
-// for the 6.7e9-element T2 step; 2048-element units: 23.7 ms). Counting passes add each block's
-// exact mask count into one of the tensor's kSlots u64 slots (relaxed integer atomics: exact in
-// any order, no fence per block); finalize_kernel folds the slots after the launch. Never used
-// for radial counting.
+// for the 6.7e9-element T2 step; 2048-element units: 23.7 ms). Counting passes report each
+// block's exact mask count (report_count), and the last block of each tensor finalises its
+// scratch, so a step is one launch. Never used for radial counting.
 // FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
 // which case every option test folds at compile time and the per-element code is straight-line.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL>
@@ -901,7 +943,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         const uint64_t e0 = (uint64_t)(unit - tv.t_begin) * (kHalf * H);
         cover = inactive_cover(D, e0, e0 + kHalf * H < tv.n ? e0 + kHalf * H : tv.n, first);
         // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing.
-        if (cover == 2) return;
+        if (!kCounting && cover == 2) return;
     }
     if (cover == 0 && tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
         const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, false, unit);
@@ -909,7 +951,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
         process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, f, unit, cnt, su, sp);
-    } else {
+    } else if (cover != 2) {
         scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, unit, cnt, su, sp, cover ? D.nskip : 0, first);
     }
     if constexpr (kCounting) {
@@ -921,31 +963,9 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
             uint32_t tot = 0;
 #pragma unroll
             for (int k = 0; k < kThreads / 64; k++) tot += wcnt[k];
-            if (tot) {
-                unsigned long long *slot = a.slots + ((size_t)t * kSlots + unit % kSlots) * kSlotStride;
-                __hip_atomic_fetch_add(slot, (unsigned long long)tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            report_count<MODE, PASS>(a, t, tv, unit, tot);
         }
     }
-}
-
-// After a counting unit launch: block t folds tensor t's kSlots slots (one per lane; the u64
-// sum is exact in any order), re-zeroes them for the next launch and finalises the scratch.
-template <int MODE, int PASS>
-__global__ void __launch_bounds__(kSlots) finalize_kernel(const Args a) {
-    static_assert(kSlots == 64, "one slot per lane of one wave");
-    const int t = blockIdx.x;
-    unsigned long long *slot = a.slots + ((size_t)t * kSlots + threadIdx.x) * kSlotStride;
-    unsigned long long c = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t lo = (uint32_t)c, hi = (uint32_t)(c >> 32);
-    unsigned long long tot = 0;
-#pragma unroll
-    for (int k = 0; k < 64; k++) {
-        unsigned long long x = ((unsigned long long)(uint32_t)__shfl(hi, k, 64) << 32) | (uint32_t)__shfl(lo, k, 64);
-        tot += x;
-    }
-    if (threadIdx.x == 0) finalize_scratch<MODE, PASS>(a, false, a.d[t], tot, 0.0f, 0.0f);
 }
 
 // Persistent launch (radial-bound counting passes): a grid of exactly the resident blocks walks
@@ -1084,20 +1104,6 @@ static KernelFn pick_kernel(int mode, int pt, int st, int pass, uint32_t flags) 
     case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass, flags);
     case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass, flags);
     default: return pick_param<LV_BUFFER_T2>(pt, st, pass, flags);
-    }
-}
-
-template <int MODE>
-KernelFn pick_finalize_mode(int pass) {
-    return pass == kFused ? finalize_kernel<MODE, kFused> : finalize_kernel<MODE, kCount>;
-}
-
-static KernelFn pick_finalize(int mode, int pass) {
-    switch (mode) {
-    case LV_BUFFER_TDCLM: return pick_finalize_mode<LV_BUFFER_TDCLM>(pass);
-    case LV_BUFFER_DUAL: return pick_finalize_mode<LV_BUFFER_DUAL>(pass);
-    case LV_BUFFER_T1: return pick_finalize_mode<LV_BUFFER_T1>(pass);
-    default: return pick_finalize_mode<LV_BUFFER_T2>(pass);
     }
 }
 
@@ -1280,7 +1286,6 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
         if (rc != LV_STATUS_SUCCESS) return rc;
     }
     args.unit_base = 0;
-    if (counting) return launch_one(pick_finalize(mode, pass), args, (uint32_t)args.ndesc, kSlots, stream);
     return LV_STATUS_SUCCESS;
 }
 
@@ -1292,15 +1297,15 @@ extern "C" {
 
 int lv_version(void) { return 100; }
 
-// Layout: [2 u64 counters per tensor, padded to 256 B][count slots: kMaxDesc x kSlots slots of
-// 64 B][radial partials: kMaxDesc x kRadialMaxBlocks x 2 doubles]. The slots and partials are
-// reused by every launch of a call (stream-ordered); finalize_kernel re-zeroes the slots.
+// Layout: [2 u64 counters per tensor, padded to 256 B][count words: kMaxDesc x kSlotWords words,
+// 64 B apart][radial partials: kMaxDesc x kRadialMaxBlocks x 2 doubles]. The words and partials
+// are reused by every launch of a call (stream-ordered); each launch leaves its words zeroed.
 static size_t counter_bytes(int n_tensors) {
     size_t b = (size_t)n_tensors * 2 * sizeof(unsigned long long);
     return (b + 255) & ~(size_t)255;
 }
 
-static constexpr size_t kSlotBytes = (size_t)lv::kMaxDesc * lv::kSlots * lv::kSlotStride * sizeof(unsigned long long);
+static constexpr size_t kSlotBytes = (size_t)lv::kMaxDesc * lv::kSlotWords * lv::kSlotStride * sizeof(unsigned long long);
 
 size_t lv_workspace_bytes(int n_tensors) {
     if (n_tensors < 1) n_tensors = 1;

@@ -247,15 +247,14 @@ def test_mask_count_exact_above_2_pow_24(oracle_mod):
         host.assert_equal(dev, f"2^25 step {s}")
 
 
-if __name__ == "__main__":
-    sys.exit(pytest.main([__file__, "-v"]))
-
 
 @pytest.mark.parametrize("buffer,pdt,sdt", [("T2", "bf16", "f32"), ("T1", "bf16", "f32"), (2, "f32", "f32")])
 def test_unit_launch_split_into_pieces(oracle_mod, monkeypatch, buffer, pdt, sdt):
     """A unit launch larger than the per-launch block cap runs as several pieces (unit_base);
     LV_MAX_GRID_BLOCKS lowers the cap so small tensors exercise it: pieces of 7 blocks (fewer
-    than the 8 XCDs) and of 37 blocks, cutting across tensor boundaries, equal the oracle."""
+    than the 8 XCDs) and of 37 blocks, cutting across tensor boundaries, equal the oracle. The
+    mask-count words of a tensor split over pieces fold in whichever piece runs its last block,
+    and every call leaves the workspace zeroed."""
     _need_gpu()
     O = oracle_mod
     group = group_dict(buffer=buffer)
@@ -274,3 +273,9 @@ def test_unit_launch_split_into_pieces(oracle_mod, monkeypatch, buffer, pdt, sdt
             dev.hip_step(st, group, [g.cuda() for g in grads], s)
             torch.cuda.synchronize()
             host.assert_equal(dev, f"cap {cap} step {s}")
+            for ws in st.workspace._bufs.values():
+                assert int(torch.count_nonzero(ws)) == 0, f"workspace not left zeroed (cap {cap} step {s})"
+
+
+if __name__ == "__main__":
+    sys.exit(pytest.main([__file__, "-v"]))
