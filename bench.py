@@ -132,23 +132,36 @@ def copy_probe(torch, n_floats: int = 1 << 30, reps: int = 5) -> float:
 
 
 def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
-    """The CPU oracle (a C restatement of the reference's Rust CPU path with its structure:
-    serial bf16 decode/encode, 2,097,152-element chunks over threads) on a bounded sample of the
-    same workload, timed with perf_counter around the step call only."""
+    """The reference's CPU path restated in C (oracle/): its AVX-512 chunk kernels
+    (luminav-simd/src/avx512/*.rs, 16 lanes) when this host has AVX-512, else its scalar core,
+    with its structure (serial bf16 decode/encode, 2,097,152-element chunks over threads), on a
+    bounded sample of the same workload, timed with perf_counter around the step call only."""
     import numpy as np
     import torch
 
     from oracle import oracle as O
 
     O.lib()
+    simd = O.avx512_available()
+    with O.backend(O.BACKEND_AVX512 if simd else O.BACKEND_SCALAR):
+        out = _cpu_baseline_timed(O, np, torch, workload, threads, target_s)
+    out["sample"] += "; " + ("AVX-512 chunk kernels (luminav-simd restatement)" if simd
+                             else "scalar core (no AVX-512 on this host)")
+    return out
+
+
+def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: float) -> dict:
     pdt = torch.bfloat16 if workload["pdt"] == "bf16" else torch.float32
     cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"])
     dual = workload["buffer"] in (2, "T2")
 
     def make(n, seed=5):
+        # a 2^24-value random block repeated over the sample: the same value mix at any size, and
+        # generating a billion normals would take longer than the timed steps
         rng = np.random.default_rng(seed)
-        p = torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)).to(pdt)
-        g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(pdt)
+        k = min(n, 1 << 24)
+        p = torch.from_numpy(np.resize((rng.standard_normal(k) * 0.02).astype(np.float32), n)).to(pdt)
+        g = torch.from_numpy(np.resize((rng.standard_normal(k) * 1e-3).astype(np.float32), n)).to(pdt)
         m = torch.zeros(n)
         v = torch.zeros(n) if dual else None
         sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
@@ -175,14 +188,16 @@ def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
             "gb_per_s": n * workload["bytes_per_param"] / t / 1e9,
         }
 
-    # calibrate on a small sample, then size the timed sample to ~target_s over 3 steps
-    n_cal = 1 << 22
+    # calibrate on 2^25 elements (16 chunks: memory-bound like the full size), then size the timed
+    # sample to ~target_s over 3 steps, at most 2^30 elements
+    n_cal = min(workload["n"], 1 << 25)
     p, g, m, v, sc = make(n_cal)
     O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)
     t0 = time.perf_counter()
     O.step(cfg, [p], [g], [m], [v], [None], [sc], [2], [0], threads=threads)
     rate = n_cal / max(time.perf_counter() - t0, 1e-6)
-    n = int(min(workload["n"], max(n_cal, rate * target_s / 3.0)))
+    del p, g, m, v
+    n = int(min(workload["n"], 1 << 30, max(n_cal, rate * target_s / 3.0)))
     n = (n // 2097152 + 1) * 2097152 if n > 2097152 else n
     p, g, m, v, sc = make(n)
     O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)  # step 1 (two-pass), untimed

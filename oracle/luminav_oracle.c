@@ -17,7 +17,7 @@
  *     the last f64 ulp of bc1/bc2; the f32 coefficients are pinned by exact
  *     rational arithmetic in the tests).
  */
-#include "luminav_oracle.h"
+#include "luminav_oracle_internal.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -357,27 +357,6 @@ int lvo_validate_config(const lvo_config *c) {
 
 /* ------------------------------------------------------- per-element core */
 
-typedef struct {
-    int mode;        /* 1 TD-CLM, 2 CLM, 3 T1, 4 T2 */
-    int triangle;    /* T1 / T2: rational coordinate bound */
-    int dual_state;  /* CLM / T2: exp_avg_sq present */
-    int clamp_v;     /* fp16 param or fp16 state: v <= 65000 */
-    int fp16_param;
-    int cautious, sr, bound, has_master, wd_nonzero;
-    int p_mode, s_mode;
-    float lr, b1, b2, omb1, omb2, b1sq, omb1sq, lam, lam1, eps, c1, c2, c_sigma, lr_wd, ratio;
-    int32_t seed_m, seed_p, seed_v;
-    uint64_t index_base;
-} coef_t;
-
-typedef struct {
-    float *p;           /* decoded f32 param */
-    float *mp;          /* master or NULL */
-    const float *g;     /* decoded f32 grad */
-    float *m;
-    float *v;           /* NULL for TD-CLM / T1 */
-} view_t;
-
 /* u for one element; m_new / v_new are returned for the apply step.
  * CLM: dual.rs:63-74; T2: dual.rs:492-506; TD-CLM / T1: tdclm.rs:102-109. */
 static inline float compute_u(const coef_t *k, float g, float m, float v, float *m_new_out, float *v_new_out) {
@@ -473,11 +452,39 @@ static inline int count_elem(const coef_t *k, const view_t *w, uint64_t idx, flo
     return active;
 }
 
-typedef struct {
-    uint64_t mask;
-    float u_sq, p_sq;
-    double du, dp; /* f64 sum mode */
-} chunk_metrics;
+int lvo_i_apply_elem(const coef_t *k, const view_t *w, uint64_t idx, float cs, float bs, float *u_sq_out,
+                     float *p_sq_out) {
+    return apply_elem(k, w, idx, cs, bs, u_sq_out, p_sq_out);
+}
+
+int lvo_i_count_elem(const coef_t *k, const view_t *w, uint64_t idx, float *u_sq_out, float *p_sq_out) {
+    return count_elem(k, w, idx, u_sq_out, p_sq_out);
+}
+
+/* luminav-simd/src/lib.rs:38-60 (the AVX-512 backend's feature test) */
+int lvo_i_cpu_has_avx512(void) {
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512dq") &&
+           __builtin_cpu_supports("avx512bw") && __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("fma");
+#else
+    return 0;
+#endif
+}
+
+/* Chunk backend: 0 = the scalar core (default, what the HIP kernels are checked against);
+ * 1 = the restatement of luminav-simd's AVX-512 chunk kernels (avx512/dual.rs, avx512/tdclm.rs),
+ * the reference's own CPU execution path. The f64 radial sum mode always uses the scalar core. */
+static int g_backend = 0;
+
+int32_t lvo_set_backend(int32_t backend) {
+    if (backend != 0 && backend != 1) return fail(LVO_ERR_CONFIG, "unknown backend");
+    if (backend == 1 && !lvo_i_cpu_has_avx512()) return fail(LVO_ERR_EXEC, "this CPU lacks AVX-512 (avx512f/dq/bw/vl + fma)");
+    g_backend = backend;
+    return LVO_OK;
+}
+
+int32_t lvo_backend(void) { return g_backend; }
 
 /* Radial sum mode (checker option, not a reference behaviour): 0 = the scalar core's f32 lane
  * and chunk order (default); 1 = every f32 square added in f64, rounded to f32 once -- the
@@ -489,6 +496,7 @@ int32_t lvo_radial_sum_mode(void) { return g_radial_sum_f64; }
 /* One 2,097,152-element chunk of a counting pass: lane sums exactly as the scalar core. */
 static chunk_metrics run_chunk(const coef_t *k, const view_t *w, uint64_t start, uint64_t end,
                                int apply, float cs, float bs) {
+    if (g_backend == 1 && !g_radial_sum_f64) return lvo_i_avx512_chunk(k, w, start, end, apply, cs, bs);
     chunk_metrics cm = {0, 0.0f, 0.0f, 0.0, 0.0};
     uint64_t len = end - start;
     uint64_t simd_len = len & ~15ull;
@@ -556,6 +564,17 @@ static chunk_metrics run_counting(const coef_t *k, const view_t *w, uint64_t n, 
 
 /* Non-counting single pass (dual.rs:52-121, dual.rs:481-553). */
 static void run_plain(const coef_t *k, const view_t *w, uint64_t n, int threads) {
+    if (g_backend == 1) {
+        /* avx512/dual.rs:891-918: the same 2,097,152-element chunks, serial or in parallel */
+        uint64_t nchunks = (n + LVO_ELEM_CHUNK_SIZE - 1) / LVO_ELEM_CHUNK_SIZE;
+#pragma omp parallel for num_threads(threads > 1 ? threads : 1) schedule(dynamic, 1) if (threads > 1 && nchunks > 1)
+        for (int64_t c = 0; c < (int64_t)nchunks; c++) {
+            uint64_t s = (uint64_t)c * LVO_ELEM_CHUNK_SIZE;
+            uint64_t e = s + LVO_ELEM_CHUNK_SIZE < n ? s + LVO_ELEM_CHUNK_SIZE : n;
+            (void)lvo_i_avx512_chunk(k, w, s, e, 1, 1.0f, 1.0f);
+        }
+        return;
+    }
     if (threads > 1 && n > LVO_ELEM_CHUNK_SIZE) {
         uint64_t nchunks = (n + LVO_ELEM_CHUNK_SIZE - 1) / LVO_ELEM_CHUNK_SIZE;
 #pragma omp parallel for num_threads(threads) schedule(dynamic, 1)

@@ -99,6 +99,13 @@ float lvo_u64_to_f32(uint64_t x);
 void lvo_set_radial_sum_mode(int32_t mode);
 int32_t lvo_radial_sum_mode(void);
 
+/* Chunk backend, process-global: 0 (default) = the scalar core (luminav-core reference_cpu,
+ * what the HIP kernels are checked against bit for bit); 1 = the restatement of the reference's
+ * AVX-512 chunk kernels (luminav-simd/src/avx512/{mod,dual,tdclm}.rs), its CPU execution path.
+ * Returns LVO_OK, or LVO_ERR_EXEC when the CPU lacks avx512f/dq/bw/vl + fma. */
+int32_t lvo_set_backend(int32_t backend);
+int32_t lvo_backend(void);
+
 /* Validate like LuminaVConfig::validate (config.rs:329-366). Returns LVO_OK or LVO_ERR_CONFIG. */
 int lvo_validate_config(const lvo_config *cfg);
 

@@ -113,6 +113,8 @@ def lib() -> ctypes.CDLL:
             "lvo_update_post_step_ema": (None, [ctypes.POINTER(f), f, ctypes.POINTER(LvoConfig), i32]),
             "lvo_u64_to_f32": (f, [u64]),
             "lvo_set_radial_sum_mode": (None, [i32]),
+            "lvo_set_backend": (i32, [i32]),
+            "lvo_backend": (i32, []),
             "lvo_radial_sum_mode": (i32, []),
             "lvo_validate_config": (ctypes.c_int, [ctypes.POINTER(LvoConfig)]),
             "lvo_step_multi": (ctypes.c_int, [ctypes.POINTER(LvoConfig), ctypes.POINTER(LvoTensor), ctypes.c_int, ctypes.c_int]),
@@ -138,6 +140,32 @@ def radial_sum_f64():
         yield
     finally:
         L.lvo_set_radial_sum_mode(old)
+
+
+BACKEND_SCALAR, BACKEND_AVX512 = 0, 1
+
+
+def avx512_available() -> bool:
+    """True when this CPU runs the AVX-512 chunk kernels (avx512f/dq/bw/vl + fma)."""
+    L = lib()
+    old = L.lvo_backend()
+    ok = L.lvo_set_backend(BACKEND_AVX512) == 0
+    L.lvo_set_backend(old)
+    return ok
+
+
+@contextlib.contextmanager
+def backend(which: int):
+    """Inside the block the oracle runs its chunks on `which`: BACKEND_SCALAR (the scalar core,
+    the default) or BACKEND_AVX512 (the restatement of luminav-simd's AVX-512 kernels)."""
+    L = lib()
+    old = L.lvo_backend()
+    if L.lvo_set_backend(int(which)) != 0:
+        raise RuntimeError(L.lvo_last_error().decode())
+    try:
+        yield
+    finally:
+        L.lvo_set_backend(old)
 
 
 def make_config(

@@ -43,10 +43,11 @@ def test_pins_reject_mutant(name, tmp_path):
     assert old in src, f"mutation anchor for {name} not found"
     mutant = tmp_path / "luminav_oracle.c"
     mutant.write_text(src.replace(old, new, 1))
-    (tmp_path / "luminav_oracle.h").write_text(open(os.path.join(ROOT, "oracle", "luminav_oracle.h")).read())
+    for other in ("luminav_oracle.h", "luminav_oracle_internal.h", "luminav_oracle_avx512.c"):
+        (tmp_path / other).write_text(open(os.path.join(ROOT, "oracle", other)).read())
     lib = tmp_path / "libmutant.so"
     subprocess.run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-march=x86-64-v3", "-ffp-contract=off", "-fno-math-errno",
-                    "-fopenmp", "-o", str(lib), str(mutant), "-lm"], check=True)
+                    "-fopenmp", "-o", str(lib), str(mutant), str(tmp_path / "luminav_oracle_avx512.c"), "-lm"], check=True)
     env = dict(os.environ, LVO_LIB_OVERRIDE=str(lib))
     res = subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider",
                           os.path.join(ROOT, "tests", "test_oracle_pins.py")], cwd=ROOT, env=env,
