@@ -100,7 +100,8 @@ int lv_version(void);
  * launch x 2048 blocks x 2 doubles). The caller allocates it once, zero-filled; the kernels
  * leave the counters and count slots zeroed again after every call (the partial slots need no
  * clearing), so it is reused from step to step. Calls that share one workspace must not
- * overlap. */
+ * overlap. After a call that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way),
+ * zero the workspace again before reusing it. */
 size_t lv_workspace_bytes(int n_tensors);
 
 /*

@@ -1508,7 +1508,13 @@ int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_
     t.step = step;
     t.param_index = 0;
     t.param_dtype = t.grad_dtype = t.state_dtype = LV_DTYPE_F32;
-    return lv_step_multi(&c, &t, 1, ws[dev], lv_workspace_bytes(1), stream);
+    int rc = lv_step_multi(&c, &t, 1, ws[dev], lv_workspace_bytes(1), stream);
+    if (rc == LV_STATUS_EXECUTION_FAILED) {
+        // a launch failed part-way: its count words may hold partial counts; start clean
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (hipStreamSynchronize(s) == hipSuccess) (void)hipMemset(ws[dev], 0, lv_workspace_bytes(1));
+    }
+    return rc;
 }
 
 }  // extern "C"

@@ -137,6 +137,11 @@ class _Workspace:
             self._bufs[device] = buf
         return buf
 
+    def discard(self, device: torch.device) -> None:
+        """Drops the device's buffer: after a failed launch its count words may hold a partial
+        launch's counts, so the next call starts from a fresh zero-filled one."""
+        self._bufs.pop(device, None)
+
 
 # lv_tensor packed little-endian: 6 pointers, numel, step, param_index, 4 x int32, index_base,
 # inactive, n_inactive (layout checked against the header by tests/test_c_abi.py).
@@ -277,8 +282,9 @@ class HipStepper:
             rc = lib.lv_step_multi(ctypes.byref(cfg), prep.items, prep.n, ws.data_ptr(), ws.numel(), stream)
         if rc != 0:
             msg = lib.lv_last_error().decode(errors="replace")
-            if rc in (-1, -3):
+            if rc in (-1, -3):  # rejected before any launch: the workspace is untouched
                 raise ValueError(f"LuminaV HIP step rejected the call ({STATUS_NAMES.get(rc, rc)}): {msg}")
+            self.workspace.discard(prep.device)
             raise RuntimeError(f"LuminaV HIP step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
 
     def step(
