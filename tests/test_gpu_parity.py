@@ -277,5 +277,50 @@ def test_unit_launch_split_into_pieces(oracle_mod, monkeypatch, buffer, pdt, sdt
                 assert int(torch.count_nonzero(ws)) == 0, f"workspace not left zeroed (cap {cap} step {s})"
 
 
+@pytest.mark.parametrize("buffer", [1, 2, 3, 4])
+@pytest.mark.parametrize("cautious,bound_mode", [(1, 2), (0, 2), (1, 0)])
+def test_lv_step_f32_matches_oracle(oracle_mod, buffer, cautious, bound_mode):
+    """lv_step_f32, the argument-for-argument twin of the reference's luminav_triton_step_f32
+    (luminav_triton_standalone.h:89-111), called through the C ABI on device pointers: four steps
+    (two-pass, then fused) bitwise equal to the oracle with the reference's defaults for the
+    rest (ema_decay per buffer mode, clamp_min 0.5, SR and fused single pass on)."""
+    _need_gpu()
+    import ctypes
+
+    import numpy as np
+
+    from luminamoon_amd.optimizer import hip_backend
+
+    O = oracle_mod
+    L = hip_backend.load_library()
+    n = 70_001
+    dual = buffer in (2, 4)
+    rng = np.random.default_rng(31 + buffer)
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    hp, hm = torch.from_numpy(p0.copy()), torch.zeros(n)
+    hv = torch.zeros(n) if dual else None
+    hs = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
+    dp, dm = hp.clone().cuda(), hm.clone().cuda()
+    dv = hv.clone().cuda() if dual else None
+    ds = hs.clone().cuda()
+    code = {1: 1, 2: 2, 3: "T1", 4: "T2"}[buffer]
+    cfg = O.make_config(lr=1e-3, buffer=code, cautious=bool(cautious), bound_type=bound_mode, seed=77)
+    stream = torch.cuda.current_stream().cuda_stream
+    for t in range(1, 5):
+        g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32))
+        dg = g.cuda()
+        rc = L.lv_step_f32(dp.data_ptr(), dg.data_ptr(), dm.data_ptr(), dv.data_ptr() if dual else None, None,
+                           ds.data_ptr(), n, 1e-3, 0.9, 0.999, 1e-8, 0.08, 0.8, 0.3, buffer, cautious, bound_mode,
+                           0.05, t, 77, ctypes.c_void_p(stream))
+        assert rc == 0, L.lv_last_error()
+        O.step(cfg, [hp], [g], [hm], [hv], [None], [hs], [t], [0])
+        torch.cuda.synchronize()
+        assert_bitwise(hp, dp, f"step {t} p")
+        assert_bitwise(hm, dm, f"step {t} m")
+        if dual:
+            assert_bitwise(hv, dv, f"step {t} v")
+        assert_bitwise(hs, ds, f"step {t} scratch")
+
+
 if __name__ == "__main__":
     sys.exit(pytest.main([__file__, "-v"]))
