@@ -14,6 +14,7 @@ import struct
 import threading
 from typing import Any, Dict, List, Optional, Sequence
 
+import numpy as np
 import torch
 
 _LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib")
@@ -127,26 +128,33 @@ class _Workspace:
 
     def __init__(self) -> None:
         self._bufs: Dict[Any, torch.Tensor] = {}
+        self._ok: Dict[Any, int] = {}  # largest tensor count the device's buffer is known to fit
 
     def get(self, device: torch.device, n_tensors: int) -> torch.Tensor:
-        need = int(load_library().lv_workspace_bytes(max(1, n_tensors)))
         buf = self._bufs.get(device)
+        if buf is not None and self._ok[device] >= n_tensors:
+            return buf
+        need = int(load_library().lv_workspace_bytes(max(1, n_tensors)))
         if buf is None or buf.numel() < need:
             cap = max(need, 4096)
             buf = torch.zeros(cap, dtype=torch.uint8, device=device)
             self._bufs[device] = buf
+            self._ok[device] = 0
+        self._ok[device] = max(self._ok[device], n_tensors)
         return buf
 
     def discard(self, device: torch.device) -> None:
         """Drops the device's buffer: after a failed launch its count words may hold a partial
         launch's counts, so the next call starts from a fresh zero-filled one."""
         self._bufs.pop(device, None)
+        self._ok.pop(device, None)
 
 
 # lv_tensor packed little-endian: 6 pointers, numel, step, param_index, 4 x int32, index_base,
 # inactive, n_inactive (layout checked against the header by tests/test_c_abi.py).
 _TENSOR = struct.Struct("<6Q3Q4i3Q")
 _STEP_OFFSET = 7 * 8   # byte offset of lv_tensor.step
+assert _TENSOR.size % 8 == 0 and _STEP_OFFSET % 8 == 0
 _GRAD_OFFSET = 1 * 8   # byte offset of lv_tensor.grad
 _OK_DTYPES = frozenset(DTYPE_CODES)
 
@@ -156,11 +164,13 @@ class PreparedStep:
     swap a tensor's grad (same shape/dtype/device, contiguous; checked) and set step counters;
     everything else stays as validated."""
 
-    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index")
+    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index", "_steps")
 
     def __init__(self, buf: bytearray, n: int, device: torch.device, numels: List[int], gdtypes: List[Any]):
         self.buf = buf
         self.items = (LvTensor * n).from_buffer(buf) if n else None
+        # the step field of every record, as one strided u64 view of the packed buffer
+        self._steps = np.frombuffer(buf, dtype=np.uint64)[_STEP_OFFSET // 8::_TENSOR.size // 8] if n else None
         self.n = n
         self.device = device
         self.numels = numels
@@ -177,6 +187,10 @@ class PreparedStep:
 
     def set_step(self, i: int, step: int) -> None:
         struct.pack_into("<Q", self.buf, i * _TENSOR.size + _STEP_OFFSET, int(step))
+
+    def set_steps(self, steps: Sequence[int]) -> None:
+        """Step counter of every descriptor at once (len(steps) == n)."""
+        self._steps[:] = steps
 
 
 class HipStepper:
@@ -277,9 +291,13 @@ class HipStepper:
         lib = load_library()
         cfg = make_config(group)
         ws = self.workspace.get(prep.device, prep.n)
-        with torch.cuda.device(prep.device):
-            stream = torch.cuda.current_stream(prep.device).cuda_stream
+        if torch.cuda.current_device() == prep.index:
+            stream = torch.cuda.current_stream().cuda_stream
             rc = lib.lv_step_multi(ctypes.byref(cfg), prep.items, prep.n, ws.data_ptr(), ws.numel(), stream)
+        else:
+            with torch.cuda.device(prep.device):
+                stream = torch.cuda.current_stream(prep.device).cuda_stream
+                rc = lib.lv_step_multi(ctypes.byref(cfg), prep.items, prep.n, ws.data_ptr(), ws.numel(), stream)
         if rc != 0:
             msg = lib.lv_last_error().decode(errors="replace")
             if rc in (-1, -3):  # rejected before any launch: the workspace is untouched

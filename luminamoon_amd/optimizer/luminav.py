@@ -1064,10 +1064,12 @@ class LuminaV(Optimizer):
                     return False
                 e[2] = weakref.ref(g)
                 e[4] = g.data_ptr()
-        for k, e in enumerate(entries):
+        steps = []
+        for e in entries:
             st = e[3]
             s = int(st["step"]) + 1
             st["step"] = s
-            prep.set_step(k, s)
+            steps.append(s)
+        prep.set_steps(steps)
         self._stepper.launch(group, prep)
         return True
