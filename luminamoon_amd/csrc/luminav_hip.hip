@@ -1278,7 +1278,7 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
         return launch_one(fn, args, grid, kThreads, stream);
     }
     // unit launches, in pieces of at most kMaxGrid blocks (LV_MAX_GRID_BLOCKS lowers the cap, so
-    // tests can split small launches), then the slot fold
+    // tests can split small launches); a counting launch folds its counts in its last blocks
     args.xcds = device_xcds();
     // b / X == (b * recip) >> 40 for b < 2^23 = kMaxGrid and X <= 64: recip exceeds 2^40 / X by at
     // most 1, so the product exceeds b * 2^40 / X by less than b < 2^23, i.e. by < 2^-17 after the
