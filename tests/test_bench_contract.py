@@ -1,0 +1,58 @@
+"""bench.py's contract on the CPU: it refuses more than one GPU before touching a device, its
+workloads have BASELINE.json's shapes and byte counts, and its CPU-baseline leg reports the
+fields the bench line carries."""
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+import sys
+
+import bench
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], cwd=ROOT,
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 2
+    line = json.loads(res.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
+
+
+def test_workload_shapes_match_the_configs():
+    assert bench.N5 == 6_738_415_616  # Llama-7B shape, one bucket
+    assert bench.N4 == 953_223_168    # Llama-1B shape
+    assert bench.N3 == 123_570_432    # GPT-2 small
+    sizes = bench.cfg2_sizes()
+    assert len(sizes) == 64 and min(sizes) >= 1 and max(sizes) <= 2 ** 20 + 1
+    assert sum(sizes) == 3_514_803
+
+
+def test_bytes_per_param_follow_the_buffers():
+    """Each buffer read once and written once: p (read + write), g (read), m and v (read + write)."""
+    size = {"bf16": 2, "f32": 4}
+    for wl in bench.WORKLOADS.values():
+        ps = size[wl["pdt"]]
+        dual = wl["buffer"] in (2, "T2")
+        state = 4  # f32 m (and v)
+        assert wl["bytes_per_param"] == 3 * ps + 2 * state * (2 if dual else 1), wl["name"]
+
+
+def test_pmc_traffic_is_the_algorithmic_bytes_plus_the_count_atomics():
+    algorithmic = bench.N5 * 22
+    traffic = bench.pmc_traffic_bytes(5)
+    blocks = bench.N5 // 1024
+    assert abs(traffic - (algorithmic + 32 * blocks)) / algorithmic < 5e-4
+    assert bench.pmc_traffic_bytes(3) is None
+
+
+def test_cpu_baseline_reports_its_fields():
+    wl = dict(bench.WORKLOADS[3])
+    wl["n"] = 1 << 21
+    out = bench.cpu_baseline(wl, threads=2, target_s=0.3)
+    assert out["unit"] == "params/s" and out["cores"] == 2 and out["kind"] == "port"
+    assert out["value"] > 0 and out["gb_per_s"] > 0
+    assert "elements of the same workload" in out["sample"]
+    assert "AVX-512" in out["sample"] or "scalar core" in out["sample"]
