@@ -94,14 +94,15 @@ typedef struct lv_tensor {
 /* Library version, major*10000 + minor*100 + patch. */
 int lv_version(void);
 
-/* Bytes of device workspace lv_step_multi needs for n_tensors tensors: 16 bytes of counters per
- * tensor (rounded up to 256), a fixed 195 KiB of cautious mask-count words (48 tensors per
- * launch x 65 words x 64 bytes) and a fixed 1.5 MiB of radial-bound partial sums (48 tensors per
- * launch x 2048 blocks x 2 doubles). The caller allocates it once, zero-filled; the kernels
- * leave the counters and count slots zeroed again after every call (the partial slots need no
- * clearing), so it is reused from step to step. Calls that share one workspace must not
- * overlap. After a call that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way),
- * zero the workspace again before reusing it. */
+/* Bytes of device workspace lv_step_multi needs (the same for any n_tensors: the launches of a
+ * call reuse per-launch regions): 195 KiB of cautious mask-count words (48 tensors per launch x
+ * 65 words x 64 bytes) and 512 bytes of radial-fold tickets, which must be zero before a call,
+ * then 34 KiB of radial running sums and chunk records and 20 MiB of radial unit records (one
+ * launch piece of 2^20 units x 20 bytes), which need no clearing. The caller allocates it once,
+ * zero-filled; the kernels leave the count words and tickets zeroed again after every call, so it
+ * is reused from step to step. Calls that share one workspace must not overlap. After a call
+ * that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero the workspace again
+ * before reusing it. */
 size_t lv_workspace_bytes(int n_tensors);
 
 /*

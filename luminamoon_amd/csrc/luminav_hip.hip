@@ -10,14 +10,18 @@
 // tensor holds the exact total and finalises the 6-float scratch on the device, so a steady step
 // is one launch and needs no host synchronisation.
 //
-// Radial bound (counting passes only): a persistent grid walks the units grid-stride; the
-// squared-norm sums sum(u_eff^2) and sum(p^2) are accumulated from the f32 squares in f64 (per
-// thread, then a fixed-order wave/block reduction), each block stores its partial in a
-// workspace slot, and the block that completes a tensor (per-tensor ticket) folds the slots in
-// block order. The result (rounded to f32 once) is the exactly rounded sum up to f64 rounding,
-// and bitwise deterministic for a given grid. The reference's own f32 sums depend on its CPU
-// backend (16-lane order in reference_cpu/dual.rs:134-253 vs. AVX-512 reductions in
-// avx512/dual.rs), so radial results match it to its cross-backend tolerance, not bit for bit.
+// Radial bound (counting passes): the same unit launch, run in pieces of at most kRadialPiece
+// units. Each block sums sum(u_eff^2) and sum(p^2) of its unit from the f32 squares in f64 (per
+// thread, then a fixed-order wave/block reduction) and stores them, with its mask count, as the
+// unit's record in the workspace with plain stores; a fold launch after each piece (the kernel
+// boundary makes the records visible, so the streaming kernel needs no fence) sums the records
+// of each tensor in unit order, carries the tensor's running sum from piece to piece, and
+// finalises the scratch in the piece that holds the tensor's last unit. The result (rounded to
+// f32 once) is the exactly rounded sum up to f64 rounding, and bitwise deterministic on any
+// device (the summation tree depends only on the unit and piece sizes). The reference's own f32
+// sums depend on its CPU backend (16-lane order in reference_cpu/dual.rs:134-253 vs. AVX-512
+// reductions in avx512/dual.rs), so radial results match it to its cross-backend tolerance, not
+// bit for bit.
 //
 // Per-element arithmetic follows the reference's scalar core operation for operation
 // (optimizer/crates/luminav-core/src/reference_cpu/dual.rs, reference_cpu/tdclm.rs,
@@ -43,7 +47,6 @@ namespace lv {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kHalf = kThreads * 4;     // a thread owns 4 consecutive elements of each half
-constexpr int kPersistHalves = 2;            // halves per work unit of a persistent launch (2048)
 
 // Halves per work unit of a unit launch. With f32 state the step is HBM-bound and 1024-element
 // units stream best (measured in one process: T2 bf16/f32 23.2 vs 23.6 ms, T1 bf16/f32 2.17 vs
@@ -56,7 +59,6 @@ constexpr int unit_halves(int mode, int pt, int st) {
     return st == LV_DTYPE_F32 ? 1 : 2;
 }
 constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
-constexpr uint32_t kRadialMaxBlocks = 2048;  // grid cap of radial launches (workspace partial slots)
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
 constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
 constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-byte segment
@@ -66,6 +68,13 @@ constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-by
 constexpr int kTicketBits = 27;
 constexpr int kFoldBits = 7;
 constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
+// Radial counting launches: units per piece (one workspace record each: 2 doubles + a u32 count),
+// and unit records one fold block sums into a chunk record.
+constexpr uint32_t kRadialPiece = 1u << 20;
+constexpr uint32_t kFoldChunk = 1024;
+constexpr uint32_t kMaxChunks = kRadialPiece / kFoldChunk + kMaxDesc;  // chunks of one piece
+// A piece's mask count (<= kRadialPiece units x 2048 elements) fits the u32 chunk sums.
+static_assert((uint64_t)kRadialPiece * 2048u <= 0xFFFFFFFFull, "piece counts fit 32 bits");
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
@@ -96,6 +105,12 @@ struct Desc {
     const uint64_t *skip;
 };
 
+// Radial-bound sums of a run of units: sum u_eff^2, sum p^2 (f64), mask count.
+struct RadialSum {
+    double su, sp;
+    unsigned long long cnt, pad;
+};
+
 // Launch-uniform constants: hyper-parameters, per-step coefficients, tensor table.
 struct Args {
     float lr, b1, b2, omb1, omb2, b1sq, omb1sq, eps, lam, lam1, neg_lr_wd, ratio;
@@ -107,10 +122,15 @@ struct Args {
     uint32_t xcds;       // unit launches: XCDs the device dispatches workgroups over (>= 1)
     uint32_t xcd_q, xcd_r;  // unit launches: grid / xcds and grid % xcds of this launch
     int32_t ndesc;
+    uint32_t piece_units;  // radial launches: units of the current piece ([unit_base, + piece_units))
+    uint32_t pad_;
     uint64_t xcd_recip;  // unit launches: floor(2^40 / xcds) + 1, so b / xcds == (b * xcd_recip) >> 40
-    unsigned long long *counters;  // persistent launches: 2 per tensor (mask count, finished-unit ticket)
-    unsigned long long *slots;     // unit launches: kSlotWords count words per tensor
-    double *partials;              // radial: [tensor][block] pairs (sum u_eff^2, sum p^2)
+    unsigned long long *slots;    // non-radial counting launches: kSlotWords count words per tensor
+    unsigned long long *tickets;  // radial fold: finished chunks of the piece, per tensor (left zero)
+    RadialSum *run;               // radial fold: per tensor, the sums of the pieces folded so far
+    RadialSum *chunks;            // radial fold: one record per chunk of the piece
+    double *unit_sq;              // radial: per unit of the piece, (sum u_eff^2, sum p^2)
+    uint32_t *unit_cnt;           // radial: per unit of the piece, the mask count
     Desc d[kMaxDesc];
 };
 
@@ -573,13 +593,6 @@ __device__ void finalize_scratch(const Args &a, bool radial, const Desc &D, unsi
     s[5] = 0.0f;
 }
 
-struct BlockShared {
-    uint32_t cnt[kThreads / 64];
-    double su[kThreads / 64];
-    double sp[kThreads / 64];
-    uint32_t last;
-};
-
 // Butterfly sum over the 64 lanes; every lane ends with the same, order-fixed value.
 __device__ __forceinline__ double wave_sum(double x) {
 #pragma unroll
@@ -587,89 +600,48 @@ __device__ __forceinline__ double wave_sum(double x) {
     return x;
 }
 
-__device__ __forceinline__ double load_partial(const double *p) {
-    uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return __longlong_as_double((long long)b);
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
 }
 
-// End of a block's run over tensor t: block sums of the mask count (and of the radial squares),
-// then the per-tensor ticket; the block that completes the tensor folds the radial partials of
-// all blocks in block order and finalises the scratch.
-template <int MODE, int PASS>
-__device__ void flush_tensor(const Args &a, bool radial, int t, uint32_t t_begin, uint32_t n_units, uint32_t cnt,
-                             double su, double sp, uint32_t units_here, BlockShared &sh) {
+// Block-wide sums in a fixed order (lanes by butterfly, then the 4 waves in order); the result
+// is valid in thread 0, which reads the shared slots after the barrier: a second call by the
+// same block needs a barrier in between.
+struct BlockSums {
+    double su[kThreads / 64];
+    double sp[kThreads / 64];
+    uint32_t cnt[kThreads / 64];
+};
+
+__device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp, uint32_t &cnt) {
+    su = wave_sum(su);
+    sp = wave_sum(sp);
+    cnt = wave_sum(cnt);
     const int w = threadIdx.x >> 6;
-    const bool lane0 = (threadIdx.x & 63) == 0;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-    if (radial) {
-        su = wave_sum(su);
-        sp = wave_sum(sp);
-    }
-    if (lane0) {
-        sh.cnt[w] = cnt;
+    if ((threadIdx.x & 63) == 0) {
         sh.su[w] = su;
         sh.sp[w] = sp;
+        sh.cnt[w] = cnt;
     }
     __syncthreads();
-    unsigned long long *ctr = a.counters + 2 * t;
     if (threadIdx.x == 0) {
-        uint32_t tot = 0;
+        su = sh.su[0];
+        sp = sh.sp[0];
+        cnt = sh.cnt[0];
 #pragma unroll
-        for (int k = 0; k < kThreads / 64; k++) tot += sh.cnt[k];
-        if (tot) atomicAdd(&ctr[0], (unsigned long long)tot);
-        if (radial) {
-            double bu = 0.0, bp = 0.0;
-#pragma unroll
-            for (int k = 0; k < kThreads / 64; k++) {
-                bu += sh.su[k];
-                bp += sh.sp[k];
-            }
-            double *slot = a.partials + 2 * ((size_t)t * gridDim.x + blockIdx.x);
-            slot[0] = bu;
-            slot[1] = bp;
-        }
-        __threadfence();
-        unsigned long long prev = atomicAdd(&ctr[1], (unsigned long long)units_here);
-        sh.last = (prev + units_here == (unsigned long long)n_units) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (sh.last) {  // block-uniform
-        __threadfence();
-        double fu = 0.0, fp = 0.0;
-        if (radial) {
-            // Unit u is processed by block u % G, so the blocks that visited t are those of its
-            // first min(n_units, G) units.
-            const uint32_t G = gridDim.x;
-            const uint32_t nb = n_units < G ? n_units : G;
-            for (uint32_t k = threadIdx.x; k < nb; k += kThreads) {
-                const double *slot = a.partials + 2 * ((size_t)t * G + (t_begin + k) % G);
-                fu += load_partial(slot);
-                fp += load_partial(slot + 1);
-            }
-            fu = wave_sum(fu);
-            fp = wave_sum(fp);
-            if (lane0) {  // thread 0 finished reading sh.su / sh.sp before the barrier above
-                sh.su[w] = fu;
-                sh.sp[w] = fp;
-            }
-            __syncthreads();
-            fu = 0.0;
-            fp = 0.0;
-#pragma unroll
-            for (int k = 0; k < kThreads / 64; k++) {
-                fu += sh.su[k];
-                fp += sh.sp[k];
-            }
-        }
-        if (threadIdx.x == 0) {
-            unsigned long long total = atomicAdd(&ctr[0], 0ull);
-            finalize_scratch<MODE, PASS>(a, radial, a.d[t], total, (float)fu, (float)fp);
-            atomicExch(&ctr[0], 0ull);
-            atomicExch(&ctr[1], 0ull);
+        for (int k = 1; k < kThreads / 64; k++) {
+            su += sh.su[k];
+            sp += sh.sp[k];
+            cnt += sh.cnt[k];
         }
     }
-    __syncthreads();
+}
+
+__device__ __forceinline__ double load_relaxed(const double *p) {
+    uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __longlong_as_double((long long)b);
 }
 
 // ------------------------------------------------------------------ per-unit work
@@ -913,15 +885,17 @@ __device__ __forceinline__ void report_count(const Args &a, int t, const View &t
 // faster than any persistent grid-stride loop over the same buffers (measured: 23.4 vs 26.5 ms
 // for the 6.7e9-element T2 step; 2048-element units: 23.7 ms). Counting passes report each
 // block's exact mask count (report_count), and the last block of each tensor finalises its
-// scratch, so a step is one launch. Never used for radial counting.
+// scratch, so a step is one launch. Radial counting passes instead store each unit's record
+// (mask count and f64 squared-norm sums) for fold_kernel.
 // FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
 // which case every option test folds at compile time and the per-element code is straight-line.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL>
 __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
-    __shared__ uint32_t wcnt[kThreads / 64];
+    __shared__ BlockSums sh;
 
     const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
+    const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
     // Workgroups are dispatched to the XCDs round-robin (block b runs on XCD b mod X). Map them so
     // that each XCD streams one contiguous range of units (measured ~1% faster than b -> b).
     // Every block is short-lived, so its prologue is on the critical path: b / X comes from the
@@ -935,117 +909,130 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const Desc &D = a.d[t];
     const View tv = open_view<MODE, PASS>(a, D, t, flags, unit);
     uint32_t cnt = 0;
-    double su = 0.0, sp = 0.0;  // unused: radial sums run in step_kernel
+    double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
     int cover = 0;
     uint32_t first = 0;
     if (D.nskip) {
         const uint64_t e0 = (uint64_t)(unit - tv.t_begin) * (kHalf * H);
         cover = inactive_cover(D, e0, e0 + kHalf * H < tv.n ? e0 + kHalf * H : tv.n, first);
-        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing.
+        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
+        // its elements still enter the radial norms.
         if (!kCounting && cover == 2) return;
     }
     if (cover == 0 && tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
-        const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, false, unit);
+        const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, unit);
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
-        process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, f, unit, cnt, su, sp);
-    } else if (cover != 2) {
-        scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, false, unit, cnt, su, sp, cover ? D.nskip : 0, first);
+        process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, f, unit, cnt, su, sp);
+    } else if (cover != 2 || radial) {
+        scalar_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, unit, cnt, su, sp, cover ? D.nskip : 0, first);
     }
     if constexpr (kCounting) {
+        if (radial) {
+            block_sums(sh, su, sp, cnt);
+            if (threadIdx.x == 0) {
+                const uint32_t k = unit - a.unit_base;  // < piece_units
+                a.unit_sq[2 * (size_t)k] = su;
+                a.unit_sq[2 * (size_t)k + 1] = sp;
+                a.unit_cnt[k] = cnt;
+            }
+        } else {
+            cnt = wave_sum(cnt);
+            if ((threadIdx.x & 63) == 0) sh.cnt[threadIdx.x >> 6] = cnt;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                uint32_t tot = 0;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-        if ((threadIdx.x & 63) == 0) wcnt[threadIdx.x >> 6] = cnt;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t tot = 0;
-#pragma unroll
-            for (int k = 0; k < kThreads / 64; k++) tot += wcnt[k];
-            report_count<MODE, PASS>(a, t, tv, unit, tot);
+                for (int k = 0; k < kThreads / 64; k++) tot += sh.cnt[k];
+                report_count<MODE, PASS>(a, t, tv, unit, tot);
+            }
         }
     }
 }
 
-// Persistent launch (radial-bound counting passes): a grid of exactly the resident blocks walks
-// the unit space grid-stride, so every block that visited a tensor owns one deterministic radial
-// partial slot; the last block of each tensor (per-tensor ticket) folds the slots in block order
-// and finalises the scratch on the device.
-template <int MODE, int PT, int ST, int PASS, uint32_t FL>
-__global__ void __launch_bounds__(kThreads) step_kernel(const Args a) {
-    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
-    __shared__ BlockShared sh;
+// Units of tensor t inside the piece [ub, ue) of the launch's unit space: [lo, hi).
+__host__ __device__ inline void piece_span(const Args &a, int t, uint32_t ub, uint32_t ue, uint32_t &lo, uint32_t &hi) {
+    const uint32_t tb = a.d[t].unit_begin;
+    const uint32_t te = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+    lo = tb > ub ? tb : ub;
+    hi = te < ue ? te : ue;
+    if (hi < lo) hi = lo;
+}
 
-    const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
-    const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
-    const uint32_t total_units = a.total_units;
-
-    int t = -1;
-    View tv{};
-    uint32_t cnt = 0, units_here = 0;
-    double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
-
-    const uint32_t stride = gridDim.x;
-    uint32_t unit = blockIdx.x;
-    while (unit < total_units) {
-        // ---- switch to the tensor that owns `unit` (units of one tensor are contiguous)
-        if constexpr (kCounting) {
-            if (t >= 0)
-                flush_tensor<MODE, PASS>(a, radial, t, tv.t_begin, tv.t_end - tv.t_begin, cnt, su, sp, units_here, sh);
-        }
-        t = find_tensor(a, t + 1, unit);  // units only grow, so search right of t
-        const Desc &D = a.d[t];
-        tv = open_view<MODE, PASS>(a, D, t, flags, unit);
-        cnt = 0;
-        units_here = 0;
-        su = 0.0;
-        sp = 0.0;
-
-        // ---- whole, aligned units: software-pipelined vector path. The loads of the next
-        // unit are issued before the current unit is computed, so a wave always has one unit
-        // of HBM traffic in flight while it computes.
-        constexpr int H = kPersistHalves;
-        // tensors with inactive ranges take the per-element path (their elements still count)
-        const uint32_t full_end = (tv.vec_ok && D.nskip == 0) ? tv.t_begin + (uint32_t)(tv.n / (kHalf * H)) : tv.t_begin;
-        if (unit < full_end) {
-            // Two register buffers in ping-pong. The prefetch is unconditional (the last one of
-            // a run re-reads the current unit, in bounds and unused) so the wait counts are the
-            // same on every path and the compiler never has to drain the prefetch early.
-            Inflight A = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, unit);
-            for (;;) {
-                uint32_t next = unit + stride;
-                bool more = next < full_end;
-                Inflight B = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, more ? next : unit);
-                process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, A, unit, cnt, su, sp);
-                units_here++;
-                unit = next;
-                if (!more) break;
-                next = unit + stride;
-                more = next < full_end;
-                A = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, more ? next : unit);
-                process_unit<MODE, PT, ST, PASS, H>(a, D, tv, flags, radial, B, unit, cnt, su, sp);
-                units_here++;
-                unit = next;
-                if (!more) break;
-            }
-        }
-
-        // ---- the partial last unit and unaligned tensors: per-element path
-        for (; unit < tv.t_end; unit += stride) {
-            uint32_t first = 0;
-            int cover = 0;
-            if (D.nskip) {
-                const uint64_t e0 = (uint64_t)(unit - tv.t_begin) * (kHalf * kPersistHalves);
-                cover = inactive_cover(D, e0, e0 + kHalf * kPersistHalves < tv.n ? e0 + kHalf * kPersistHalves : tv.n, first);
-            }
-            scalar_unit<MODE, PT, ST, PASS, kPersistHalves>(a, D, tv, flags, radial, unit, cnt, su, sp,
-                                                            cover ? D.nskip : 0, first);
-            units_here++;
-        }
+// Radial fold, one launch after each piece of a radial counting launch. The piece's units are
+// cut, per tensor, into chunks of kFoldChunk; block j sums the unit records of chunk j in unit
+// order into chunk record j, and the block that completes a tensor's chunks (per-tensor ticket,
+// release/acquire fences: this grid is small and has little dirty L2 to write back) sums the
+// tensor's chunk records in order, adds them after the running sum of the earlier pieces, and
+// either stores the new running sum or, in the piece that holds the tensor's last unit,
+// finalises the scratch. Every sum runs in an order fixed by the unit and piece sizes.
+template <int MODE, int PASS>
+__global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
+    __shared__ BlockSums sh;
+    __shared__ uint32_t last;
+    const uint32_t ub = a.unit_base, ue = a.unit_base + a.piece_units;
+    uint32_t j = blockIdx.x, cbase = 0, lo = 0, hi = 0, nc = 0;
+    int t = 0;
+    for (; t < a.ndesc; t++) {  // block-uniform; the grid is exactly the piece's chunk count
+        piece_span(a, t, ub, ue, lo, hi);
+        nc = (hi - lo + kFoldChunk - 1) / kFoldChunk;
+        if (j < nc) break;
+        j -= nc;
+        cbase += nc;
     }
-    if constexpr (kCounting) {
-        if (t >= 0) flush_tensor<MODE, PASS>(a, radial, t, tv.t_begin, tv.t_end - tv.t_begin, cnt, su, sp, units_here, sh);
+    if (t == a.ndesc) return;
+    const uint32_t u0 = lo + j * kFoldChunk;
+    const uint32_t u1 = (hi - u0 > kFoldChunk) ? u0 + kFoldChunk : hi;
+    double su = 0.0, sp = 0.0;
+    uint32_t cnt = 0;
+    for (uint32_t u = u0 + threadIdx.x; u < u1; u += kThreads) {
+        const size_t k = u - ub;
+        su += a.unit_sq[2 * k];
+        sp += a.unit_sq[2 * k + 1];
+        cnt += a.unit_cnt[k];
+    }
+    block_sums(sh, su, sp, cnt);
+    if (threadIdx.x == 0) {
+        RadialSum *r = a.chunks + cbase + j;
+        r->su = su;
+        r->sp = sp;
+        r->cnt = cnt;
+        __threadfence();
+        const unsigned long long prev = atomicAdd(&a.tickets[t], 1ull);
+        last = (prev + 1ull == (unsigned long long)nc) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;  // block-uniform
+    __threadfence();
+    su = 0.0;
+    sp = 0.0;
+    cnt = 0;
+    for (uint32_t k = threadIdx.x; k < nc; k += kThreads) {
+        const RadialSum *r = a.chunks + cbase + k;
+        su += load_relaxed(&r->su);
+        sp += load_relaxed(&r->sp);
+        cnt += (uint32_t)__hip_atomic_load(&r->cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    block_sums(sh, su, sp, cnt);
+    if (threadIdx.x == 0) {
+        RadialSum &run = a.run[t];
+        unsigned long long total = cnt;
+        if (lo != a.d[t].unit_begin) {  // earlier pieces hold the tensor's first units
+            su = run.su + su;
+            sp = run.sp + sp;
+            total += run.cnt;
+        }
+        const uint32_t te = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+        if (hi == te) {
+            finalize_scratch<MODE, PASS>(a, true, a.d[t], total, (float)su, (float)sp);
+        } else {
+            run.su = su;
+            run.sp = sp;
+            run.cnt = total;
+        }
+        __hip_atomic_store(&a.tickets[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1061,28 +1048,18 @@ constexpr uint32_t static_flags(int PT, int PASS) {
            (uint32_t)kFCoordinate | (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8);
 }
 
-// The same defaults with bound_type="radial" (the radial passes never run SINGLE). Runtime flags
-// leave the persistent radial kernel at 175 VGPRs (2 waves/SIMD); specialised it holds 118 (4
-// waves/SIMD) and measured 11% faster on the cfg5 shape (25.7 vs 28.9 ms).
+// The same defaults with bound_type="radial" (the radial passes never run SINGLE).
 constexpr uint32_t radial_flags(int PT) {
     return ((uint32_t)kFCautious | (uint32_t)kFSR | (uint32_t)kFWeightDecay | (uint32_t)kFRadial |
             (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8));
 }
 
-// Radial-bound counting passes run persistent (deterministic partial slots); everything else
-// runs as a unit launch.
 template <int MODE, int PT, int ST, int PASS>
 KernelFn pick_flags(uint32_t flags) {
     constexpr uint32_t kStatic = static_flags(PT, PASS);
     constexpr uint32_t kRadial = radial_flags(PT);
-    if constexpr (PASS == kFused || PASS == kCount) {
-        if (flags & kFRadial)
-            return flags == kRadial ? step_kernel<MODE, PT, ST, PASS, kRadial> : step_kernel<MODE, PT, ST, PASS, kFDynamic>;
-    }
     if (flags == kStatic) return unit_kernel<MODE, PT, ST, PASS, kStatic>;
-    if constexpr (PASS == kApply) {
-        if (flags == kRadial) return unit_kernel<MODE, PT, ST, PASS, kRadial>;
-    }
+    if (flags == kRadial) return unit_kernel<MODE, PT, ST, PASS, kRadial>;
     return unit_kernel<MODE, PT, ST, PASS, kFDynamic>;
 }
 
@@ -1117,6 +1094,20 @@ static KernelFn pick_kernel(int mode, int pt, int st, int pass, uint32_t flags) 
     case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass, flags);
     case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass, flags);
     default: return pick_param<LV_BUFFER_T2>(pt, st, pass, flags);
+    }
+}
+
+template <int MODE>
+KernelFn pick_fold_pass(int pass) {
+    return pass == kFused ? fold_kernel<MODE, kFused> : fold_kernel<MODE, kCount>;
+}
+
+static KernelFn pick_fold(int mode, int pass) {
+    switch (mode) {
+    case LV_BUFFER_TDCLM: return pick_fold_pass<LV_BUFFER_TDCLM>(pass);
+    case LV_BUFFER_DUAL: return pick_fold_pass<LV_BUFFER_DUAL>(pass);
+    case LV_BUFFER_T1: return pick_fold_pass<LV_BUFFER_T1>(pass);
+    default: return pick_fold_pass<LV_BUFFER_T2>(pass);
     }
 }
 
@@ -1189,37 +1180,6 @@ static int validate_config(const lv_config *c) {
     return LV_STATUS_SUCCESS;
 }
 
-// Persistent grid: exactly the blocks that can be resident at once (CUs x occupancy), so no
-// block waits for another to finish and the grid-stride loop has no tail round.
-static uint32_t resident_blocks(KernelFn fn) {
-    struct Entry {
-        int dev;
-        KernelFn fn;
-        uint32_t blocks;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    std::lock_guard<std::mutex> lk(mu);
-    for (const Entry &e : cache)
-        if (e.dev == dev && e.fn == fn) return e.blocks;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), kThreads, 0) !=
-            hipSuccess ||
-        per_cu <= 0)
-        per_cu = 4;
-    if (const char *e = std::getenv("LV_BLOCKS_PER_CU")) {
-        int v = std::atoi(e);
-        if (v > 0 && v <= 64) per_cu = v;
-    }
-    uint32_t blocks = (uint32_t)cus * (uint32_t)per_cu;
-    cache.push_back({dev, fn, blocks});
-    return blocks;
-}
-
 // XCDs of the current device (hipDeviceAttributeNumberOfXccs; 1 if unknown).
 static uint32_t device_xcds() {
     static std::mutex mu;
@@ -1265,38 +1225,45 @@ static int assign_units(Args &args, uint32_t unit_elems) {
 
 static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
     KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags);
-    const bool counting = pass == kFused || pass == kCount;
-    const bool persistent = counting && (args.flags & kFRadial);
-    int rc = assign_units(args, kHalf * (persistent ? kPersistHalves : unit_halves(mode, pt, st)));
+    const bool radial = (pass == kFused || pass == kCount) && (args.flags & kFRadial);
+    int rc = assign_units(args, kHalf * unit_halves(mode, pt, st));
     if (rc != LV_STATUS_SUCCESS) return rc;
     if (args.total_units == 0) return LV_STATUS_SUCCESS;
-    if (persistent) {
-        // persistent: at most kRadialMaxBlocks blocks (the partial slots per tensor)
-        uint32_t grid = std::min<uint32_t>(args.total_units, resident_blocks(fn));
-        grid = std::min<uint32_t>(grid, kRadialMaxBlocks);
-        args.unit_base = 0;
-        return launch_one(fn, args, grid, kThreads, stream);
-    }
-    // unit launches, in pieces of at most kMaxGrid blocks (LV_MAX_GRID_BLOCKS lowers the cap, so
-    // tests can split small launches); a counting launch folds its counts in its last blocks
+    // Unit launches, in pieces of at most kMaxGrid blocks (kRadialPiece for radial counting, the
+    // records of one piece; LV_MAX_GRID_BLOCKS lowers the cap, so tests can split small launches).
+    // A counting launch folds its counts in its last blocks; a radial one runs fold_kernel after
+    // every piece.
     args.xcds = device_xcds();
     // b / X == (b * recip) >> 40 for b < 2^23 = kMaxGrid and X <= 64: recip exceeds 2^40 / X by at
     // most 1, so the product exceeds b * 2^40 / X by less than b < 2^23, i.e. by < 2^-17 after the
     // shift, while the fraction of b / X is at most 1 - 1/X <= 1 - 2^-6.
     static_assert(kMaxGrid <= (1u << 23), "the reciprocal is exact for grids up to 2^23 blocks");
+    static_assert(kRadialPiece <= kMaxGrid, "a radial piece is one unit launch");
     args.xcd_recip = ((uint64_t)1 << 40) / args.xcds + 1;
-    uint32_t max_grid = kMaxGrid;
+    uint32_t max_grid = radial ? kRadialPiece : kMaxGrid;
     if (const char *e = std::getenv("LV_MAX_GRID_BLOCKS")) {
         long v = std::atol(e);
-        if (v > 0 && (uint32_t)v < kMaxGrid) max_grid = (uint32_t)v;
+        if (v > 0 && (uint32_t)v < max_grid) max_grid = (uint32_t)v;
     }
+    KernelFn fold = radial ? pick_fold(mode, pass) : nullptr;
     for (uint32_t ub = 0; ub < args.total_units; ub += std::min<uint32_t>(max_grid, args.total_units - ub)) {
         const uint32_t grid = std::min<uint32_t>(max_grid, args.total_units - ub);
         args.unit_base = ub;
+        args.piece_units = grid;
         args.xcd_q = grid / args.xcds;
         args.xcd_r = grid % args.xcds;
         rc = launch_one(fn, args, grid, kThreads, stream);
         if (rc != LV_STATUS_SUCCESS) return rc;
+        if (radial) {
+            uint32_t chunks = 0;
+            for (int t = 0; t < args.ndesc; t++) {
+                uint32_t lo, hi;
+                piece_span(args, t, ub, ub + grid, lo, hi);
+                chunks += (hi - lo + kFoldChunk - 1) / kFoldChunk;
+            }
+            rc = launch_one(fold, args, chunks, kThreads, stream);
+            if (rc != LV_STATUS_SUCCESS) return rc;
+        }
     }
     args.unit_base = 0;
     return LV_STATUS_SUCCESS;
@@ -1310,19 +1277,26 @@ extern "C" {
 
 int lv_version(void) { return 100; }
 
-// Layout: [2 u64 counters per tensor, padded to 256 B][count words: kMaxDesc x kSlotWords words,
-// 64 B apart][radial partials: kMaxDesc x kRadialMaxBlocks x 2 doubles]. The words and partials
-// are reused by every launch of a call (stream-ordered); each launch leaves its words zeroed.
-static size_t counter_bytes(int n_tensors) {
-    size_t b = (size_t)n_tensors * 2 * sizeof(unsigned long long);
-    return (b + 255) & ~(size_t)255;
-}
-
+// Layout (every region a multiple of 256 B):
+//   [count words: kMaxDesc x kSlotWords words, 64 B apart][radial tickets: kMaxDesc u64, 512 B]
+//     -- kZeroBytes that must be zero before a call; every launch leaves them zeroed again --
+//   [radial running sums: kMaxDesc RadialSum][chunk records: kMaxChunks RadialSum]
+//   [unit records: kRadialPiece x (2 doubles)][unit counts: kRadialPiece x u32]
+// Everything is reused by every launch of a call (stream-ordered).
 static constexpr size_t kSlotBytes = (size_t)lv::kMaxDesc * lv::kSlotWords * lv::kSlotStride * sizeof(unsigned long long);
+static constexpr size_t kTicketBytes = 512;
+static constexpr size_t kZeroBytes = kSlotBytes + kTicketBytes;
+static constexpr size_t kRunBytes = (size_t)lv::kMaxDesc * sizeof(lv::RadialSum);
+static constexpr size_t kChunkBytes = (size_t)lv::kMaxChunks * sizeof(lv::RadialSum);
+static constexpr size_t kUnitSqBytes = (size_t)lv::kRadialPiece * 2 * sizeof(double);
+static constexpr size_t kUnitCntBytes = (size_t)lv::kRadialPiece * sizeof(uint32_t);
+static_assert(kSlotBytes % 256 == 0 && kRunBytes % 256 == 0 && kChunkBytes % 256 == 0, "region alignment");
+static_assert(lv::kMaxDesc * sizeof(unsigned long long) <= kTicketBytes, "ticket region");
+static_assert(sizeof(lv::RadialSum) == 32, "radial record layout");
 
 size_t lv_workspace_bytes(int n_tensors) {
-    if (n_tensors < 1) n_tensors = 1;
-    return counter_bytes(n_tensors) + kSlotBytes + (size_t)lv::kMaxDesc * lv::kRadialMaxBlocks * 2 * sizeof(double);
+    (void)n_tensors;  // launches of a call reuse the same per-launch regions
+    return kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes + kUnitCntBytes;
 }
 
 const char *lv_last_error(void) { return lv::g_err; }
@@ -1396,7 +1370,6 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     });
 
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    unsigned long long *ctr = static_cast<unsigned long long *>(workspace);
     size_t begin = 0;
     while (begin < items.size()) {
         const Item &h = items[begin];
@@ -1457,9 +1430,13 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             D.nskip = (uint32_t)T.n_inactive;
             D.skip = T.n_inactive ? T.inactive : nullptr;
         }
-        args.counters = ctr + 2 * begin;  // slots [begin, end) of this call's workspace
-        args.slots = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace) + counter_bytes(count));
-        args.partials = reinterpret_cast<double *>(static_cast<char *>(workspace) + counter_bytes(count) + kSlotBytes);
+        char *ws = static_cast<char *>(workspace);
+        args.slots = reinterpret_cast<unsigned long long *>(ws);
+        args.tickets = reinterpret_cast<unsigned long long *>(ws + kSlotBytes);
+        args.run = reinterpret_cast<RadialSum *>(ws + kZeroBytes);
+        args.chunks = reinterpret_cast<RadialSum *>(ws + kZeroBytes + kRunBytes);
+        args.unit_sq = reinterpret_cast<double *>(ws + kZeroBytes + kRunBytes + kChunkBytes);
+        args.unit_cnt = reinterpret_cast<uint32_t *>(ws + kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes);
         if (h.pass == kCount) {
             rc = launch(args, cfg->buffer, h.pt, h.st, kCount, stream);
             if (rc == LV_STATUS_SUCCESS) rc = launch(args, cfg->buffer, h.pt, h.st, kApply, stream);

@@ -7,13 +7,13 @@ AVX-512 reductions), and its own cross-backend test accepts 1.5e-6 absolute
 (luminav-simd/tests/differential_parity.rs:16). Two bars here:
   * bit for bit against the oracle in its f64 sum mode (same per-element values, same sums up to
     f64 rounding): every option combination, ragged multi-tensor calls, more tensors than one
-    launch holds, tensors with more work units than the grid has blocks;
+    launch holds, tensors summed over several fold chunks and launch pieces;
   * against the oracle in the scalar core's f32 order, on the reference's own differential-parity
     configurations and inputs: m and v bitwise (the scale never feeds them), fp32 params within
     1.5e-6, bf16 params within 1 ULP on a small fraction of elements (a stochastic-rounding
     decision near its threshold can flip when the scale moves in its last bits), the bound scale
     within the f32 summation bound (adds per lane x 2^-24).
-The same call twice gives identical bits (fixed-order fold of the block partials).
+The same call twice gives identical bits (fixed-order fold of the unit records).
 """
 from __future__ import annotations
 
@@ -40,7 +40,12 @@ def _stepper():
     return HipStepper()
 
 
-def _run_bitwise(O, sizes, pdt, gdt, sdt, steps=4, seed=31, threads=1, **gkw):
+# Leading workspace bytes that must be zero between calls: 48 x 65 count words 64 B apart, then
+# the radial fold's 512 B of per-tensor tickets (the rest holds records and needs no clearing).
+WORKSPACE_ZERO_BYTES = 48 * 65 * 64 + 512
+
+
+def _run_bitwise(O, sizes, pdt, gdt, sdt, steps=4, seed=31, threads=1, check_workspace=False, **gkw):
     _need_gpu()
     group = group_dict(bound_type="radial", **gkw)
     dual = group["buffer"] in (2, "T2")
@@ -58,6 +63,9 @@ def _run_bitwise(O, sizes, pdt, gdt, sdt, steps=4, seed=31, threads=1, **gkw):
             dev.hip_step(st, group, [g.cuda() for g in grads], s)
             torch.cuda.synchronize()
             host.assert_equal(dev, f"{label} step {s}")
+            if check_workspace:
+                for ws in st.workspace._bufs.values():
+                    assert int(torch.count_nonzero(ws[:WORKSPACE_ZERO_BYTES])) == 0, f"{label} step {s}: words left set"
     return host
 
 
@@ -87,12 +95,27 @@ def test_radial_bitwise_vs_oracle_f64_sums(oracle_mod, buffer, pdt, gdt, sdt, ex
     assert float(host.sc[-1][4]) < 0.999
 
 
-def test_radial_many_tensors_and_more_units_than_blocks(oracle_mod):
-    """64 tensors (two launches sharing the workspace partial slots) and one tensor with more
-    work units (2,442 of 2,048 elements) than a radial launch has blocks."""
+def test_radial_many_tensors_and_several_fold_chunks(oracle_mod):
+    """64 tensors (two launches sharing the workspace records and tickets) and one tensor of
+    4,883 work units, whose records the fold sums in five chunks."""
     rng = np.random.default_rng(9)
     sizes = [int(np.exp(rng.uniform(0, np.log(2 ** 14)))) + 1 for _ in range(62)] + [5_000_003, 70_001]
     _run_bitwise(oracle_mod, sizes, "bf16", "bf16", "f32", steps=3, threads=8, buffer="T2", lr=1e-3)
+
+
+@pytest.mark.parametrize("cap", ["7", "1500"])
+def test_radial_launch_split_into_pieces(oracle_mod, monkeypatch, cap):
+    """A radial counting launch runs in pieces (at most 2^20 units, one workspace record each)
+    with a fold launch after each; a tensor's running sums carry from piece to piece and the
+    piece holding its last unit finalises the scratch. LV_MAX_GRID_BLOCKS lowers the piece size:
+    7 units (tensors spanning hundreds of pieces, pieces spanning tensors) and 1,500 units (a
+    tensor's part of a piece spans two fold chunks). Bitwise against the oracle's f64 sums over
+    the two-pass first step and the fused steps, and the count words and tickets are left zero."""
+    monkeypatch.setenv("LV_MAX_GRID_BLOCKS", cap)
+    _run_bitwise(oracle_mod, [100_003, 5, 66_000, 2048, 1, 3_000_001], "bf16", "bf16", "f32", steps=3,
+                 check_workspace=True, buffer="T2", lr=1e-3)
+    _run_bitwise(oracle_mod, [70_001, 2_100_000], "f32", "f32", "f32", steps=2, check_workspace=True, buffer=1,
+                 lam=0.3, cautious=False, lr=1e-3)
 
 
 def test_radial_is_deterministic(oracle_mod):
