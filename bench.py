@@ -68,7 +68,26 @@ PMC_TRAFFIC = {
 }
 
 
-def pmc_traffic_bytes(config: int):
+def workload(config: int, bound: str = "coordinate", state: str = "fp32") -> dict:
+    """The workload of `config` with the bound type and state precision of the run. state="param"
+    keeps m/v in the param dtype (the reference's Python default for 16-bit params), which changes
+    the bytes per param: a bf16 m or v moves 2 + 2 bytes instead of 4 + 4."""
+    wl = dict(WORKLOADS[config])
+    wl["bound"] = bound
+    wl["state"] = state
+    wl["sdt"] = wl["pdt"] if state == "param" else "f32"
+    if wl["sdt"] != "f32":
+        per_state = 4  # read + write of one 16-bit state element
+        n_state = 2 if wl["buffer"] in (2, "T2") else 1
+        wl["bytes_per_param"] -= n_state * (8 - per_state)
+    if bound != "coordinate" or state != "fp32":
+        wl["name"] += f" [bound={bound}, state={state}]"
+    return wl
+
+
+def pmc_traffic_bytes(config: int, bound: str = "coordinate", state: str = "fp32"):
+    if bound != "coordinate" or state != "fp32":
+        return None  # the counter runs were taken on the default workload
     t = PMC_TRAFFIC.get(config)
     if t is None:
         return None
@@ -152,7 +171,9 @@ def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
 
 def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: float) -> dict:
     pdt = torch.bfloat16 if workload["pdt"] == "bf16" else torch.float32
-    cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"])
+    sdt = torch.bfloat16 if workload.get("sdt", "f32") == "bf16" else torch.float32
+    cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"],
+                        bound_type=1 if workload.get("bound") == "radial" else 2)
     dual = workload["buffer"] in (2, "T2")
 
     def make(n, seed=5):
@@ -162,8 +183,8 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
         k = min(n, 1 << 24)
         p = torch.from_numpy(np.resize((rng.standard_normal(k) * 0.02).astype(np.float32), n)).to(pdt)
         g = torch.from_numpy(np.resize((rng.standard_normal(k) * 1e-3).astype(np.float32), n)).to(pdt)
-        m = torch.zeros(n)
-        v = torch.zeros(n) if dual else None
+        m = torch.zeros(n, dtype=sdt)
+        v = torch.zeros(n, dtype=sdt) if dual else None
         sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
         return p, g, m, v, sc
 
@@ -233,6 +254,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=5, choices=sorted(WORKLOADS))
+    ap.add_argument("--bound", default="coordinate", choices=("coordinate", "radial"),
+                    help="bound_type of the optimizer (the configs use the default, coordinate)")
+    ap.add_argument("--state", default="fp32", choices=("fp32", "param"),
+                    help="state_precision: fp32 m/v (the configs) or the param dtype (reference Python default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-reserve", action="store_true", help="skip the HBM reserve/release before allocating")
@@ -252,12 +277,12 @@ def main() -> int:
     if not torch.cuda.is_available():
         log("no GPU visible")
         return 1
-    wl = WORKLOADS[args.config]
+    wl = workload(args.config, args.bound, args.state)
     pdt = torch.bfloat16 if wl["pdt"] == "bf16" else torch.float32
     sizes = wl.get("sizes", [wl.get("n", 0)])
     n = sum(sizes)
     free, total = torch.cuda.mem_get_info()
-    state_b = 4 * n * (2 if wl["buffer"] in (2, "T2") else 1)
+    state_b = (4 if wl["sdt"] == "f32" else 2) * n * (2 if wl["buffer"] in (2, "T2") else 1)
     need = n * (2 if pdt == torch.bfloat16 else 4) * 2 + state_b
     log(f"workload {wl['name']}: n={n}, resident {need / 1e9:.1f} GB, free {free / 1e9:.1f} GB")
     if need + (8 << 30) > free:
@@ -282,7 +307,8 @@ def main() -> int:
         p.grad = g_data
         params.append(p)
     del p_data, g_data
-    opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"])
+    opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"], bound_type=args.bound,
+                  state_precision=args.state)
     torch.cuda.synchronize()
     log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
 
@@ -344,8 +370,9 @@ def main() -> int:
             "params": n,
             "tensors": len(sizes),
             "param_dtype": wl["pdt"],
-            "state_dtype": "f32",
+            "state_dtype": wl["sdt"],
             "cautious": wl["cautious"],
+            "bound_type": args.bound,
             "bytes_per_param": wl["bytes_per_param"],
         },
         "achieved_gb_per_s": achieved,
@@ -357,7 +384,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": pmc_traffic_bytes(args.config),
+            "traffic": pmc_traffic_bytes(args.config, args.bound, args.state),
         },
         "cpu_baseline": cpu,
     }

@@ -97,8 +97,8 @@ int lv_version(void);
 /* Bytes of device workspace lv_step_multi needs (the same for any n_tensors: the launches of a
  * call reuse per-launch regions): 195 KiB of cautious mask-count words (48 tensors per launch x
  * 65 words x 64 bytes) and 512 bytes of radial-fold tickets, which must be zero before a call,
- * then 34 KiB of radial running sums and chunk records and 20 MiB of radial unit records (one
- * launch piece of 2^20 units x 20 bytes), which need no clearing. The caller allocates it once,
+ * then 35 KiB of radial running sums and chunk records and 80 MiB of radial unit records (one
+ * launch piece of 2^22 units x 20 bytes), which need no clearing. The caller allocates it once,
  * zero-filled; the kernels leave the count words and tickets zeroed again after every call, so it
  * is reused from step to step. Calls that share one workspace must not overlap. After a call
  * that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero the workspace again

@@ -70,11 +70,13 @@ constexpr int kFoldBits = 7;
 constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
 // Radial counting launches: units per piece (one workspace record each: 2 doubles + a u32 count),
 // and unit records one fold block sums into a chunk record.
-constexpr uint32_t kRadialPiece = 1u << 20;
-constexpr uint32_t kFoldChunk = 1024;
+constexpr uint32_t kRadialPiece = 1u << 22;
+constexpr uint32_t kFoldChunk = 4096;  // fold blocks per full piece: kRadialPiece / kFoldChunk
+constexpr int kFoldBatch = 16;         // unit records a fold thread loads before adding them
 constexpr uint32_t kMaxChunks = kRadialPiece / kFoldChunk + kMaxDesc;  // chunks of one piece
-// A piece's mask count (<= kRadialPiece units x 2048 elements) fits the u32 chunk sums.
-static_assert((uint64_t)kRadialPiece * 2048u <= 0xFFFFFFFFull, "piece counts fit 32 bits");
+// A chunk's mask count (<= kFoldChunk units x 2048 elements) fits the u32 chunk sums; the
+// sums over chunks run in u64.
+static_assert((uint64_t)kFoldChunk * 2048u <= 0xFFFFFFFFull, "chunk counts fit 32 bits");
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
@@ -506,8 +508,11 @@ __device__ __forceinline__ void decode_raw_dyn(int dt, const Raw8 &r, float out[
 }
 
 // The loads of one work unit that are in flight while the previous unit computes.
+// p holds the param or, with master weights, the f32 master: one field for both, so that the
+// run-time choice never becomes a select between two register arrays (which the compiler would
+// place in scratch memory).
 struct Inflight {
-    Raw8 p, g, m, v, mp;
+    Raw8 p, g, m, v;
 };
 
 // ------------------------------------------------------------------ element update
@@ -606,16 +611,27 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
     return x;
 }
 
+__device__ __forceinline__ unsigned long long wave_sum(unsigned long long x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)x, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), off, 64);
+        x += ((unsigned long long)hi << 32) | lo;
+    }
+    return x;
+}
+
 // Block-wide sums in a fixed order (lanes by butterfly, then the 4 waves in order); the result
 // is valid in thread 0, which reads the shared slots after the barrier: a second call by the
 // same block needs a barrier in between.
 struct BlockSums {
     double su[kThreads / 64];
     double sp[kThreads / 64];
-    uint32_t cnt[kThreads / 64];
+    unsigned long long cnt[kThreads / 64];
 };
 
-__device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp, uint32_t &cnt) {
+template <typename C>
+__device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp, C &cnt) {
     su = wave_sum(su);
     sp = wave_sum(sp);
     cnt = wave_sum(cnt);
@@ -629,12 +645,12 @@ __device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp
     if (threadIdx.x == 0) {
         su = sh.su[0];
         sp = sh.sp[0];
-        cnt = sh.cnt[0];
+        cnt = (C)sh.cnt[0];
 #pragma unroll
         for (int k = 1; k < kThreads / 64; k++) {
             su += sh.su[k];
             sp += sh.sp[k];
-            cnt += sh.cnt[k];
+            cnt += (C)sh.cnt[k];
         }
     }
 }
@@ -700,7 +716,7 @@ __device__ __forceinline__ Inflight issue_unit(const Desc &D, const View &tv, ui
     f.m = load_raw<ST, H>(D.m, e);
     if constexpr (kDual) f.v = load_raw<ST, H>(D.v, e);
     if (PASS != kCount || radial) {  // the count pass reads p only for the radial norm
-        if (flags & kFMaster) f.mp = load_raw<LV_DTYPE_F32, H>(D.mp, e);
+        if (flags & kFMaster) f.p = load_raw<LV_DTYPE_F32, H>(D.mp, e);
         else f.p = load_raw<PT, H>(D.p, e);
     }
     return f;
@@ -722,7 +738,7 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
     if constexpr (PASS == kCount) {
         float pin[8];
         if (radial) {
-            if (master) decode_raw<LV_DTYPE_F32, H>(cur.mp, pin);
+            if (master) decode_raw<LV_DTYPE_F32, H>(cur.p, pin);
             else decode_raw<PT, H>(cur.p, pin);
         }
 #pragma unroll
@@ -736,7 +752,7 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
         }
     } else {
         float pin[8], pout[8], mpout[8];
-        if (master) decode_raw<LV_DTYPE_F32, H>(cur.mp, pin);
+        if (master) decode_raw<LV_DTYPE_F32, H>(cur.p, pin);
         else decode_raw<PT, H>(cur.p, pin);
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
@@ -945,7 +961,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
             if (threadIdx.x == 0) {
                 uint32_t tot = 0;
 #pragma unroll
-                for (int k = 0; k < kThreads / 64; k++) tot += sh.cnt[k];
+                for (int k = 0; k < kThreads / 64; k++) tot += (uint32_t)sh.cnt[k];
                 report_count<MODE, PASS>(a, t, tv, unit, tot);
             }
         }
@@ -962,12 +978,14 @@ __host__ __device__ inline void piece_span(const Args &a, int t, uint32_t ub, ui
 }
 
 // Radial fold, one launch after each piece of a radial counting launch. The piece's units are
-// cut, per tensor, into chunks of kFoldChunk; block j sums the unit records of chunk j in unit
-// order into chunk record j, and the block that completes a tensor's chunks (per-tensor ticket,
-// release/acquire fences: this grid is small and has little dirty L2 to write back) sums the
-// tensor's chunk records in order, adds them after the running sum of the earlier pieces, and
-// either stores the new running sum or, in the piece that holds the tensor's last unit,
-// finalises the scratch. Every sum runs in an order fixed by the unit and piece sizes.
+// cut, per tensor, into chunks of kFoldChunk; block j sums the unit records of chunk j into
+// chunk record j (thread k adds records k, k + 256, ... in order, kFoldBatch loads in flight,
+// then the fixed block order), and the block that completes a tensor's chunks (per-tensor
+// ticket, release/acquire fences: <= 1072 blocks per piece, after a kernel boundary that already
+// wrote the L2 back) sums the tensor's chunk records in order, adds them after the running sum
+// of the earlier pieces, and either stores the new running sum or, in the piece that holds the
+// tensor's last unit, finalises the scratch. Every sum runs in an order fixed by the unit and
+// piece sizes.
 template <int MODE, int PASS>
 __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
     __shared__ BlockSums sh;
@@ -987,11 +1005,26 @@ __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
     const uint32_t u1 = (hi - u0 > kFoldChunk) ? u0 + kFoldChunk : hi;
     double su = 0.0, sp = 0.0;
     uint32_t cnt = 0;
-    for (uint32_t u = u0 + threadIdx.x; u < u1; u += kThreads) {
-        const size_t k = u - ub;
-        su += a.unit_sq[2 * k];
-        sp += a.unit_sq[2 * k + 1];
-        cnt += a.unit_cnt[k];
+    const uint32_t k0 = u0 - ub, k1 = u1 - ub;  // piece-relative record indices, <= kRadialPiece
+    const double2 *sq = reinterpret_cast<const double2 *>(a.unit_sq);
+    for (uint32_t kb = k0; kb < k1; kb += kFoldBatch * kThreads) {  // block-uniform
+        double2 x[kFoldBatch];
+        uint32_t c[kFoldBatch];
+#pragma unroll
+        for (int r = 0; r < kFoldBatch; r++) {
+            const uint32_t k = kb + r * kThreads + threadIdx.x;
+            const uint32_t kc = k < k1 ? k : k0;  // always in range, so every load can issue at once
+            x[r] = sq[kc];
+            c[r] = a.unit_cnt[kc];
+        }
+#pragma unroll
+        for (int r = 0; r < kFoldBatch; r++) {
+            if (kb + r * kThreads + threadIdx.x < k1) {
+                su += x[r].x;
+                sp += x[r].y;
+                cnt += c[r];
+            }
+        }
     }
     block_sums(sh, su, sp, cnt);
     if (threadIdx.x == 0) {
@@ -1008,17 +1041,16 @@ __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
     __threadfence();
     su = 0.0;
     sp = 0.0;
-    cnt = 0;
+    unsigned long long total = 0;
     for (uint32_t k = threadIdx.x; k < nc; k += kThreads) {
         const RadialSum *r = a.chunks + cbase + k;
         su += load_relaxed(&r->su);
         sp += load_relaxed(&r->sp);
-        cnt += (uint32_t)__hip_atomic_load(&r->cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        total += __hip_atomic_load(&r->cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    block_sums(sh, su, sp, cnt);
+    block_sums(sh, su, sp, total);
     if (threadIdx.x == 0) {
         RadialSum &run = a.run[t];
-        unsigned long long total = cnt;
         if (lo != a.d[t].unit_begin) {  // earlier pieces hold the tensor's first units
             su = run.su + su;
             sp = run.sp + sp;

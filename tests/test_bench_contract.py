@@ -40,6 +40,17 @@ def test_bytes_per_param_follow_the_buffers():
         assert wl["bytes_per_param"] == 3 * ps + 2 * state * (2 if dual else 1), wl["name"]
 
 
+def test_variant_workloads():
+    """--state param keeps m/v in bf16 (2 + 2 bytes each), --bound radial moves the same bytes."""
+    assert bench.workload(5)["bytes_per_param"] == 22
+    assert bench.workload(5, state="param")["bytes_per_param"] == 14   # p 2+2, g 2, m 2+2, v 2+2
+    assert bench.workload(4, state="param")["bytes_per_param"] == 10   # p 2+2, g 2, m 2+2
+    assert bench.workload(3, state="param")["bytes_per_param"] == 28   # fp32 params: fp32 state
+    assert bench.workload(5, bound="radial")["bytes_per_param"] == 22
+    assert bench.workload(5, state="param")["sdt"] == "bf16"
+    assert bench.pmc_traffic_bytes(5, bound="radial") is None
+
+
 def test_pmc_traffic_is_the_algorithmic_bytes_plus_the_count_atomics():
     algorithmic = bench.N5 * 22
     traffic = bench.pmc_traffic_bytes(5)

@@ -46,9 +46,9 @@ def test_version_and_workspace(lib):
     assert ws % 256 == 0
     # the launches of a call reuse per-launch regions, so the size does not grow with the count
     assert lib.lv_workspace_bytes(1000) == ws
-    # 48 x 65 count words 64 B apart, 48 tickets, and the radial records of one 2^20-unit piece
+    # 48 x 65 count words 64 B apart, 48 tickets, and the radial records of one 2^22-unit piece
     # (2 doubles + a u32 count per unit)
-    assert ws >= 48 * 65 * 64 + 48 * 8 + (1 << 20) * 20
+    assert ws >= 48 * 65 * 64 + 48 * 8 + (1 << 22) * 20
 
 
 def _c_layout(struct, fields, tmp_path):

@@ -97,22 +97,23 @@ def test_radial_bitwise_vs_oracle_f64_sums(oracle_mod, buffer, pdt, gdt, sdt, ex
 
 def test_radial_many_tensors_and_several_fold_chunks(oracle_mod):
     """64 tensors (two launches sharing the workspace records and tickets) and one tensor of
-    4,883 work units, whose records the fold sums in five chunks."""
+    19,532 work units, whose records the fold sums in five chunks of 4,096."""
     rng = np.random.default_rng(9)
-    sizes = [int(np.exp(rng.uniform(0, np.log(2 ** 14)))) + 1 for _ in range(62)] + [5_000_003, 70_001]
+    sizes = [int(np.exp(rng.uniform(0, np.log(2 ** 14)))) + 1 for _ in range(62)] + [20_000_003, 70_001]
     _run_bitwise(oracle_mod, sizes, "bf16", "bf16", "f32", steps=3, threads=8, buffer="T2", lr=1e-3)
 
 
-@pytest.mark.parametrize("cap", ["7", "1500"])
+@pytest.mark.parametrize("cap", ["7", "9000"])
 def test_radial_launch_split_into_pieces(oracle_mod, monkeypatch, cap):
-    """A radial counting launch runs in pieces (at most 2^20 units, one workspace record each)
+    """A radial counting launch runs in pieces (at most 2^22 units, one workspace record each)
     with a fold launch after each; a tensor's running sums carry from piece to piece and the
     piece holding its last unit finalises the scratch. LV_MAX_GRID_BLOCKS lowers the piece size:
-    7 units (tensors spanning hundreds of pieces, pieces spanning tensors) and 1,500 units (a
-    tensor's part of a piece spans two fold chunks). Bitwise against the oracle's f64 sums over
-    the two-pass first step and the fused steps, and the count words and tickets are left zero."""
+    7 units (tensors spanning hundreds of pieces, pieces spanning tensors) and 9,000 units (the
+    10M-element tensor's 8,833 units in the first piece span three fold chunks of 4,096). Bitwise
+    against the oracle's f64 sums over the two-pass first step and the fused steps, and the count
+    words and tickets are left zero."""
     monkeypatch.setenv("LV_MAX_GRID_BLOCKS", cap)
-    _run_bitwise(oracle_mod, [100_003, 5, 66_000, 2048, 1, 3_000_001], "bf16", "bf16", "f32", steps=3,
+    _run_bitwise(oracle_mod, [100_003, 5, 66_000, 2048, 1, 10_000_000], "bf16", "bf16", "f32", steps=3,
                  check_workspace=True, buffer="T2", lr=1e-3)
     _run_bitwise(oracle_mod, [70_001, 2_100_000], "f32", "f32", "f32", steps=2, check_workspace=True, buffer=1,
                  lam=0.3, cautious=False, lr=1e-3)
