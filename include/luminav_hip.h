@@ -94,11 +94,13 @@ typedef struct lv_tensor {
 /* Library version, major*10000 + minor*100 + patch. */
 int lv_version(void);
 
-/* Bytes of device workspace lv_step_multi needs (the same for any n_tensors: the launches of a
- * call reuse per-launch regions): 195 KiB of cautious mask-count words (48 tensors per launch x
- * 65 words x 64 bytes) and 512 bytes of radial-fold tickets, which must be zero before a call,
- * then 35 KiB of radial running sums and chunk records and 80 MiB of radial unit records (one
- * launch piece of 2^22 units x 20 bytes), which need no clearing. The caller allocates it once,
+/* Bytes of device workspace lv_step_multi needs for a call with n_tensors tensors (the launches
+ * of a call reuse per-launch regions): 195 KiB of cautious mask-count words (48 tensors per
+ * launch x 65 words x 64 bytes) and 512 bytes of radial-fold tickets, which must be zero before a
+ * call, then 35 KiB of radial running sums and chunk records and 80 MiB of radial unit records
+ * (one launch piece of 2^22 units x 20 bytes), which need no clearing. Above 48 tensors, table
+ * launches (up to 960 tensors each) add 3.8 MiB of count words, which must be zero, and a 75 KiB
+ * descriptor table. The caller allocates it once,
  * zero-filled; the kernels leave the count words and tickets zeroed again after every call, so it
  * is reused from step to step. Calls that share one workspace must not overlap. After a call
  * that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero the workspace again

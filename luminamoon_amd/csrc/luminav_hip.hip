@@ -1,6 +1,8 @@
 // MI355X (gfx950) LuminaV optimizer step: HIP kernels + C ABI (include/luminav_hip.h).
 //
-// One multi-tensor launch per (pass, step, dtype) class of tensors. Each tensor is cut into work
+// One multi-tensor launch per (pass, step, dtype) class of tensors: up to 48 descriptors in the
+// kernel arguments (inline launch), or up to 960 uploaded to the workspace through pinned staging
+// with their first units in the kernel arguments (table launch). Each tensor is cut into work
 // units of 1024 elements (2048 with 16-bit state); every block of a unit launch updates exactly
 // one unit and exits. A thread moves 4 consecutive elements of each 1024-element half with
 // vector loads/stores (16 bytes for f32, 8 for 16-bit types) and falls back to per-element
@@ -58,7 +60,7 @@ constexpr int unit_halves(int mode, int pt, int st) {
     (void)pt;
     return st == LV_DTYPE_F32 ? 1 : 2;
 }
-constexpr int kMaxDesc = 48;                 // tensors per launch (kernel argument table, < 4 KiB)
+constexpr int kMaxDesc = 48;                 // tensors per inline launch (kernel argument table, < 4 KiB)
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
 constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
 constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-byte segment
@@ -91,7 +93,8 @@ enum Flags : uint32_t {
     kFCoordinate = 1u << 6,
 };
 
-// One tensor of a launch (80 bytes, lives in the kernel argument segment).
+// One tensor of a launch (80 bytes): in the kernel arguments (inline launches) or in the
+// workspace (table launches).
 struct Desc {
     void *p;
     const void *g;
@@ -133,8 +136,16 @@ struct Args {
     RadialSum *chunks;            // radial fold: one record per chunk of the piece
     double *unit_sq;              // radial: per unit of the piece, (sum u_eff^2, sum p^2)
     uint32_t *unit_cnt;           // radial: per unit of the piece, the mask count
-    Desc d[kMaxDesc];
+    const Desc *dtab;             // table launches: the tensor table in device memory
+    union {
+        Desc d[kMaxDesc];  // inline launches: the tensor table
+        uint32_t ubegin[kMaxDesc * sizeof(Desc) / sizeof(uint32_t)];  // table launches: first unit per tensor
+    };
 };
+
+// Table launches: up to kTableMax tensors, their descriptors uploaded to the workspace and their
+// first units in the kernel arguments (where the inline table would be).
+constexpr int kTableMax = kMaxDesc * (int)(sizeof(Desc) / sizeof(uint32_t));  // 960
 
 static_assert(sizeof(Desc) == 80, "descriptor layout");
 static_assert(sizeof(Args) <= 4096, "kernel arguments must fit in 4 KiB");
@@ -662,6 +673,19 @@ __device__ __forceinline__ double load_relaxed(const double *p) {
 
 // ------------------------------------------------------------------ per-unit work
 
+// First unit of tensor t, and its descriptor, in an inline or a table launch.
+template <bool TABLE>
+__device__ __forceinline__ uint32_t unit_begin_of(const Args &a, int t) {
+    if constexpr (TABLE) return a.ubegin[t];
+    else return a.d[t].unit_begin;
+}
+
+template <bool TABLE>
+__device__ __forceinline__ const Desc &desc_of(const Args &a, int t) {
+    if constexpr (TABLE) return a.dtab[t];
+    else return a.d[t];
+}
+
 // What a block needs to know about the tensor that owns its current unit.
 struct View {
     uint32_t t_begin, t_end;  // the tensor's unit range in the launch
@@ -672,12 +696,12 @@ struct View {
     uint32_t ibase;
 };
 
-template <int MODE, int PASS>
+template <int MODE, int PASS, bool TABLE>
 __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, uint32_t flags, uint32_t unit) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     View tv;
-    tv.t_begin = D.unit_begin;
-    tv.t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+    tv.t_begin = unit_begin_of<TABLE>(a, t);
+    tv.t_end = (t + 1 < a.ndesc) ? unit_begin_of<TABLE>(a, t + 1) : a.total_units;
     tv.n = D.n;
     uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
     if (kDual) al |= (uintptr_t)D.v;
@@ -848,12 +872,13 @@ __device__ __forceinline__ int inactive_cover(const Desc &D, uint64_t e0, uint64
     return (b <= e0 && e >= e1) ? 2 : 1;
 }
 
-// Index of the tensor that owns `unit`: binary search of the unit ranges, right of `lo`.
-__device__ __forceinline__ int find_tensor(const Args &a, int lo, uint32_t unit) {
-    int hi = a.ndesc - 1;
+// Index of the tensor that owns `unit`: binary search of the unit ranges.
+template <bool TABLE>
+__device__ __forceinline__ int find_tensor(const Args &a, uint32_t unit) {
+    int lo = 0, hi = a.ndesc - 1;
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
-        if (a.d[mid].unit_begin <= unit) lo = mid;
+        if (unit_begin_of<TABLE>(a, mid) <= unit) lo = mid;
         else hi = mid - 1;
     }
     return lo;
@@ -872,7 +897,8 @@ __device__ __forceinline__ int find_tensor(const Args &a, int lo, uint32_t unit)
 // release fence per block measured 7x slower); integer sums are exact in any order, so the
 // result is deterministic. Wholly inactive units report a zero count.
 template <int MODE, int PASS>
-__device__ __forceinline__ void report_count(const Args &a, int t, const View &tv, uint32_t unit, uint32_t count) {
+__device__ __forceinline__ void report_count(const Args &a, int t, const Desc &D, const View &tv, uint32_t unit,
+                                             uint32_t count) {
     const uint32_t n_units = tv.t_end - tv.t_begin;
     const uint32_t k = unit - tv.t_begin;
     const uint32_t s = k % kSlots;
@@ -891,7 +917,7 @@ __device__ __forceinline__ void report_count(const Args &a, int t, const View &t
     const uint32_t nslots = n_units < kSlots ? n_units : kSlots;
     if ((uint32_t)(prev & ((1ull << kFoldBits) - 1ull)) + 1u != nslots) return;
     __hip_atomic_store(fold, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    finalize_scratch<MODE, PASS>(a, false, a.d[t], (prev >> kFoldBits) + slot_count, 0.0f, 0.0f);
+    finalize_scratch<MODE, PASS>(a, false, D, (prev >> kFoldBits) + slot_count, 0.0f, 0.0f);
 }
 
 // Unit launch: each block updates exactly one work unit (1024 or 2048 elements, unit_halves) and
@@ -905,7 +931,8 @@ __device__ __forceinline__ void report_count(const Args &a, int t, const View &t
 // (mask count and f64 squared-norm sums) for fold_kernel.
 // FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
 // which case every option test folds at compile time and the per-element code is straight-line.
-template <int MODE, int PT, int ST, int PASS, uint32_t FL>
+// TABLE: the tensor table is in device memory (a.dtab) and the first units in a.ubegin.
+template <int MODE, int PT, int ST, int PASS, uint32_t FL, bool TABLE>
 __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
     __shared__ BlockSums sh;
@@ -921,9 +948,9 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const uint32_t i = (uint32_t)(((uint64_t)b * a.xcd_recip) >> 40);
     const uint32_t x = b - i * a.xcds;
     const uint32_t unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
-    const int t = find_tensor(a, 0, unit);
-    const Desc &D = a.d[t];
-    const View tv = open_view<MODE, PASS>(a, D, t, flags, unit);
+    const int t = find_tensor<TABLE>(a, unit);
+    const Desc &D = desc_of<TABLE>(a, t);
+    const View tv = open_view<MODE, PASS, TABLE>(a, D, t, flags, unit);
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
@@ -962,7 +989,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
                 uint32_t tot = 0;
 #pragma unroll
                 for (int k = 0; k < kThreads / 64; k++) tot += (uint32_t)sh.cnt[k];
-                report_count<MODE, PASS>(a, t, tv, unit, tot);
+                report_count<MODE, PASS>(a, t, D, tv, unit, tot);
             }
         }
     }
@@ -1086,46 +1113,48 @@ constexpr uint32_t radial_flags(int PT) {
             (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8));
 }
 
+// Table launches (many small tensors, launch-bound) use the run-time-flag kernel only.
 template <int MODE, int PT, int ST, int PASS>
-KernelFn pick_flags(uint32_t flags) {
+KernelFn pick_flags(uint32_t flags, bool table) {
     constexpr uint32_t kStatic = static_flags(PT, PASS);
     constexpr uint32_t kRadial = radial_flags(PT);
-    if (flags == kStatic) return unit_kernel<MODE, PT, ST, PASS, kStatic>;
-    if (flags == kRadial) return unit_kernel<MODE, PT, ST, PASS, kRadial>;
-    return unit_kernel<MODE, PT, ST, PASS, kFDynamic>;
+    if (table) return unit_kernel<MODE, PT, ST, PASS, kFDynamic, true>;
+    if (flags == kStatic) return unit_kernel<MODE, PT, ST, PASS, kStatic, false>;
+    if (flags == kRadial) return unit_kernel<MODE, PT, ST, PASS, kRadial, false>;
+    return unit_kernel<MODE, PT, ST, PASS, kFDynamic, false>;
 }
 
 template <int MODE, int PT, int ST>
-KernelFn pick_pass(int pass, uint32_t flags) {
+KernelFn pick_pass(int pass, uint32_t flags, bool table) {
     switch (pass) {
-    case kSingle: return pick_flags<MODE, PT, ST, kSingle>(flags);
-    case kFused: return pick_flags<MODE, PT, ST, kFused>(flags);
-    case kCount: return pick_flags<MODE, PT, ST, kCount>(flags);
-    default: return pick_flags<MODE, PT, ST, kApply>(flags);
+    case kSingle: return pick_flags<MODE, PT, ST, kSingle>(flags, table);
+    case kFused: return pick_flags<MODE, PT, ST, kFused>(flags, table);
+    case kCount: return pick_flags<MODE, PT, ST, kCount>(flags, table);
+    default: return pick_flags<MODE, PT, ST, kApply>(flags, table);
     }
 }
 
 template <int MODE, int PT>
-KernelFn pick_state(int st, int pass, uint32_t flags) {
-    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass, flags)
-                              : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass, flags);
+KernelFn pick_state(int st, int pass, uint32_t flags, bool table) {
+    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass, flags, table)
+                              : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass, flags, table);
 }
 
 template <int MODE>
-KernelFn pick_param(int pt, int st, int pass, uint32_t flags) {
+KernelFn pick_param(int pt, int st, int pass, uint32_t flags, bool table) {
     switch (pt) {
-    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass, flags);
-    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass, flags);
-    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass, flags);
+    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass, flags, table);
+    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass, flags, table);
+    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass, flags, table);
     }
 }
 
-static KernelFn pick_kernel(int mode, int pt, int st, int pass, uint32_t flags) {
+static KernelFn pick_kernel(int mode, int pt, int st, int pass, uint32_t flags, bool table) {
     switch (mode) {
-    case LV_BUFFER_TDCLM: return pick_param<LV_BUFFER_TDCLM>(pt, st, pass, flags);
-    case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass, flags);
-    case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass, flags);
-    default: return pick_param<LV_BUFFER_T2>(pt, st, pass, flags);
+    case LV_BUFFER_TDCLM: return pick_param<LV_BUFFER_TDCLM>(pt, st, pass, flags, table);
+    case LV_BUFFER_DUAL: return pick_param<LV_BUFFER_DUAL>(pt, st, pass, flags, table);
+    case LV_BUFFER_T1: return pick_param<LV_BUFFER_T1>(pt, st, pass, flags, table);
+    default: return pick_param<LV_BUFFER_T2>(pt, st, pass, flags, table);
     }
 }
 
@@ -1243,24 +1272,99 @@ static int launch_one(KernelFn fn, const Args &args, uint32_t grid, uint32_t thr
     return LV_STATUS_SUCCESS;
 }
 
-// Gives the tensors of a launch consecutive ranges of units of `unit_elems` elements.
-static int assign_units(Args &args, uint32_t unit_elems) {
+// Gives the tensors of a launch consecutive ranges of units of `unit_elems` elements. A table
+// launch (`table` = its descriptors in host staging memory) keeps the first units both in the
+// staged descriptors and in the kernel arguments.
+static int assign_units(Args &args, uint32_t unit_elems, Desc *table) {
     uint64_t units = 0;
     for (int k = 0; k < args.ndesc; k++) {
-        args.d[k].unit_begin = (uint32_t)units;
-        units += (args.d[k].n + unit_elems - 1) / unit_elems;
+        Desc &D = table ? table[k] : args.d[k];
+        D.unit_begin = (uint32_t)units;
+        if (table) args.ubegin[k] = (uint32_t)units;
+        units += (D.n + unit_elems - 1) / unit_elems;
         if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
     }
     args.total_units = (uint32_t)units;
     return LV_STATUS_SUCCESS;
 }
 
-static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t stream) {
-    KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags);
-    const bool radial = (pass == kFused || pass == kCount) && (args.flags & kFRadial);
-    int rc = assign_units(args, kHalf * unit_halves(mode, pt, st));
+// Pinned host staging for the descriptor tables of table launches: kStageSlots tables per
+// device, used round-robin. A slot is written only after the upload that last read it has
+// finished (its event), so the host rarely waits and the uploads stay asynchronous.
+constexpr int kStageSlots = 4;
+
+struct Staging {
+    int dev;
+    Desc *host;
+    hipEvent_t ev[kStageSlots];
+    bool used[kStageSlots];
+    int next;
+};
+
+static std::mutex g_stage_mu;
+static std::vector<Staging *> g_stage;
+
+// A staging table for the current device, free for the host to write. Allocates the device's
+// ring on first use (the only allocation of the step path, once per device and process).
+static int acquire_staging(Desc **table, hipEvent_t *ev) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(LV_STATUS_NO_DRIVER, "no HIP device");
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    Staging *S = nullptr;
+    for (Staging *x : g_stage)
+        if (x->dev == dev) S = x;
+    if (!S) {
+        S = new Staging();
+        S->dev = dev;
+        S->next = 0;
+        void *h = nullptr;
+        if (hipHostMalloc(&h, sizeof(Desc) * kTableMax * kStageSlots, hipHostMallocDefault) != hipSuccess) {
+            delete S;
+            return fail(LV_STATUS_EXECUTION_FAILED, "pinned staging allocation failed");
+        }
+        S->host = static_cast<Desc *>(h);
+        for (int k = 0; k < kStageSlots; k++) {
+            S->used[k] = false;
+            if (hipEventCreateWithFlags(&S->ev[k], hipEventDisableTiming) != hipSuccess)
+                return fail(LV_STATUS_EXECUTION_FAILED, "event creation failed");
+        }
+        g_stage.push_back(S);
+    }
+    const int k = S->next;
+    S->next = (k + 1) % kStageSlots;
+    if (S->used[k] && hipEventSynchronize(S->ev[k]) != hipSuccess)
+        return fail(LV_STATUS_EXECUTION_FAILED, "staging event wait failed");
+    S->used[k] = true;
+    *table = S->host + (size_t)k * kTableMax;
+    *ev = S->ev[k];
+    return LV_STATUS_SUCCESS;
+}
+
+// Table launches: assigns the units of the args.ndesc descriptors staged in `table` and
+// uploads them to args.dtab on the stream; `staged` is recorded after the upload. The launches
+// of the class (COUNT and APPLY use the same unit size) then read the uploaded table.
+static int stage_table(Args &args, int mode, int pt, int st, Desc *table, hipEvent_t staged, hipStream_t stream) {
+    int rc = assign_units(args, kHalf * unit_halves(mode, pt, st), table);
     if (rc != LV_STATUS_SUCCESS) return rc;
+    if (hipMemcpyAsync(const_cast<Desc *>(args.dtab), table, sizeof(Desc) * args.ndesc, hipMemcpyHostToDevice,
+                       stream) != hipSuccess ||
+        hipEventRecord(staged, stream) != hipSuccess)
+        return fail(LV_STATUS_EXECUTION_FAILED, "descriptor upload failed");
+    return LV_STATUS_SUCCESS;
+}
+
+// Inline launch: the descriptors are in args.d and get their units here. Table launch: the
+// table was staged (stage_table).
+static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t stream, bool table = false) {
+    KernelFn fn = pick_kernel(mode, pt, st, pass, args.flags, table);
+    const bool radial = (pass == kFused || pass == kCount) && (args.flags & kFRadial);
+    if (table && radial) return fail(LV_STATUS_INVALID_CONFIG, "radial counting launches are inline");
+    if (!table) {
+        int rc = assign_units(args, kHalf * unit_halves(mode, pt, st), nullptr);
+        if (rc != LV_STATUS_SUCCESS) return rc;
+    }
     if (args.total_units == 0) return LV_STATUS_SUCCESS;
+    int rc = LV_STATUS_SUCCESS;
     // Unit launches, in pieces of at most kMaxGrid blocks (kRadialPiece for radial counting, the
     // records of one piece; LV_MAX_GRID_BLOCKS lowers the cap, so tests can split small launches).
     // A counting launch folds its counts in its last blocks; a radial one runs fold_kernel after
@@ -1313,7 +1417,10 @@ int lv_version(void) { return 100; }
 //   [count words: kMaxDesc x kSlotWords words, 64 B apart][radial tickets: kMaxDesc u64, 512 B]
 //     -- kZeroBytes that must be zero before a call; every launch leaves them zeroed again --
 //   [radial running sums: kMaxDesc RadialSum][chunk records: kMaxChunks RadialSum]
-//   [unit records: kRadialPiece x (2 doubles)][unit counts: kRadialPiece x u32]
+//   [unit records: kRadialPiece x (2 doubles)][unit counts: kRadialPiece x u32]   = kFixedBytes
+// and, when a call has more than kMaxDesc tensors (table launches):
+//   [count words: kTableMax x kSlotWords words, 64 B apart] (zero, like the first region)
+//   [descriptor table: kTableMax x Desc]
 // Everything is reused by every launch of a call (stream-ordered).
 static constexpr size_t kSlotBytes = (size_t)lv::kMaxDesc * lv::kSlotWords * lv::kSlotStride * sizeof(unsigned long long);
 static constexpr size_t kTicketBytes = 512;
@@ -1322,13 +1429,18 @@ static constexpr size_t kRunBytes = (size_t)lv::kMaxDesc * sizeof(lv::RadialSum)
 static constexpr size_t kChunkBytes = (size_t)lv::kMaxChunks * sizeof(lv::RadialSum);
 static constexpr size_t kUnitSqBytes = (size_t)lv::kRadialPiece * 2 * sizeof(double);
 static constexpr size_t kUnitCntBytes = (size_t)lv::kRadialPiece * sizeof(uint32_t);
+static constexpr size_t kFixedBytes = kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes + kUnitCntBytes;
+static constexpr size_t kTableSlotBytes =
+    (size_t)lv::kTableMax * lv::kSlotWords * lv::kSlotStride * sizeof(unsigned long long);
+static constexpr size_t kTableDescBytes = (size_t)lv::kTableMax * sizeof(lv::Desc);
 static_assert(kSlotBytes % 256 == 0 && kRunBytes % 256 == 0 && kChunkBytes % 256 == 0, "region alignment");
+static_assert(kFixedBytes % 256 == 0 && kTableSlotBytes % 256 == 0 && kTableDescBytes % 256 == 0, "region alignment");
 static_assert(lv::kMaxDesc * sizeof(unsigned long long) <= kTicketBytes, "ticket region");
 static_assert(sizeof(lv::RadialSum) == 32, "radial record layout");
 
 size_t lv_workspace_bytes(int n_tensors) {
-    (void)n_tensors;  // launches of a call reuse the same per-launch regions
-    return kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes + kUnitCntBytes;
+    // the launches of a call reuse per-launch regions; table launches need their own words
+    return kFixedBytes + (n_tensors > lv::kMaxDesc ? kTableSlotBytes + kTableDescBytes : 0);
 }
 
 const char *lv_last_error(void) { return lv::g_err; }
@@ -1402,81 +1514,101 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     });
 
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    char *ws = static_cast<char *>(workspace);
+    // Radial counting launches fold per tensor after each piece, which needs the inline table.
+    const bool table_ok = bound != LV_BOUND_RADIAL;
     size_t begin = 0;
     while (begin < items.size()) {
         const Item &h = items[begin];
-        size_t end = begin + 1;
-        while (end < items.size() && end - begin < (size_t)kMaxDesc) {
-            const Item &x = items[end];
+        size_t cls_end = begin + 1;
+        while (cls_end < items.size()) {
+            const Item &x = items[cls_end];
             if (x.pass != h.pass || x.step != h.step || x.pt != h.pt || x.gt != h.gt || x.st != h.st ||
                 x.master != h.master || x.clampv != h.clampv)
                 break;
-            end++;
+            cls_end++;
         }
-        Args args;
-        std::memset(&args, 0, sizeof args);
-        args.lr = cfg->lr;
-        args.b1 = cfg->beta1;
-        args.b2 = cfg->beta2;
-        args.omb1 = 1.0f - cfg->beta1;
-        args.omb2 = 1.0f - cfg->beta2;
-        args.b1sq = cfg->beta1 * cfg->beta1;
-        args.omb1sq = 1.0f - args.b1sq;
-        args.eps = cfg->eps;
-        args.lam = cfg->lam;
-        args.lam1 = 0.5f * cfg->lam;
-        args.neg_lr_wd = -(cfg->lr * cfg->weight_decay);
-        args.ratio = cfg->bound_ratio;
-        StepCoeffs sc = step_coeffs(h.step, cfg->beta1, cfg->beta2, cfg->eps, cfg->tau, cfg->lam);
-        args.c1 = sc.c1;
-        args.c2 = sc.c2;
-        args.c_sigma = sc.c_sigma;
-        args.ema = cfg->ema_decay;
-        args.ema_c = 1.0f - cfg->ema_decay;
-        args.clamp_min = cfg->cautious_clamp_min;
-        args.seed_base = (uint32_t)((uint64_t)cfg->seed + h.step * 0x9E3779B9ull);
-        uint32_t flags = 0;
-        if (cautious) flags |= kFCautious;
-        if (cfg->stochastic_rounding) flags |= kFSR;
-        if (h.master) flags |= kFMaster;
-        if (cfg->weight_decay != 0.0f) flags |= kFWeightDecay;
-        if (h.clampv) flags |= kFClampV;
-        if (bound == LV_BOUND_COORDINATE) flags |= kFCoordinate;
-        if (bound == LV_BOUND_RADIAL) flags |= kFRadial;
-        flags |= (uint32_t)h.gt << 8;
-        args.flags = flags;
-        args.ndesc = (int32_t)(end - begin);
-        for (size_t k = begin; k < end; k++) {
-            const lv_tensor &T = tensors[items[k].idx];
-            Desc &D = args.d[k - begin];
-            D.p = T.param;
-            D.g = T.grad;
-            D.m = T.exp_avg;
-            D.v = T.exp_avg_sq;
-            D.mp = items[k].master ? T.master_param : nullptr;
-            D.scratch = T.scratch;
-            D.n = T.numel;
-            D.unit_begin = 0;  // set per launch (the unit size depends on the launch shape)
-            D.pidx = (uint32_t)T.param_index;
-            D.ibase = (uint32_t)T.index_base;
-            D.nskip = (uint32_t)T.n_inactive;
-            D.skip = T.n_inactive ? T.inactive : nullptr;
+        // One launch (pair) per kMaxDesc tensors of the class, or per kTableMax tensors when more
+        // than kMaxDesc remain and the class can use a table launch.
+        while (begin < cls_end) {
+            const size_t left = cls_end - begin;
+            const bool table = table_ok && left > (size_t)kMaxDesc;
+            const size_t end = begin + std::min(left, (size_t)(table ? kTableMax : kMaxDesc));
+            Args args;
+            std::memset(&args, 0, sizeof args);
+            args.lr = cfg->lr;
+            args.b1 = cfg->beta1;
+            args.b2 = cfg->beta2;
+            args.omb1 = 1.0f - cfg->beta1;
+            args.omb2 = 1.0f - cfg->beta2;
+            args.b1sq = cfg->beta1 * cfg->beta1;
+            args.omb1sq = 1.0f - args.b1sq;
+            args.eps = cfg->eps;
+            args.lam = cfg->lam;
+            args.lam1 = 0.5f * cfg->lam;
+            args.neg_lr_wd = -(cfg->lr * cfg->weight_decay);
+            args.ratio = cfg->bound_ratio;
+            StepCoeffs sc = step_coeffs(h.step, cfg->beta1, cfg->beta2, cfg->eps, cfg->tau, cfg->lam);
+            args.c1 = sc.c1;
+            args.c2 = sc.c2;
+            args.c_sigma = sc.c_sigma;
+            args.ema = cfg->ema_decay;
+            args.ema_c = 1.0f - cfg->ema_decay;
+            args.clamp_min = cfg->cautious_clamp_min;
+            args.seed_base = (uint32_t)((uint64_t)cfg->seed + h.step * 0x9E3779B9ull);
+            uint32_t flags = 0;
+            if (cautious) flags |= kFCautious;
+            if (cfg->stochastic_rounding) flags |= kFSR;
+            if (h.master) flags |= kFMaster;
+            if (cfg->weight_decay != 0.0f) flags |= kFWeightDecay;
+            if (h.clampv) flags |= kFClampV;
+            if (bound == LV_BOUND_COORDINATE) flags |= kFCoordinate;
+            if (bound == LV_BOUND_RADIAL) flags |= kFRadial;
+            flags |= (uint32_t)h.gt << 8;
+            args.flags = flags;
+            args.ndesc = (int32_t)(end - begin);
+            Desc *staged = nullptr;
+            hipEvent_t staged_ev = nullptr;
+            if (table) {
+                rc = acquire_staging(&staged, &staged_ev);
+                if (rc != LV_STATUS_SUCCESS) return rc;
+            }
+            for (size_t k = begin; k < end; k++) {
+                const lv_tensor &T = tensors[items[k].idx];
+                Desc &D = table ? staged[k - begin] : args.d[k - begin];
+                D.p = T.param;
+                D.g = T.grad;
+                D.m = T.exp_avg;
+                D.v = T.exp_avg_sq;
+                D.mp = items[k].master ? T.master_param : nullptr;
+                D.scratch = T.scratch;
+                D.n = T.numel;
+                D.unit_begin = 0;  // set per launch (the unit size depends on the launch shape)
+                D.pidx = (uint32_t)T.param_index;
+                D.ibase = (uint32_t)T.index_base;
+                D.nskip = (uint32_t)T.n_inactive;
+                D.skip = T.n_inactive ? T.inactive : nullptr;
+            }
+            args.slots = reinterpret_cast<unsigned long long *>(table ? ws + kFixedBytes : ws);
+            args.tickets = reinterpret_cast<unsigned long long *>(ws + kSlotBytes);
+            args.run = reinterpret_cast<RadialSum *>(ws + kZeroBytes);
+            args.chunks = reinterpret_cast<RadialSum *>(ws + kZeroBytes + kRunBytes);
+            args.unit_sq = reinterpret_cast<double *>(ws + kZeroBytes + kRunBytes + kChunkBytes);
+            args.unit_cnt = reinterpret_cast<uint32_t *>(ws + kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes);
+            if (table) {
+                args.dtab = reinterpret_cast<const Desc *>(ws + kFixedBytes + kTableSlotBytes);
+                rc = stage_table(args, cfg->buffer, h.pt, h.st, staged, staged_ev, stream);
+                if (rc != LV_STATUS_SUCCESS) return rc;
+            }
+            if (h.pass == kCount) {
+                rc = launch(args, cfg->buffer, h.pt, h.st, kCount, stream, table);
+                if (rc == LV_STATUS_SUCCESS) rc = launch(args, cfg->buffer, h.pt, h.st, kApply, stream, table);
+            } else {
+                rc = launch(args, cfg->buffer, h.pt, h.st, h.pass, stream, table);
+            }
+            if (rc != LV_STATUS_SUCCESS) return rc;
+            begin = end;
         }
-        char *ws = static_cast<char *>(workspace);
-        args.slots = reinterpret_cast<unsigned long long *>(ws);
-        args.tickets = reinterpret_cast<unsigned long long *>(ws + kSlotBytes);
-        args.run = reinterpret_cast<RadialSum *>(ws + kZeroBytes);
-        args.chunks = reinterpret_cast<RadialSum *>(ws + kZeroBytes + kRunBytes);
-        args.unit_sq = reinterpret_cast<double *>(ws + kZeroBytes + kRunBytes + kChunkBytes);
-        args.unit_cnt = reinterpret_cast<uint32_t *>(ws + kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes);
-        if (h.pass == kCount) {
-            rc = launch(args, cfg->buffer, h.pt, h.st, kCount, stream);
-            if (rc == LV_STATUS_SUCCESS) rc = launch(args, cfg->buffer, h.pt, h.st, kApply, stream);
-        } else {
-            rc = launch(args, cfg->buffer, h.pt, h.st, h.pass, stream);
-        }
-        if (rc != LV_STATUS_SUCCESS) return rc;
-        begin = end;
     }
     return LV_STATUS_SUCCESS;
 }

@@ -45,10 +45,13 @@ def test_version_and_workspace(lib):
     ws = lib.lv_workspace_bytes(1)
     assert ws % 256 == 0
     # the launches of a call reuse per-launch regions, so the size does not grow with the count
-    assert lib.lv_workspace_bytes(1000) == ws
+    assert lib.lv_workspace_bytes(48) == ws
     # 48 x 65 count words 64 B apart, 48 tickets, and the radial records of one 2^22-unit piece
     # (2 doubles + a u32 count per unit)
     assert ws >= 48 * 65 * 64 + 48 * 8 + (1 << 22) * 20
+    # more than 48 tensors: table launches add count words and a descriptor table for 960 tensors
+    assert lib.lv_workspace_bytes(49) == ws + 960 * 65 * 64 + 960 * 80
+    assert lib.lv_workspace_bytes(100_000) == lib.lv_workspace_bytes(49)
 
 
 def _c_layout(struct, fields, tmp_path):

@@ -83,12 +83,64 @@ def test_hip_matches_oracle(oracle_mod, buffer, pdt, gdt, sdt, extra):
 
 
 def test_many_tensors_multiple_launches(oracle_mod):
-    """64 ragged tensors (more than one kernel-argument table) in one call."""
+    """64 ragged tensors (more than one kernel-argument table: one table launch) in one call."""
     import numpy as np
 
     rng = np.random.default_rng(3)
     sizes = [int(np.exp(rng.uniform(0, np.log(2 ** 14)))) + 1 for _ in range(64)]
     _run_case(oracle_mod, sizes, "f32", "f32", "f32", steps=4, buffer=1, lr=8e-4)
+
+
+# Leading workspace bytes that must be zero between calls (48 x 65 count words 64 B apart and
+# 512 B of radial tickets), and the count words of table launches (960 tensors) that follow the
+# fixed regions.
+ZERO_BYTES = 48 * 65 * 64 + 512
+TABLE_SLOT_BYTES = 960 * 65 * 64
+
+
+@pytest.mark.parametrize("count,buffer,pdt,sdt,extra", [
+    (1000, "T2", "bf16", "f32", {}),
+    (2000, 1, "f32", "f32", {"lam": 0.3}),
+    (1000, 2, "bf16", "f32", {"master_weights": "full"}),
+    (1000, 2, "f32", "f32", {"cautious": False}),
+    (1000, "T1", "bf16", "bf16", {"state_precision": "param", "fused_single_pass": False}),
+], ids=["T2-bf16-1000", "TDCLM-f32-2000", "CLM-master-1000", "CLM-nocautious-1000", "T1-bf16state-twopass-1000"])
+def test_table_launches_thousands_of_tensors(oracle_mod, count, buffer, pdt, sdt, extra):
+    """More tensors than the kernel-argument table holds: the descriptors go to the workspace
+    (up to 960 per launch, the first units stay in the kernel arguments), so 1000 ragged tensors
+    are one table launch and an inline launch of 40, and 2000 are 960 + 960 + 80. Every buffer
+    and scratch bit for bit over the two-pass first step and fused steps; the count words of both
+    kinds of launch are left zero."""
+    import numpy as np
+
+    _need_gpu()
+    O = oracle_mod
+    rng = np.random.default_rng(count + 7)
+    sizes = [int(np.exp(rng.uniform(0, np.log(2 ** 12)))) + 1 for _ in range(count - 3)] + [100_003, 2048, 70_001]
+    kw = dict(extra)
+    kw.setdefault("lr", 1e-3)
+    group = group_dict(buffer=buffer, **kw)
+    dual = group["buffer"] in (2, "T2")
+    master = group["master_weights"] > 0 and pdt != "f32"
+    host = TensorSet(sizes, pdt, pdt, sdt, dual, master, 13)
+    dev = host.to("cuda")
+    cfg = oracle_config(O, group)
+    st = _stepper()
+    print(f"[case] table launch {count} tensors buffer={buffer} {pdt}/{sdt} {extra}", flush=True)
+    for s in range(1, 4):
+        grads = host.grads(s, 13)
+        host.oracle_step(O, cfg, grads, s, threads=8)
+        dev.hip_step(st, group, [g.cuda() for g in grads], s)
+        torch.cuda.synchronize()
+        host.assert_equal(dev, f"{count} tensors step {s}")
+        for ws in st.workspace._bufs.values():
+            assert int(torch.count_nonzero(ws[:ZERO_BYTES])) == 0, f"count words left set (step {s})"
+            from luminamoon_amd.optimizer import hip_backend
+
+            fixed = int(hip_backend.load_library().lv_workspace_bytes(1))
+            table_words = ws[fixed:fixed + TABLE_SLOT_BYTES]
+            assert table_words.numel() == TABLE_SLOT_BYTES
+            assert int(torch.count_nonzero(table_words)) == 0, f"table count words left set (step {s})"
 
 
 def test_mixed_steps_in_one_call(oracle_mod):
