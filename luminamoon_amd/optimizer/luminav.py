@@ -1030,6 +1030,8 @@ class LuminaV(Optimizer):
             self._unfused_plans[id(group)] = {
                 "epoch": self._plan_epoch, "group": group, "layout": tuple(group.get(k) for k in self._LAYOUT_KEYS),
                 "ids": [id(p) for p in group["params"]], "active": active,
+                # every param has a grad and elements, so the entries follow the params one to one
+                "all_active": len(rows) == len(group["params"]),
                 "entries": [[r[0], r[0].data_ptr(), weakref.ref(r[2]), r[9], r[2].data_ptr()] for r in rows],
                 "prep": prep,
             }
@@ -1049,27 +1051,41 @@ class LuminaV(Optimizer):
         ids, active = plan["ids"], plan["active"]
         if len(params) != len(ids):
             return False
-        for i, p in enumerate(params):
-            if id(p) != ids[i] or (p.grad is not None) != active[i]:
-                return False
         prep = plan["prep"]
         entries = plan["entries"]
-        for k, e in enumerate(entries):
-            p = e[0]
-            if p.data_ptr() != e[1]:
-                return False
-            g = p.grad
-            if g is not e[2]() or g.data_ptr() != e[4]:
-                if g.is_sparse or not prep.set_grad(k, g):
+        if plan["all_active"]:
+            # every param has an entry, in order: one pass checks identity, storage and grad
+            for k, (p, pid, e) in enumerate(zip(params, ids, entries)):
+                g = p.grad
+                if id(p) != pid or g is None or p.data_ptr() != e[1]:
                     return False
-                e[2] = weakref.ref(g)
-                e[4] = g.data_ptr()
+                if g is not e[2]() or g.data_ptr() != e[4]:
+                    if g.is_sparse or not prep.set_grad(k, g):
+                        return False
+                    e[2] = weakref.ref(g)
+                    e[4] = g.data_ptr()
+        else:
+            for i, p in enumerate(params):
+                if id(p) != ids[i] or (p.grad is not None) != active[i]:
+                    return False
+            for k, e in enumerate(entries):
+                p = e[0]
+                if p.data_ptr() != e[1]:
+                    return False
+                g = p.grad
+                if g is not e[2]() or g.data_ptr() != e[4]:
+                    if g.is_sparse or not prep.set_grad(k, g):
+                        return False
+                    e[2] = weakref.ref(g)
+                    e[4] = g.data_ptr()
+        # nothing above touched the step counters, so a False return leaves them for the slow path
         steps = []
+        add = steps.append
         for e in entries:
             st = e[3]
             s = int(st["step"]) + 1
             st["step"] = s
-            steps.append(s)
+            add(s)
         prep.set_steps(steps)
         self._stepper.launch(group, prep)
         return True
