@@ -1314,20 +1314,20 @@ static int acquire_staging(Desc **table, hipEvent_t *ev) {
     for (Staging *x : g_stage)
         if (x->dev == dev) S = x;
     if (!S) {
-        S = new Staging();
-        S->dev = dev;
-        S->next = 0;
         void *h = nullptr;
-        if (hipHostMalloc(&h, sizeof(Desc) * kTableMax * kStageSlots, hipHostMallocDefault) != hipSuccess) {
-            delete S;
+        if (hipHostMalloc(&h, sizeof(Desc) * kTableMax * kStageSlots, hipHostMallocDefault) != hipSuccess)
             return fail(LV_STATUS_EXECUTION_FAILED, "pinned staging allocation failed");
-        }
-        S->host = static_cast<Desc *>(h);
+        Staging fresh{};
+        fresh.dev = dev;
+        fresh.host = static_cast<Desc *>(h);
         for (int k = 0; k < kStageSlots; k++) {
-            S->used[k] = false;
-            if (hipEventCreateWithFlags(&S->ev[k], hipEventDisableTiming) != hipSuccess)
+            if (hipEventCreateWithFlags(&fresh.ev[k], hipEventDisableTiming) != hipSuccess) {
+                for (int j = 0; j < k; j++) (void)hipEventDestroy(fresh.ev[j]);
+                (void)hipHostFree(h);
                 return fail(LV_STATUS_EXECUTION_FAILED, "event creation failed");
+            }
         }
+        S = new Staging(fresh);  // kept until the process ends
         g_stage.push_back(S);
     }
     const int k = S->next;
