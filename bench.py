@@ -68,25 +68,42 @@ PMC_TRAFFIC = {
 }
 
 
-def workload(config: int, bound: str = "coordinate", state: str = "fp32") -> dict:
-    """The workload of `config` with the bound type and state precision of the run. state="param"
-    keeps m/v in the param dtype (the reference's Python default for 16-bit params), which changes
-    the bytes per param: a bf16 m or v moves 2 + 2 bytes instead of 4 + 4."""
+def workload(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",
+             pdt: str = "") -> dict:
+    """The workload of `config` with the run's bound type, state precision, master weights and
+    16-bit param dtype. Each changes the bytes per param:
+    - state="param" keeps m/v in the param dtype (the reference's Python default for 16-bit
+      params): a 16-bit m or v moves 2 + 2 bytes instead of 4 + 4;
+    - master="semi"/"full" reads the update from an fp32 master copy: p becomes write-only and
+      the master moves 4 + 4 bytes;
+    - pdt="f16" runs a 16-bit config with fp16 params and grads (same byte counts as bf16)."""
     wl = dict(WORKLOADS[config])
+    if pdt:
+        if wl["pdt"] == "f32" or pdt not in ("bf16", "f16"):
+            raise ValueError("--pdt applies to the 16-bit configs (4, 5) and takes bf16 or f16")
+        wl["pdt"] = pdt
     wl["bound"] = bound
     wl["state"] = state
-    wl["sdt"] = wl["pdt"] if state == "param" else "f32"
+    wl["master"] = master
+    # the reference's rule for state="param": state in the param dtype unless the master is full
+    wl["sdt"] = wl["pdt"] if state == "param" and master != "full" else "f32"
+    n_state = 2 if wl["buffer"] in (2, "T2") else 1
     if wl["sdt"] != "f32":
-        per_state = 4  # read + write of one 16-bit state element
-        n_state = 2 if wl["buffer"] in (2, "T2") else 1
-        wl["bytes_per_param"] -= n_state * (8 - per_state)
-    if bound != "coordinate" or state != "fp32":
-        wl["name"] += f" [bound={bound}, state={state}]"
+        wl["bytes_per_param"] -= n_state * (8 - 4)  # read + write of a 16-bit state element
+    if master != "none" and wl["pdt"] != "f32":
+        wl["bytes_per_param"] += 8 - 2  # master read + write; the 16-bit p is no longer read
+    if bound != "coordinate" or state != "fp32" or master != "none" or pdt:
+        wl["name"] += f" [bound={bound}, state={state}, master={master}, param={wl['pdt']}]"
     return wl
 
 
-def pmc_traffic_bytes(config: int, bound: str = "coordinate", state: str = "fp32"):
-    if bound != "coordinate" or state != "fp32":
+def is_default_variant(bound: str = "coordinate", state: str = "fp32", master: str = "none", pdt: str = "") -> bool:
+    return bound == "coordinate" and state == "fp32" and master == "none" and not pdt
+
+
+def pmc_traffic_bytes(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",
+                      pdt: str = ""):
+    if not is_default_variant(bound, state, master, pdt):
         return None  # the counter runs were taken on the default workload
     t = PMC_TRAFFIC.get(config)
     if t is None:
@@ -170,10 +187,12 @@ def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
 
 
 def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: float) -> dict:
-    pdt = torch.bfloat16 if workload["pdt"] == "bf16" else torch.float32
-    sdt = torch.bfloat16 if workload.get("sdt", "f32") == "bf16" else torch.float32
+    dtypes = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+    pdt = dtypes[workload["pdt"]]
+    sdt = dtypes[workload.get("sdt", "f32")]
+    master = {"none": 0, "semi": 1, "full": 2}[workload.get("master", "none")] if workload["pdt"] != "f32" else 0
     cfg = O.make_config(lr=1e-3, buffer=workload["buffer"], cautious=workload["cautious"],
-                        bound_type=1 if workload.get("bound") == "radial" else 2)
+                        bound_type=1 if workload.get("bound") == "radial" else 2, master_weights=master)
     dual = workload["buffer"] in (2, "T2")
 
     def make(n, seed=5):
@@ -185,20 +204,21 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
         g = torch.from_numpy(np.resize((rng.standard_normal(k) * 1e-3).astype(np.float32), n)).to(pdt)
         m = torch.zeros(n, dtype=sdt)
         v = torch.zeros(n, dtype=sdt) if dual else None
+        mp = p.float().clone() if master else None
         sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
-        return p, g, m, v, sc
+        return p, g, m, v, mp, sc
 
     if "sizes" in workload:
         # a multi-tensor workload small enough to time whole: every tensor, one call per step
         sizes = workload["sizes"]
         k = len(sizes)
-        P, G, M, V, S = map(list, zip(*[make(sz, seed=5 + i) for i, sz in enumerate(sizes)]))
+        P, G, M, V, MP, S = map(list, zip(*[make(sz, seed=5 + i) for i, sz in enumerate(sizes)]))
         idx = list(range(k))
-        O.step(cfg, P, G, M, V, [None] * k, S, [1] * k, idx, threads=threads)  # step 1 (two-pass), untimed
+        O.step(cfg, P, G, M, V, MP, S, [1] * k, idx, threads=threads)  # step 1 (two-pass), untimed
         times = []
         for s in range(2, 12):
             t0 = time.perf_counter()
-            O.step(cfg, P, G, M, V, [None] * k, S, [s] * k, idx, threads=threads)
+            O.step(cfg, P, G, M, V, MP, S, [s] * k, idx, threads=threads)
             times.append(time.perf_counter() - t0)
         t = float(np.median(times))
         n = sum(sizes)
@@ -212,20 +232,20 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
     # calibrate on 2^25 elements (16 chunks: memory-bound like the full size), then size the timed
     # sample to ~target_s over 3 steps, at most 2^30 elements
     n_cal = min(workload["n"], 1 << 25)
-    p, g, m, v, sc = make(n_cal)
-    O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)
+    p, g, m, v, mp, sc = make(n_cal)
+    O.step(cfg, [p], [g], [m], [v], [mp], [sc], [1], [0], threads=threads)
     t0 = time.perf_counter()
-    O.step(cfg, [p], [g], [m], [v], [None], [sc], [2], [0], threads=threads)
+    O.step(cfg, [p], [g], [m], [v], [mp], [sc], [2], [0], threads=threads)
     rate = n_cal / max(time.perf_counter() - t0, 1e-6)
-    del p, g, m, v
+    del p, g, m, v, mp
     n = int(min(workload["n"], 1 << 30, max(n_cal, rate * target_s / 3.0)))
     n = (n // 2097152 + 1) * 2097152 if n > 2097152 else n
-    p, g, m, v, sc = make(n)
-    O.step(cfg, [p], [g], [m], [v], [None], [sc], [1], [0], threads=threads)  # step 1 (two-pass), untimed
+    p, g, m, v, mp, sc = make(n)
+    O.step(cfg, [p], [g], [m], [v], [mp], [sc], [1], [0], threads=threads)  # step 1 (two-pass), untimed
     times = []
     for s in (2, 3, 4):
         t0 = time.perf_counter()
-        O.step(cfg, [p], [g], [m], [v], [None], [sc], [s], [0], threads=threads)
+        O.step(cfg, [p], [g], [m], [v], [mp], [sc], [s], [0], threads=threads)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     cpu_model = ""
@@ -258,6 +278,10 @@ def main() -> int:
                     help="bound_type of the optimizer (the configs use the default, coordinate)")
     ap.add_argument("--state", default="fp32", choices=("fp32", "param"),
                     help="state_precision: fp32 m/v (the configs) or the param dtype (reference Python default)")
+    ap.add_argument("--master", default="none", choices=("none", "semi", "full"),
+                    help="master_weights (16-bit configs: an fp32 master copy of the params)")
+    ap.add_argument("--pdt", default="", choices=("", "bf16", "f16"),
+                    help="param and grad dtype of a 16-bit config (default: the config's bf16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-reserve", action="store_true", help="skip the HBM reserve/release before allocating")
@@ -277,13 +301,18 @@ def main() -> int:
     if not torch.cuda.is_available():
         log("no GPU visible")
         return 1
-    wl = workload(args.config, args.bound, args.state)
-    pdt = torch.bfloat16 if wl["pdt"] == "bf16" else torch.float32
+    try:
+        wl = workload(args.config, args.bound, args.state, args.master, args.pdt)
+    except ValueError as e:
+        print(json.dumps({"error": str(e)}), flush=True)
+        return 2
+    pdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[wl["pdt"]]
     sizes = wl.get("sizes", [wl.get("n", 0)])
     n = sum(sizes)
     free, total = torch.cuda.mem_get_info()
     state_b = (4 if wl["sdt"] == "f32" else 2) * n * (2 if wl["buffer"] in (2, "T2") else 1)
-    need = n * (2 if pdt == torch.bfloat16 else 4) * 2 + state_b
+    master_b = 4 * n if args.master != "none" and wl["pdt"] != "f32" else 0
+    need = n * (4 if wl["pdt"] == "f32" else 2) * 2 + state_b + master_b
     log(f"workload {wl['name']}: n={n}, resident {need / 1e9:.1f} GB, free {free / 1e9:.1f} GB")
     if need + (8 << 30) > free:
         log("not enough HBM for this workload")
@@ -308,7 +337,7 @@ def main() -> int:
         params.append(p)
     del p_data, g_data
     opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"], bound_type=args.bound,
-                  state_precision=args.state)
+                  state_precision=args.state, master_weights=args.master)
     torch.cuda.synchronize()
     log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
 
@@ -373,6 +402,7 @@ def main() -> int:
             "state_dtype": wl["sdt"],
             "cautious": wl["cautious"],
             "bound_type": args.bound,
+            "master_weights": args.master,
             "bytes_per_param": wl["bytes_per_param"],
         },
         "achieved_gb_per_s": achieved,
@@ -384,7 +414,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": pmc_traffic_bytes(args.config, args.bound, args.state),
+            "traffic": pmc_traffic_bytes(args.config, args.bound, args.state, args.master, args.pdt),
         },
         "cpu_baseline": cpu,
     }

@@ -44,6 +44,7 @@
 #include <vector>
 
 #include "luminav_hip.h"
+#include "lv_fp16.h"
 
 namespace lv {
 
@@ -198,44 +199,7 @@ __device__ __forceinline__ float rne_bf16(float v) {
     return bits_f(a > 0x7F800000u ? nan : fin);
 }
 
-// prng.rs:29-67
-__device__ __forceinline__ uint32_t f32_to_f16_rne(float val) {
-    uint32_t bits = f_bits(val);
-    uint32_t sign = (bits >> 16) & 0x8000u;
-    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
-    uint32_t mant = bits & 0x007FFFFFu;
-    if (exp == 255) return sign | (mant != 0 ? 0x7E00u : 0x7BFFu);
-    int32_t ne = exp - 112;
-    if (ne >= 31) return sign | 0x7BFFu;
-    if (ne <= 0) {
-        if (ne < -10) return sign;
-        uint32_t fm = mant | 0x00800000u;
-        uint32_t sh = (uint32_t)(14 - ne);
-        uint32_t half = 1u << (sh - 1);
-        uint32_t r = (fm + half - 1u + ((fm >> sh) & 1u)) >> sh;
-        return sign | r;
-    }
-    uint32_t r = mant + 0x0FFFu + ((mant >> 13) & 1u);
-    uint32_t body = ((uint32_t)ne << 10) + (r >> 13);
-    return body >= 0x7C00u ? (sign | 0x7BFFu) : (sign | body);
-}
-
-// prng.rs:69-96
-__device__ __forceinline__ float f16_to_f32(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t exp = (h >> 10) & 0x1Fu;
-    uint32_t mant = h & 0x03FFu;
-    if (exp == 0) {
-        if (mant == 0) return bits_f(sign);
-        // subnormal: normalise (leading one of a 10-bit field)
-        uint32_t lz = __clz(mant) - 21;  // shifts until bit 10 is set
-        uint32_t m = (mant << lz) & 0x03FFu;
-        uint32_t e = 113u - lz;
-        return bits_f(sign | (e << 23) | (m << 13));
-    }
-    if (exp == 31) return bits_f(sign | 0x7F800000u | (mant << 13));
-    return bits_f(sign | ((exp + 112u) << 23) | (mant << 13));
-}
+// f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_fp16.h.
 
 // prng.rs:98-130
 __device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
@@ -249,7 +213,14 @@ __device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
     int32_t noise = prng(seed, off) & mask;
     int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
     int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
-    return f16_to_f32(f32_to_f16_rne(bits_f((uint32_t)((p & (int32_t)0x80000000u) | r))));
+    // The reference converts sign | r to fp16 and back (prng.rs:129). That is the identity here,
+    // because sign | r is already an fp16 value. r is one of:
+    // - 0, or 65504;
+    // - the sign bit alone (-0.0), when a NaN's magnitude plus the noise wraps past 2^31;
+    // - a value with its (13 + sub) low bits clear. For ex >= 113 that leaves 10 fraction bits
+    //   below 65504 (an fp16 normal). For 103 <= ex <= 112 it leaves a multiple of 2^-24 below
+    //   2^-13 (fp16 subnormals and the lowest normal binade).
+    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
 }
 
 __device__ __forceinline__ float rne_fp16(float v) { return f16_to_f32(f32_to_f16_rne(v)); }

@@ -8,6 +8,8 @@ import os
 import subprocess
 import sys
 
+import pytest
+
 import bench
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -49,6 +51,22 @@ def test_variant_workloads():
     assert bench.workload(5, bound="radial")["bytes_per_param"] == 22
     assert bench.workload(5, state="param")["sdt"] == "bf16"
     assert bench.pmc_traffic_bytes(5, bound="radial") is None
+    # an fp32 master copy: p write-only (2), master read + write (8)
+    assert bench.workload(5, master="full")["bytes_per_param"] == 28
+    assert bench.workload(4, master="semi")["bytes_per_param"] == 20
+    assert bench.workload(5, state="param", master="full")["sdt"] == "f32"  # full master keeps fp32 state
+    assert bench.workload(5, state="param", master="semi")["bytes_per_param"] == 14 - 2 + 8
+    assert bench.workload(5, pdt="f16")["pdt"] == "f16" and bench.workload(5, pdt="f16")["bytes_per_param"] == 22
+    with pytest.raises(ValueError):
+        bench.workload(3, pdt="f16")
+    assert bench.pmc_traffic_bytes(5, master="full") is None
+
+
+def test_cpu_baseline_with_master_and_fp16():
+    wl = dict(bench.workload(5, master="full", pdt="f16"))
+    wl["n"] = 1 << 21
+    out = bench.cpu_baseline(wl, threads=2, target_s=0.3)
+    assert out["value"] > 0 and out["cores"] == 2
 
 
 def test_pmc_traffic_is_the_algorithmic_bytes_plus_the_count_atomics():
