@@ -44,7 +44,7 @@
 #include <vector>
 
 #include "luminav_hip.h"
-#include "lv_fp16.h"
+#include "lv_exact.h"
 
 namespace lv {
 
@@ -165,13 +165,18 @@ __device__ __forceinline__ float rclamp(float x, float lo, float hi) {
 // prng.rs:21-26 -- wrapping i32 arithmetic, arithmetic right shifts.
 // The multipliers are the reference's decimal i32 constants; the first one is close to, but not,
 // MurmurHash3's fmix32 constant.
-__device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
+// prng_mixed is the state before the last step, z ^ (z >> 16).
+__device__ __forceinline__ int32_t prng_mixed(int32_t seed, int32_t idx) {
     constexpr uint32_t kAdd = (uint32_t)-1640531527;  // wrapping_sub(1_640_531_527)
     constexpr uint32_t kMul1 = (uint32_t)-2048173461;
     constexpr uint32_t kMul2 = (uint32_t)-1028477387;
     int32_t z = (int32_t)((uint32_t)idx + (uint32_t)seed + kAdd);
     z = (int32_t)((uint32_t)(z ^ (z >> 16)) * kMul1);
-    z = (int32_t)((uint32_t)(z ^ (z >> 13)) * kMul2);
+    return (int32_t)((uint32_t)(z ^ (z >> 13)) * kMul2);
+}
+
+__device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
+    const int32_t z = prng_mixed(seed, idx);
     return z ^ (z >> 16);
 }
 
@@ -180,7 +185,7 @@ __device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
 __device__ __forceinline__ float sr_bf16(float v, int32_t seed, int32_t off) {
     uint32_t p = f_bits(v);
     uint32_t a = p & 0x7FFFFFFFu;
-    uint32_t noise = (uint32_t)prng(seed, off) & 0xFFFFu;
+    uint32_t noise = xor_fold16((uint32_t)prng_mixed(seed, off));  // prng(seed, off) & 0xFFFF
     uint32_t added = (a + noise) & 0xFFFF0000u;  // a <= 0x7F800000 when used: no wrap, never "negative"
     uint32_t r = added > 0x7F7F0000u ? 0x7F7F0000u : added;
     uint32_t fin = (p & 0x80000000u) | r;
@@ -199,7 +204,7 @@ __device__ __forceinline__ float rne_bf16(float v) {
     return bits_f(a > 0x7F800000u ? nan : fin);
 }
 
-// f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_fp16.h.
+// f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
 
 // prng.rs:98-130
 __device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
@@ -273,7 +278,7 @@ __device__ __forceinline__ float coordinate_bound(float step, float p_init, floa
         float bb = b * (b + fabsf(step));
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
-        float b = ratio * __builtin_sqrtf(__builtin_fmaf(p_init, p_init, 1.0e-4f));
+        float b = ratio * sqrt_rn(__builtin_fmaf(p_init, p_init, 1.0e-4f));
         return b * tanh_pade(step / b);
     }
 }
@@ -336,7 +341,7 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
         float diff = clamp_defect(g - m_new);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
-        float sigma = __builtin_fmaf(__builtin_sqrtf(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
+        float sigma = __builtin_fmaf(sqrt_rn(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
         return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
     } else if constexpr (MODE == LV_BUFFER_T2) {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
@@ -346,7 +351,7 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
         float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
-        float env = __builtin_fmaf(a.c_sigma, __builtin_sqrtf(__builtin_fmaxf(v_new, 0.0f)), env2);
+        float env = __builtin_fmaf(a.c_sigma, sqrt_rn(__builtin_fmaxf(v_new, 0.0f)), env2);
         return clm / env;
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);

@@ -10,24 +10,24 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-FP16_SRC = os.path.join(HERE, "fp16_check.hip")
-FP16_LIB = os.path.join(HERE, "libfp16check.so")
+EXACT_SRC = os.path.join(HERE, "exact_check.hip")
+EXACT_LIB = os.path.join(HERE, "libexactcheck.so")
 
 
 def build(verbose: bool = False) -> str:
     from luminamoon_amd import build_ext
 
-    tmp = FP16_LIB + ".tmp"
+    tmp = EXACT_LIB + ".tmp"
     cmd = [build_ext.hipcc(), *build_ext.HIPCC_FLAGS, "-I", os.path.join(ROOT, "luminamoon_amd", "csrc"),
-           FP16_SRC, "-o", tmp]
+           EXACT_SRC, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {FP16_SRC}")
-    os.replace(tmp, FP16_LIB)
-    return FP16_LIB
+        raise RuntimeError(f"hipcc failed building {EXACT_SRC}")
+    os.replace(tmp, EXACT_LIB)
+    return EXACT_LIB
 
 
 if __name__ == "__main__":

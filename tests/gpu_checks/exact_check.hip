@@ -1,0 +1,101 @@
+// Exhaustive check of the library's exact helpers (luminamoon_amd/csrc/lv_exact.h) against their
+// reference definitions, every input:
+//   f32 -> f16 against the reference's integer algorithm (prng.rs:29-67, restated here), 2^32;
+//   f16 -> f32 against prng.rs:69-96 (restated here), 2^16;
+//   sqrt_rn against the compiler's correctly rounded square root (IEEE, as Rust's f32::sqrt), 2^32;
+//   xor_fold16 against (z ^ (z >> 16)) & 0xFFFF with the arithmetic shift of prng.rs:25, 2^32.
+// Test infrastructure: built by __graft_entry__.build() into tests/gpu_checks/libexactcheck.so
+// and run by tests/test_gpu_exact_exhaustive.py.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "lv_exact.h"
+
+namespace {
+
+// prng.rs:29-67, integer form
+__device__ uint32_t ref_f32_to_f16(uint32_t bits) {
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x007FFFFFu;
+    if (exp == 255) return sign | (mant != 0 ? 0x7E00u : 0x7BFFu);
+    int32_t ne = exp - 112;
+    if (ne >= 31) return sign | 0x7BFFu;
+    if (ne <= 0) {
+        if (ne < -10) return sign;
+        uint32_t fm = mant | 0x00800000u;
+        uint32_t sh = (uint32_t)(14 - ne);
+        uint32_t half = 1u << (sh - 1);
+        return sign | ((fm + half - 1u + ((fm >> sh) & 1u)) >> sh);
+    }
+    uint32_t r = mant + 0x0FFFu + ((mant >> 13) & 1u);
+    uint32_t body = ((uint32_t)ne << 10) + (r >> 13);
+    return body >= 0x7C00u ? (sign | 0x7BFFu) : (sign | body);
+}
+
+// prng.rs:69-96, integer form
+__device__ uint32_t ref_f16_to_f32(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x03FFu;
+    if (exp == 0) {
+        if (mant == 0) return sign;
+        uint32_t lz = __clz(mant) - 21;
+        return sign | ((113u - lz) << 23) | (((mant << lz) & 0x03FFu) << 13);
+    }
+    if (exp == 31) return sign | 0x7F800000u | (mant << 13);
+    return sign | ((exp + 112u) << 23) | (mant << 13);
+}
+
+__device__ bool is_nan(uint32_t b) { return (b & 0x7FFFFFFFu) > 0x7F800000u; }
+
+__device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) {
+    const unsigned long long k = atomicAdd(count, 1ull);
+    if (k < 8) ex[k] = input;
+}
+
+// Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
+// NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
+// [4] xor_fold16 mismatches; ex[8 * c + k] holds the first inputs of counter c.
+__global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex) {
+    const uint32_t i = base + blockIdx.x * blockDim.x + threadIdx.x;
+    if (lv::f32_to_f16_rne(__uint_as_float(i)) != ref_f32_to_f16(i)) record(&out[0], ex + 0, i);
+    const uint32_t s = __float_as_uint(lv::sqrt_rn(__uint_as_float(i)));
+    const uint32_t s_ref = __float_as_uint(__builtin_sqrtf(__uint_as_float(i)));
+    if (s != s_ref && !(is_nan(s) && is_nan(s_ref))) record(&out[3], ex + 24, i);
+    if (lv::xor_fold16(i) != ((i ^ (uint32_t)((int32_t)i >> 16)) & 0xFFFFu)) record(&out[4], ex + 32, i);
+}
+
+__global__ void check_f16_to_f32(unsigned long long *out, uint32_t *ex) {
+    const uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;  // grid covers exactly 2^16
+    const uint32_t got = __float_as_uint(lv::f16_to_f32(h));
+    const uint32_t want = ref_f16_to_f32(h);
+    if (got == want) return;
+    if (is_nan(got) && is_nan(want) && (got >> 31) == (want >> 31)) {
+        atomicAdd(&out[2], 1ull);
+        return;
+    }
+    record(&out[1], ex + 8, h);
+}
+
+}  // namespace
+
+extern "C" int exact_check(unsigned long long *host_counts /* 5 */, uint32_t *host_examples /* 40 */) {
+    unsigned long long *out = nullptr;
+    uint32_t *ex = nullptr;
+    if (hipMalloc(&out, 5 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMalloc(&ex, 40 * sizeof(uint32_t)) != hipSuccess) return -1;
+    if (hipMemset(out, 0, 5 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMemset(ex, 0, 40 * sizeof(uint32_t)) != hipSuccess) return -1;
+    const uint32_t per = 1u << 24;  // 65536 blocks of 256 per launch; 256 launches cover 2^32
+    for (uint64_t base = 0; base < (1ull << 32); base += per) check_2_32<<<per / 256, 256>>>((uint32_t)base, out, ex);
+    check_f16_to_f32<<<(1u << 16) / 256, 256>>>(out, ex);
+    int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -2;
+    if (rc == 0 && hipMemcpy(host_counts, out, 5 * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
+        rc = -3;
+    if (rc == 0 && hipMemcpy(host_examples, ex, 40 * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) rc = -3;
+    (void)hipFree(out);
+    (void)hipFree(ex);
+    return rc;
+}
