@@ -63,7 +63,7 @@ WORKLOADS = {
 # 2.0) and WRITE_SIZE is exact (factor 1.0); TCC_EA0_RDREQ_DRAM_32B / TCC_EA0_WRREQ_WRITE_DRAM_32B
 # give the same byte totals for this kernel.
 PMC_TRAFFIC = {
-    5: dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u>", fetch_kib=39499801.875, write_kib=66010493.9375,
+    5: dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>", fetch_kib=39500422.71875, write_kib=66010502.75,
             probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0),
 }
 
