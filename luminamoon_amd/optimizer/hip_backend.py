@@ -124,7 +124,8 @@ def make_config(group: Dict[str, Any]) -> LvConfig:
 
 
 class _Workspace:
-    """Per-device zero-filled counter workspace; kernels leave it zeroed after each call."""
+    """Per-device workspace (count words, radial records, table-launch descriptors), allocated
+    zero-filled; the kernels leave its count words zeroed after each call."""
 
     def __init__(self) -> None:
         self._bufs: Dict[Any, torch.Tensor] = {}

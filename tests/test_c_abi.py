@@ -126,6 +126,14 @@ def test_host_side_rejections_without_device(lib):
     assert b"inactive" in lib.lv_last_error()
     t.n_inactive = 0
     t.grad = t.param
+    # more than 48 tensors need the table-launch regions of the workspace
+    many = (H.LvTensor * 49)()
+    for k in range(49):
+        many[k].numel, many[k].step = 10, 1
+        many[k].param, many[k].grad, many[k].exp_avg, many[k].exp_avg_sq, many[k].scratch = (
+            0x1000, 0x3000, 0x2000, 0x2400, 0x2800)
+    assert lib.lv_step_multi(ctypes.byref(cfg), many, 49, ws, WS, None) == -3
+    assert b"workspace too small" in lib.lv_last_error()
     # radial: same host checks (the call is never launched here)
     rcfg = _cfg(buffer="T2", bound_type="radial")
     assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, WS, None) == -3
