@@ -466,6 +466,14 @@ class LuminaV(Optimizer):
                 "Disabling fsdp_sync to prevent collective communication errors."
             )
             fsdp_sync = False
+        if fsdp_sync and torch.distributed.get_world_size() > 1:
+            # The reference all-reduces the per-tensor mask counts across ranks before the scale
+            # (fsdp_sync.py:20-38). This build steps one GPU per process without that collective,
+            # so a sharded run would silently use rank-local scales: refuse it instead.
+            raise NotImplementedError(
+                f"LuminaV: fsdp_sync=True across {torch.distributed.get_world_size()} ranks is not supported by "
+                "this build (one GPU per process, no cross-rank scratch all-reduce)."
+            )
 
         raw_cap = group.get("bucket_cap_mb", DEFAULT_BUCKET_CAP_MB)
         if raw_cap is None or not is_valid_number(raw_cap) or float(raw_cap) <= 0.0:

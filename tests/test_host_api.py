@@ -217,3 +217,24 @@ def test_state_dict_cleanliness_and_round_trip():
 def test_detect_hardware_shape():
     hw = LuminaV.detect_hardware()
     assert hw["backend"] == "hip" and "gpu_dispatch_threshold" in hw and "hip_backend_built" in hw
+
+
+def test_fsdp_sync_across_ranks_is_refused(monkeypatch):
+    """fsdp_sync all-reduces the mask counts across ranks in the reference (fsdp_sync.py:20-38);
+    this one-GPU build has no such collective, so it refuses a multi-rank fsdp_sync run instead
+    of silently stepping with rank-local scales. One rank, or no process group, is fine."""
+    import pytest
+    import torch
+
+    from luminamoon_amd import LuminaV
+
+    p = torch.nn.Parameter(torch.zeros(4))
+    monkeypatch.setattr(torch.distributed, "is_available", lambda: True)
+    monkeypatch.setattr(torch.distributed, "is_initialized", lambda: True)
+    monkeypatch.setattr(torch.distributed, "get_world_size", lambda *a, **k: 2)
+    with pytest.raises(NotImplementedError, match="fsdp_sync"):
+        LuminaV([p], fsdp_sync=True)
+    monkeypatch.setattr(torch.distributed, "get_world_size", lambda *a, **k: 1)
+    LuminaV([p], fsdp_sync=True)
+    monkeypatch.setattr(torch.distributed, "is_initialized", lambda: False)
+    LuminaV([p], fsdp_sync=True)
