@@ -111,6 +111,19 @@ def test_table_launches_thousands_of_tensors(oracle_mod, count, buffer, pdt, sdt
     are one table launch and an inline launch of 40, and 2000 are 960 + 960 + 80. Every buffer
     and scratch bit for bit over the two-pass first step and fused steps; the count words of both
     kinds of launch are left zero."""
+    _table_case(oracle_mod, count, buffer, pdt, sdt, extra)
+
+
+def test_table_launch_split_into_pieces(oracle_mod, monkeypatch):
+    """A table launch cut into pieces of 37 blocks (LV_MAX_GRID_BLOCKS): each piece finds its
+    tensors through the first units in the kernel arguments, and counts fold across pieces."""
+    monkeypatch.setenv("LV_MAX_GRID_BLOCKS", "37")
+    _table_case(oracle_mod, 100, "T2", "bf16", "f32", {})
+
+
+def _table_case(oracle_mod, count, buffer, pdt, sdt, extra):
+    """`count` ragged tensors (plus three larger ones) stepped three times, bitwise against the
+    oracle, with the count words of inline and table launches checked zero after every step."""
     import numpy as np
 
     _need_gpu()
