@@ -1387,7 +1387,7 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
 
 extern "C" {
 
-int lv_version(void) { return 100; }
+int lv_version(void) { return 200; }
 
 // Layout (every region a multiple of 256 B):
 //   [count words: kMaxDesc x kSlotWords words, 64 B apart][radial tickets: kMaxDesc u64, 512 B]
