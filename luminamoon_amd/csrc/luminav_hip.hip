@@ -41,6 +41,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "luminav_hip.h"
@@ -1266,26 +1267,36 @@ static int assign_units(Args &args, uint32_t unit_elems, Desc *table) {
 
 // Pinned host staging for the descriptor tables of table launches: kStageSlots tables per
 // device, used round-robin. A slot is written only after the upload that last read it has
-// finished (its event), so the host rarely waits and the uploads stay asynchronous.
+// finished (its event), so the host rarely waits and the uploads stay asynchronous. A slot is
+// leased to one call from acquire_staging until its upload is enqueued (release_staging), so
+// host threads stepping on the same device never write the same slot.
 constexpr int kStageSlots = 4;
 
 struct Staging {
     int dev;
     Desc *host;
     hipEvent_t ev[kStageSlots];
-    bool used[kStageSlots];
+    bool used[kStageSlots];  // an upload was enqueued from the slot (its event was recorded)
+    bool busy[kStageSlots];  // leased to a call that has not enqueued its upload yet
     int next;
+};
+
+struct StagingLease {
+    Staging *S = nullptr;
+    int slot = -1;
+    Desc *table = nullptr;
+    hipEvent_t ev = nullptr;
 };
 
 static std::mutex g_stage_mu;
 static std::vector<Staging *> g_stage;
 
-// A staging table for the current device, free for the host to write. Allocates the device's
-// ring on first use (the only allocation of the step path, once per device and process).
-static int acquire_staging(Desc **table, hipEvent_t *ev) {
+// Leases a staging table of the current device, free for the host to write. Allocates the
+// device's ring on first use (the only allocation of the step path, once per device and process).
+static int acquire_staging(StagingLease &lease) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(LV_STATUS_NO_DRIVER, "no HIP device");
-    std::lock_guard<std::mutex> lk(g_stage_mu);
+    std::unique_lock<std::mutex> lk(g_stage_mu);
     Staging *S = nullptr;
     for (Staging *x : g_stage)
         if (x->dev == dev) S = x;
@@ -1306,14 +1317,32 @@ static int acquire_staging(Desc **table, hipEvent_t *ev) {
         S = new Staging(fresh);  // kept until the process ends
         g_stage.push_back(S);
     }
-    const int k = S->next;
+    int k = S->next;
+    while (S->busy[k]) {  // every slot leased by other threads' calls: wait for one to enqueue
+        lk.unlock();
+        std::this_thread::yield();
+        lk.lock();
+        k = S->next;
+    }
     S->next = (k + 1) % kStageSlots;
     if (S->used[k] && hipEventSynchronize(S->ev[k]) != hipSuccess)
         return fail(LV_STATUS_EXECUTION_FAILED, "staging event wait failed");
-    S->used[k] = true;
-    *table = S->host + (size_t)k * kTableMax;
-    *ev = S->ev[k];
+    S->busy[k] = true;
+    lease.S = S;
+    lease.slot = k;
+    lease.table = S->host + (size_t)k * kTableMax;
+    lease.ev = S->ev[k];
     return LV_STATUS_SUCCESS;
+}
+
+// Ends a lease: `enqueued` says whether an upload from the slot was enqueued (and its event
+// recorded after it).
+static void release_staging(StagingLease &lease, bool enqueued) {
+    if (!lease.S) return;
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    if (enqueued) lease.S->used[lease.slot] = true;
+    lease.S->busy[lease.slot] = false;
+    lease.S = nullptr;
 }
 
 // Table launches: assigns the units of the args.ndesc descriptors staged in `table` and
@@ -1543,12 +1572,12 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             flags |= (uint32_t)h.gt << 8;
             args.flags = flags;
             args.ndesc = (int32_t)(end - begin);
-            Desc *staged = nullptr;
-            hipEvent_t staged_ev = nullptr;
+            StagingLease lease;
             if (table) {
-                rc = acquire_staging(&staged, &staged_ev);
+                rc = acquire_staging(lease);
                 if (rc != LV_STATUS_SUCCESS) return rc;
             }
+            Desc *staged = lease.table;
             for (size_t k = begin; k < end; k++) {
                 const lv_tensor &T = tensors[items[k].idx];
                 Desc &D = table ? staged[k - begin] : args.d[k - begin];
@@ -1573,7 +1602,8 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
             args.unit_cnt = reinterpret_cast<uint32_t *>(ws + kZeroBytes + kRunBytes + kChunkBytes + kUnitSqBytes);
             if (table) {
                 args.dtab = reinterpret_cast<const Desc *>(ws + kFixedBytes + kTableSlotBytes);
-                rc = stage_table(args, cfg->buffer, h.pt, h.st, staged, staged_ev, stream);
+                rc = stage_table(args, cfg->buffer, h.pt, h.st, staged, lease.ev, stream);
+                release_staging(lease, rc == LV_STATUS_SUCCESS);
                 if (rc != LV_STATUS_SUCCESS) return rc;
             }
             if (h.pass == kCount) {

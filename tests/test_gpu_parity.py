@@ -121,6 +121,53 @@ def test_table_launch_split_into_pieces(oracle_mod, monkeypatch):
     _table_case(oracle_mod, 100, "T2", "bf16", "f32", {})
 
 
+def test_table_launches_from_two_host_threads(oracle_mod):
+    """Two host threads, each with its own stepper (workspace) and stream, step 100-tensor sets
+    at the same time: table launches share the device's pinned staging ring, whose slots are
+    leased to one call at a time. Both end bit for bit equal to the oracle."""
+    import threading
+
+    import numpy as np
+
+    _need_gpu()
+    O = oracle_mod
+    group = group_dict(buffer="T2", lr=1e-3)
+    cfg = oracle_config(O, group)
+    rng = np.random.default_rng(5)
+    sets = []
+    for k in range(2):
+        sizes = [int(np.exp(rng.uniform(0, np.log(5000)))) + 1 for _ in range(100)]
+        host = TensorSet(sizes, "bf16", "bf16", "f32", True, False, 40 + k)
+        sets.append((host, host.to("cuda"), _stepper(), torch.cuda.Stream()))
+    steps = 6
+    grads = [[host.grads(s, 50 + k) for s in range(1, steps + 1)] for k, (host, _, _, _) in enumerate(sets)]
+    dev_grads = [[[g.cuda() for g in gs] for gs in per] for per in grads]
+    torch.cuda.synchronize()
+    errors = []
+
+    def run(k):
+        try:
+            host, dev, st, stream = sets[k]
+            with torch.cuda.stream(stream):
+                for s in range(1, steps + 1):
+                    dev.hip_step(st, group, dev_grads[k][s - 1], s)
+            stream.synchronize()
+        except Exception as e:  # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+    print("[case] table launches from two host threads", flush=True)
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for k, (host, dev, _, _) in enumerate(sets):
+        for s in range(1, steps + 1):
+            host.oracle_step(O, cfg, grads[k][s - 1], s)
+        host.assert_equal(dev, f"thread {k}")
+
+
 def _table_case(oracle_mod, count, buffer, pdt, sdt, extra):
     """`count` ragged tensors (plus three larger ones) stepped three times, bitwise against the
     oracle, with the count words of inline and table launches checked zero after every step."""
