@@ -124,7 +124,8 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count,
  * luminav_triton_step_f32 (optimizer/include/luminav_triton_standalone.h:89-111) without the
  * engine handle; ema_decay is the reference default for the buffer mode, cautious_clamp_min
  * 0.5, stochastic rounding and fused single pass on (config.rs:297-321). Uses an internal
- * per-device workspace allocated on first use.
+ * per-device workspace allocated on first use: calls on one device share it, so calls on
+ * different streams must not overlap in time (stream-ordered calls on one stream are fine).
  */
 int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
                 float *master_param, float *scratch, size_t num_elements, float lr, float beta1,
