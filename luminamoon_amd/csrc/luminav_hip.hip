@@ -166,27 +166,30 @@ __device__ __forceinline__ float rclamp(float x, float lo, float hi) {
 // prng.rs:21-26 -- wrapping i32 arithmetic, arithmetic right shifts.
 // The multipliers are the reference's decimal i32 constants; the first one is close to, but not,
 // MurmurHash3's fmix32 constant.
+// The hash input is z0 = idx + seed + kPrngAdd (wrapping); callers form z0 themselves, so a
+// thread adds a per-stream base once and each element only its constant offset.
 // prng_mixed is the state before the last step, z ^ (z >> 16).
-__device__ __forceinline__ int32_t prng_mixed(int32_t seed, int32_t idx) {
-    constexpr uint32_t kAdd = (uint32_t)-1640531527;  // wrapping_sub(1_640_531_527)
+constexpr uint32_t kPrngAdd = (uint32_t)-1640531527;  // wrapping_sub(1_640_531_527)
+
+__device__ __forceinline__ int32_t prng_mixed(uint32_t z0) {
     constexpr uint32_t kMul1 = (uint32_t)-2048173461;
     constexpr uint32_t kMul2 = (uint32_t)-1028477387;
-    int32_t z = (int32_t)((uint32_t)idx + (uint32_t)seed + kAdd);
+    int32_t z = (int32_t)z0;
     z = (int32_t)((uint32_t)(z ^ (z >> 16)) * kMul1);
     return (int32_t)((uint32_t)(z ^ (z >> 13)) * kMul2);
 }
 
-__device__ __forceinline__ int32_t prng(int32_t seed, int32_t idx) {
-    const int32_t z = prng_mixed(seed, idx);
+__device__ __forceinline__ int32_t prng(uint32_t z0) {
+    const int32_t z = prng_mixed(z0);
     return z ^ (z >> 16);
 }
 
 // prng.rs:137-160 (value form: f32 carrying the bf16 bits). Branch-free: both the finite and
 // the NaN result are formed and one is selected, so a wave never splits on NaN lanes.
-__device__ __forceinline__ float sr_bf16(float v, int32_t seed, int32_t off) {
+__device__ __forceinline__ float sr_bf16(float v, uint32_t z0) {
     uint32_t p = f_bits(v);
     uint32_t a = p & 0x7FFFFFFFu;
-    uint32_t noise = xor_fold16((uint32_t)prng_mixed(seed, off));  // prng(seed, off) & 0xFFFF
+    uint32_t noise = xor_fold16((uint32_t)prng_mixed(z0));  // prng(z0) & 0xFFFF
     uint32_t added = (a + noise) & 0xFFFF0000u;  // a <= 0x7F800000 when used: no wrap, never "negative"
     uint32_t r = added > 0x7F7F0000u ? 0x7F7F0000u : added;
     uint32_t fin = (p & 0x80000000u) | r;
@@ -208,7 +211,7 @@ __device__ __forceinline__ float rne_bf16(float v) {
 // f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
 
 // prng.rs:98-130
-__device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
+__device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
     int32_t p = (int32_t)f_bits(v);
     int32_t a = p & 0x7FFFFFFF;
     int32_t ex = (a >> 23) & 0xFF;
@@ -216,7 +219,7 @@ __device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
     sub = sub > 0 ? sub : 0;
     sub = sub < 11 ? sub : 11;
     int32_t mask = (int32_t)((1u << (13 + sub)) - 1u);
-    int32_t noise = prng(seed, off) & mask;
+    int32_t noise = prng(z0) & mask;
     int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
     int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
     // The reference converts sign | r to fp16 and back (prng.rs:129). That is the identity here,
@@ -231,13 +234,14 @@ __device__ __forceinline__ float sr_fp16(float v, int32_t seed, int32_t off) {
 
 __device__ __forceinline__ float rne_fp16(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
 
-// prng.rs:180-195; dtype is a compile-time constant at every call site.
+// prng.rs:180-195; dtype is a compile-time constant at every call site. z0 is the element's
+// hash input for the buffer's seed (offset + seed + kPrngAdd).
 template <int DT>
-__device__ __forceinline__ float quantize(float v, int32_t seed, int32_t off, bool sr) {
+__device__ __forceinline__ float quantize(float v, uint32_t z0, bool sr) {
     if constexpr (DT == LV_DTYPE_BF16) {
-        return sr ? sr_bf16(v, seed, off) : rne_bf16(v);
+        return sr ? sr_bf16(v, z0) : rne_bf16(v);
     } else if constexpr (DT == LV_DTYPE_F16) {
-        return sr ? sr_fp16(v, seed, off) : rne_fp16(v);
+        return sr ? sr_fp16(v, z0) : rne_fp16(v);
     } else {
         return v;
     }
@@ -509,11 +513,20 @@ struct Seeds {
     int32_t m, p, v;
 };
 
+// Hash inputs of one element offset for the m, p and v streams.
+struct HashIn {
+    uint32_t m, p, v;
+};
+
+__device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
+    return {off + (uint32_t)sd.m + kPrngAdd, off + (uint32_t)sd.p + kPrngAdd, off + (uint32_t)sd.v + kPrngAdd};
+}
+
 // Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
 // Returns the cautious mask bit; u_eff is the (masked) direction whose square feeds the radial
 // norm (dual.rs:176-180).
 template <int MODE, int PT, int ST>
-__device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const Seeds &sd, int32_t off,
+__device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const HashIn &z,
                                                float cs, float bs, float p_init, float g_raw, float &m_io,
                                                float &v_io, float &p_out, float &mp_out, float &u_eff) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
@@ -524,8 +537,8 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
     float u = compute_u<MODE>(a, flags & kFClampV, g, m_io, v_io, m_new, v_new);
     bool active = (u * g) > 0.0f;
     float m_mask = active ? 1.0f : 0.0f;
-    m_io = quantize<ST>(m_new, sd.m, off, sr);
-    if constexpr (kDual) v_io = quantize<ST>(v_new, sd.v, off, sr);
+    m_io = quantize<ST>(m_new, z.m, sr);
+    if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
     u_eff = (flags & kFCautious) ? u * m_mask : u;
     float delta = (flags & kFCautious) ? u_eff * cs : u;
     float step = a.lr * delta;
@@ -536,9 +549,9 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
     float p_upd = p_dec - step;
     if (flags & kFMaster) {
         mp_out = p_upd;
-        p_out = quantize<PT>(p_upd, sd.p, off, false);
+        p_out = quantize<PT>(p_upd, z.p, false);
     } else {
-        p_out = quantize<PT>(p_upd, sd.p, off, sr);
+        p_out = quantize<PT>(p_upd, z.p, sr);
     }
     return active ? 1u : 0u;
 }
@@ -755,13 +768,16 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
         float pin[8], pout[8], mpout[8];
         if (master) decode_raw<LV_DTYPE_F32, H>(cur.p, pin);
         else decode_raw<PT, H>(cur.p, pin);
+        // the thread's hash inputs at its first element (offsets wrap at 2^32 as (int32)idx does)
+        const HashIn zb = hash_in(tv.sd, (uint32_t)e0 + tv.ibase);
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
             float ue;
-            const uint64_t ej = e0 + (j < 4 ? (uint64_t)j : (uint64_t)(kHalf + j - 4));
-            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, tv.sd, (int32_t)((uint32_t)ej + tv.ibase), tv.cs, tv.bs,
-                                                    pin[j], g[j], m[j], vj, pout[j], mpout[j], ue);
+            const uint32_t jj = j < 4 ? (uint32_t)j : kHalf + (uint32_t)j - 4u;  // a constant once unrolled
+            const HashIn zj = {zb.m + jj, zb.p + jj, zb.v + jj};
+            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+                                                    mpout[j], ue);
             if constexpr (kDual) v[j] = vj;
             if constexpr (kCounting) {
                 cnt += act;
@@ -814,8 +830,8 @@ __device__ __forceinline__ void scalar_unit(const Args &a, const Desc &D, const 
         } else {
             float pin = master ? D.mp[i] : load1<PT>(D.p, i);
             float pout, mpout, ue;
-            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, tv.sd, (int32_t)((uint32_t)i + tv.ibase), tv.cs, tv.bs, pin,
-                                                    g, m, v, pout, mpout, ue);
+            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs,
+                                                    pin, g, m, v, pout, mpout, ue);
             if (!inactive) {
                 store1<PT>(D.p, i, pout);
                 if (master) D.mp[i] = mpout;
