@@ -758,7 +758,8 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
             float ue;
-            cnt += count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
+            // every lane of the wave is on this path: count the wave's mask bits in one ballot
+            cnt += (uint32_t)__popcll(__ballot(count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue)));
             if (radial) {
                 su += (double)(ue * ue);
                 sp += (double)(pin[j] * pin[j]);
@@ -780,7 +781,7 @@ __device__ __forceinline__ void process_unit(const Args &a, const Desc &D, const
                                                     mpout[j], ue);
             if constexpr (kDual) v[j] = vj;
             if constexpr (kCounting) {
-                cnt += act;
+                cnt += (uint32_t)__popcll(__ballot(act));  // the wave's count (all lanes active here)
                 if (radial) {
                     su += (double)(ue * ue);
                     sp += (double)(pin[j] * pin[j]);
@@ -956,7 +957,10 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         // its elements still enter the radial norms.
         if (!kCounting && cover == 2) return;
     }
-    if (cover == 0 && tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H))) {
+    // Vector path: cnt ends as the wave's count (the same in every lane, from ballots); per-element
+    // path: cnt is the lane's count.
+    const bool vec = cover == 0 && tv.vec_ok && unit < tv.t_begin + (uint32_t)(tv.n / (kHalf * H));
+    if (vec) {
         const Inflight f = issue_unit<MODE, PT, ST, PASS, H>(D, tv, flags, radial, unit);
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
@@ -967,7 +971,9 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     }
     if constexpr (kCounting) {
         if (radial) {
-            block_sums(sh, su, sp, cnt);
+            uint32_t lane_cnt = vec ? ((threadIdx.x & 63) == 0 ? cnt : 0u) : cnt;
+            block_sums(sh, su, sp, lane_cnt);
+            cnt = lane_cnt;
             if (threadIdx.x == 0) {
                 const uint32_t k = unit - a.unit_base;  // < piece_units
                 a.unit_sq[2 * (size_t)k] = su;
@@ -975,7 +981,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
                 a.unit_cnt[k] = cnt;
             }
         } else {
-            cnt = wave_sum(cnt);
+            if (!vec) cnt = wave_sum(cnt);  // block-uniform branch
             if ((threadIdx.x & 63) == 0) sh.cnt[threadIdx.x >> 6] = cnt;
             __syncthreads();
             if (threadIdx.x == 0) {
