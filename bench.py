@@ -288,8 +288,9 @@ def main() -> int:
     ap.add_argument("--reserve-gb", type=float, default=200.0)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the step shards by "
-                                   "element ranges, see DESIGN.md)", "n_gpus": args.gpus}), flush=True)
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (across GPUs the step "
+                                   "would shard each bucket by element ranges, one range per rank)",
+                          "n_gpus": args.gpus}), flush=True)
         return 2
 
     import torch
