@@ -94,44 +94,84 @@ typedef struct lv_tensor {
 /* Library version, major*10000 + minor*100 + patch. */
 int lv_version(void);
 
-/* Bytes of device workspace lv_step_multi needs for a call with n_tensors tensors (the launches
- * of a call reuse per-launch regions): 195 KiB of cautious mask-count words (48 tensors per
- * launch x 65 words x 64 bytes) and 512 bytes of radial-fold tickets, which must be zero before a
- * call, then 35 KiB of radial running sums and chunk records and 80 MiB of radial unit records
- * (one launch piece of 2^22 units x 20 bytes), which need no clearing. Above 48 tensors, table
- * launches (up to 960 tensors each) add 3.8 MiB of count words, which must be zero, and a 75 KiB
- * descriptor table. The caller allocates it once,
- * zero-filled; the kernels leave the count words and tickets zeroed again after every call, so it
- * is reused from step to step. Calls that share one workspace must not overlap. After a call
- * that returned LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero the workspace again
- * before reusing it. */
+/* Workspace. lv_step_multi needs caller-owned device memory, 256-byte aligned, ZERO-FILLED before
+ * its first use; every call leaves all of it zero again (the kernels re-zero the cautious count
+ * slots and tickets they use, and the radial fold zeroes every record it reads), so one workspace
+ * serves every later call, whatever its tensors or options. Calls that share a workspace must
+ * not overlap in time (stream-ordered calls on one stream are fine). After a call that returned
+ * LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero it again before reusing it.
+ * Layout of one call: 195 KiB of inline count slots (48 tensors x 65 slots x 64 B) and 2 KiB of
+ * radial tickets and running sums; with more than 48 tensors, table count slots
+ * (min(64, units) + 1 slots of 64 B per tensor, units of 1024 elements); with the radial bound,
+ * 32 B of chunk record per 4096 units and 20 B of unit record per unit, up to one piece of 2^22
+ * units (80 MiB). No radial space is needed without the radial bound. */
+
+/* Bytes of workspace any call with n_tensors tensors can need (64 count slots per tensor and a
+ * full radial piece: an upper bound for callers that do not inspect their tensors). */
 size_t lv_workspace_bytes(int n_tensors);
+
+/* Bytes of workspace this call needs (the same arguments as lv_step_multi; step counters and
+ * pointers do not matter, only the sizes, the count and whether the radial bound is on). */
+size_t lv_workspace_bytes_for(const lv_config *cfg, const lv_tensor *tensors, int count);
 
 /*
  * One optimizer step over `count` tensors, in place, asynchronous on `stream`.
  * Replaces the reference's GPU seam LuminaVGpuMixin._step_gpu_group
  * (python/luminamoon/optimizer/gpu_backend.py:2603-2733) and the CPU seam
  * step_pyo3 -> process_work_item (optimizer/src/python_ffi/mod.rs:201-391,
- * optimizer/src/python_ffi/worker.rs:77-179) with one multi-tensor launch per
- * (dtype, step, pass) class instead of one launch per tensor.
+ * optimizer/src/python_ffi/worker.rs:77-179) with one multi-tensor launch (pair) per
+ * (dtype, step, pass) class instead of one launch per tensor: up to 48 tensors in the kernel
+ * arguments, any number above that from a descriptor table in device memory. The tables belong to
+ * the library (a small ring per device, allocated on first use and grown when a call needs more);
+ * a call whose table equals one already on the device launches with no upload.
+ * Validation follows step_pyo3 (mod.rs:57-173): null pointers (-1), dtype codes, master and
+ * exp_avg_sq presence, and pointer aliasing (-3 with the reference's "Pointer aliasing detected"
+ * messages): no param, exp_avg, exp_avg_sq, master_param or scratch buffer may appear twice or
+ * overlap another, and no grad may overlap any of them.
  * Returns LV_STATUS_* ; lv_last_error() describes a failure.
  */
 int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count,
                   void *workspace, size_t workspace_bytes, void *stream);
 
 /*
- * Single fp32 tensor step on device pointers, argument-for-argument the reference's
- * luminav_triton_step_f32 (optimizer/include/luminav_triton_standalone.h:89-111) without the
- * engine handle; ema_decay is the reference default for the buffer mode, cautious_clamp_min
- * 0.5, stochastic rounding and fused single pass on (config.rs:297-321). Uses an internal
- * per-device workspace allocated on first use: calls on one device share it, so calls on
- * different streams must not overlap in time (stream-ordered calls on one stream are fine).
+ * Single fp32 tensor step with luminav_triton_step_f32's argument mapping
+ * (optimizer/crates/luminav-triton-aot/src/c_api.rs:108-199): buffer_mode 1 is TD-CLM and every
+ * other value the dual buffer (c_api.rs:143-146); exp_avg_sq is used only when buffer_mode == 2
+ * (c_api.rs:120-124), so any other dual-buffer call fails; bound_mode 1 radial, 2 coordinate,
+ * anything else no bound; master weights iff master_param != NULL; cautious_clamp_min 0.5,
+ * ema_decay the buffer mode's default, stochastic rounding off, fused single pass on; status -1
+ * for a null param/grad/exp_avg/scratch and -4 for every other failure (c_api.rs:178-181).
+ * The one deliberate difference: device pointers and a stream instead of the engine and host
+ * buffers (luminav_triton_step_f32 below takes those). The step runs like lv_step_multi's (the
+ * reference CPU core's pass selection). Uses an internal per-device workspace allocated on first
+ * use: calls on one device share it, so calls on different streams must not overlap in time.
  */
 int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
                 float *master_param, float *scratch, size_t num_elements, float lr, float beta1,
                 float beta2, float eps, float weight_decay, float tau, float lam, int buffer_mode,
                 int cautious, int bound_mode, float bound_ratio, uint64_t step, uint32_t seed,
                 void *stream);
+
+/*
+ * The reference's standalone C API (optimizer/include/luminav_triton_standalone.h:21-111,
+ * optimizer/crates/luminav-triton-aot/src/c_api.rs:9-199), same names, signatures and status
+ * codes, so a C program written against that header links against this library unchanged.
+ * luminav_triton_engine_create: the current HIP device and a stream of its own; NULL when no
+ * device is present. get_platform: "rocm" ("none" for NULL). get_arch: the device's gfx name,
+ * e.g. "gfx950" ("unknown" for NULL). luminav_triton_step_f32 takes HOST buffers: it copies
+ * them to the device, steps as lv_step_f32 does, copies param, exp_avg, exp_avg_sq (mode 2),
+ * master_param and scratch back and returns when done. Calls on one engine are serialised.
+ */
+typedef struct LuminaVTritonEngine LuminaVTritonEngine;
+LuminaVTritonEngine *luminav_triton_engine_create(void);
+void luminav_triton_engine_destroy(LuminaVTritonEngine *engine);
+const char *luminav_triton_get_platform(const LuminaVTritonEngine *engine);
+const char *luminav_triton_get_arch(const LuminaVTritonEngine *engine);
+int luminav_triton_step_f32(LuminaVTritonEngine *engine, float *param, const float *grad,
+                            float *exp_avg, float *exp_avg_sq, float *master_param, float *scratch,
+                            size_t num_elements, float lr, float beta1, float beta2, float eps,
+                            float weight_decay, float tau, float lam, int buffer_mode, int cautious,
+                            int bound_mode, float bound_ratio, uint64_t step, uint32_t seed);
 
 /* Description of the last error on this thread ("" if none). */
 const char *lv_last_error(void);

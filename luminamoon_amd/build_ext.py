@@ -1,5 +1,9 @@
 """Builds libluminav_hip.so for gfx950 with hipcc (in-tree, into luminamoon_amd/_lib/).
 
+Five objects compiled in parallel and linked into one shared library: the host side and C ABI
+(csrc/luminav_hip.hip) and the kernels of each buffer mode (csrc/lv_kernels.hip with
+-DLV_MODE=1..4).
+
 Flags that the bitwise-parity contract depends on:
   -ffp-contract=off                          no fused multiply-add except the explicit fmaf calls
   -fhip-fp32-correctly-rounded-divide-sqrt   IEEE division and square root
@@ -11,13 +15,18 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "luminav_hip.hip")
+CSRC = os.path.join(HERE, "csrc")
+HOST_SRC = os.path.join(CSRC, "luminav_hip.hip")
+KERNEL_SRC = os.path.join(CSRC, "lv_kernels.hip")
+SRC = HOST_SRC
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libluminav_hip.so")
 ARCH = os.environ.get("LUMINAV_OFFLOAD_ARCH", "gfx950")
+MODES = (1, 2, 3, 4)  # LV_BUFFER_TDCLM, _DUAL, _T1, _T2
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -25,6 +34,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]
+COMPILE_FLAGS = [f for f in HIPCC_FLAGS if f != "-shared"]
 
 
 def hipcc() -> str:
@@ -34,17 +44,31 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), SRC, "-o", tmp]
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {SRC}")
+        raise RuntimeError(f"hipcc failed building {what}")
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    jobs = [([hipcc(), *COMPILE_FLAGS, *inc, "-c", HOST_SRC, "-o", os.path.join(OUT_DIR, "host.o")], HOST_SRC)]
+    for m in MODES:
+        jobs.append(([hipcc(), *COMPILE_FLAGS, *inc, f"-DLV_MODE={m}", "-c", KERNEL_SRC,
+                      "-o", os.path.join(OUT_DIR, f"kernels_{m}.o")], f"{KERNEL_SRC} (mode {m})"))
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        for f in [ex.submit(_run, cmd, what, verbose) for cmd, what in jobs]:
+            f.result()
+    tmp = OUT + ".tmp"
+    objs = [os.path.join(OUT_DIR, "host.o")] + [os.path.join(OUT_DIR, f"kernels_{m}.o") for m in MODES]
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], OUT, verbose)
     os.replace(tmp, OUT)
+    for o in objs:
+        os.remove(o)
     return OUT
 
 

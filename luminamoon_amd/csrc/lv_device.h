@@ -1,0 +1,1230 @@
+// Device side of the MI355X LuminaV step: constants, descriptor and argument layouts, the exact
+// per-element arithmetic, the unit kernel, the radial fold kernel and the kernel pickers. Included
+// by the per-mode kernel units (lv_kernels.hip, one object per buffer mode so that they compile in
+// parallel) and, for the layouts alone, by the host side (luminav_hip.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "luminav_hip.h"
+#include "lv_exact.h"
+
+namespace lv {
+
+
+constexpr int kThreads = 256;
+constexpr uint32_t kHalf = kThreads * 4;     // a thread owns 4 consecutive elements of each half
+
+// Halves per work unit of a unit launch. With f32 state the step is HBM-bound and 1024-element
+// units stream best (measured in one process: T2 bf16/f32 23.2 vs 23.6 ms, T1 bf16/f32 2.17 vs
+// 2.25 ms, CLM and TD-CLM f32 0.58 vs 0.63 ms and 0.41 vs 0.44 ms for 1024 vs 2048). With 16-bit
+// state, stochastic rounding of m (and v) makes the step VALU-bound and 2048-element units are
+// faster (T2 bf16/bf16 3.05 vs 3.40 ms, T1 bf16/bf16 2.22 vs 2.49 ms).
+constexpr int unit_halves(int mode, int pt, int st) {
+    (void)mode;
+    (void)pt;
+    return st == LV_DTYPE_F32 ? 1 : 2;
+}
+constexpr int kMaxDesc = 48;                 // tensors per inline launch (kernel argument table, < 4 KiB)
+constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
+constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
+constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-byte segment
+// Slot word: mask count << kTicketBits | blocks that reported. A tensor has < 2^32 units of
+// >= 1024 elements and at most 2^42 elements, so a slot sees <= 2^26 blocks (27 bits) and
+// counts <= 2^36 elements (37 bits). Fold word: count << 7 | slots completed (<= 64).
+constexpr int kTicketBits = 27;
+constexpr int kFoldBits = 7;
+constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
+// Radial counting launches: units per piece (one workspace record each: 2 doubles + a u32 count),
+// and unit records one fold block sums into a chunk record.
+constexpr uint32_t kRadialPiece = 1u << 22;
+constexpr uint32_t kFoldChunk = 4096;  // fold blocks per full piece: kRadialPiece / kFoldChunk
+constexpr int kFoldBatch = 16;         // unit records a fold thread loads before adding them
+constexpr uint32_t kMaxChunks = kRadialPiece / kFoldChunk + kMaxDesc;  // chunks of one piece
+// A chunk's mask count (<= kFoldChunk units x 2048 elements) fits the u32 chunk sums; the
+// sums over chunks run in u64.
+static_assert((uint64_t)kFoldChunk * 2048u <= 0xFFFFFFFFull, "chunk counts fit 32 bits");
+
+enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
+
+enum Flags : uint32_t {
+    kFDynamic = 1u << 31,  // template flag set: read the flags from the launch arguments
+    kFCautious = 1u << 0,
+    kFSR = 1u << 1,
+    kFMaster = 1u << 2,
+    kFWeightDecay = 1u << 3,
+    kFClampV = 1u << 4,
+    kFRadial = 1u << 5,
+    kFCoordinate = 1u << 6,
+};
+
+// One tensor of a launch (80 bytes): in the kernel arguments (inline launches) or in the
+// workspace (table launches).
+struct Desc {
+    void *p;
+    const void *g;
+    void *m;
+    void *v;
+    float *mp;
+    float *scratch;
+    uint64_t n;
+    uint32_t unit_begin;  // first work unit of this tensor in the launch's unit space
+    uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
+    uint32_t ibase;       // low 32 bits of index_base (the SR offset is taken mod 2^32)
+    uint32_t nskip;       // inactive [begin, end) ranges in `skip` (sorted, disjoint)
+    const uint64_t *skip;
+};
+
+// A tensor of a table launch, in device memory: its descriptor, the end of its unit range and the
+// first of its count slots (64-byte slot index into Args::slots; the tensor has
+// table_count_slots(units) slots and one fold slot after them).
+struct TDesc {
+    Desc d;
+    uint32_t unit_end;
+    uint32_t slot_base;
+};
+
+// Count slots of a tensor of `units` work units in a table launch: the smallest power of two that
+// keeps every slot at <= 64 blocks, at most kSlots. Inline launches give every tensor
+// min(kSlots, units) slots instead (their slot words are preallocated).
+__host__ __device__ inline uint32_t table_count_slots(uint32_t units) {
+    const uint32_t c = (units + 63u) >> 6;
+    if (c <= 1u) return 1u;
+    if (c >= kSlots) return kSlots;
+    return 1u << (32 - __builtin_clz(c - 1u));
+}
+
+// Radial-bound sums of a run of units: sum u_eff^2, sum p^2 (f64), mask count.
+struct RadialSum {
+    double su, sp;
+    unsigned long long cnt, pad;
+};
+
+// Launch-uniform constants: hyper-parameters, per-step coefficients, tensor table.
+struct Args {
+    float lr, b1, b2, omb1, omb2, b1sq, omb1sq, eps, lam, lam1, neg_lr_wd, ratio;
+    float c1, c2, c_sigma, ema, ema_c, clamp_min;
+    uint32_t seed_base;  // low 32 bits of seed + step * 0x9E3779B9 (prng.rs:4-13)
+    uint32_t flags;      // Flags | grad dtype << 8
+    uint32_t total_units;
+    uint32_t unit_base;  // unit launches: the blocks cover units [unit_base, unit_base + grid)
+    uint32_t xcds;       // unit launches: XCDs the device dispatches workgroups over (>= 1)
+    uint32_t xcd_q, xcd_r;  // unit launches: grid / xcds and grid % xcds of this launch
+    int32_t ndesc;
+    uint32_t piece_units;  // radial launches: units of the current piece ([unit_base, + piece_units))
+    uint32_t group;        // table launches: tensors per head (ubegin[h] is tensor h * group's first unit)
+    uint32_t nheads;       // table launches: entries of ubegin
+    uint32_t pad_;
+    uint64_t xcd_recip;  // unit launches: floor(2^40 / xcds) + 1, so b / xcds == (b * xcd_recip) >> 40
+    unsigned long long *slots;    // counting launches: count slots (inline: kSlotWords per tensor, in order)
+    unsigned long long *tickets;  // radial fold: finished chunks of the piece, per tensor (left zero)
+    RadialSum *run;               // radial fold: per tensor, the sums of the pieces folded so far
+    RadialSum *chunks;            // radial fold: one record per chunk of the piece
+    double *unit_sq;              // radial: per unit of the piece, (sum u_eff^2, sum p^2)
+    uint32_t *unit_cnt;           // radial: per unit of the piece, the mask count
+    const TDesc *dtab;            // table launches: the tensor table in device memory
+    union {
+        Desc d[kMaxDesc];  // inline launches: the tensor table
+        uint32_t ubegin[kMaxDesc * sizeof(Desc) / sizeof(uint32_t)];  // table launches: first unit per head
+    };
+};
+
+// Table launches: any number of tensors in device memory; the kernel arguments hold the first unit
+// of every group-th tensor (the heads, where the inline table would be), so a block finds its
+// tensor by a binary search of the heads and, above kTableHeads tensors, of its head's group.
+constexpr int kTableHeads = kMaxDesc * (int)(sizeof(Desc) / sizeof(uint32_t));  // 960
+
+static_assert(sizeof(Desc) == 80, "descriptor layout");
+static_assert(sizeof(TDesc) == 88, "table descriptor layout");
+static_assert(sizeof(Args) <= 4096, "kernel arguments must fit in 4 KiB");
+
+// ------------------------------------------------------------------ device math
+
+__device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f_bits(float f) { return __float_as_uint(f); }
+
+// Rust f32::clamp: NaN passes through.
+__device__ __forceinline__ float rclamp(float x, float lo, float hi) {
+    x = x < lo ? lo : x;
+    return x > hi ? hi : x;
+}
+
+// prng.rs:21-26 -- wrapping i32 arithmetic, arithmetic right shifts.
+// The multipliers are the reference's decimal i32 constants; the first one is close to, but not,
+// MurmurHash3's fmix32 constant.
+// The hash input is z0 = idx + seed + kPrngAdd (wrapping); callers form z0 themselves, so a
+// thread adds a per-stream base once and each element only its constant offset.
+// prng_mixed is the state before the last step, z ^ (z >> 16).
+constexpr uint32_t kPrngAdd = (uint32_t)-1640531527;  // wrapping_sub(1_640_531_527)
+
+__device__ __forceinline__ int32_t prng_mixed(uint32_t z0) {
+    constexpr uint32_t kMul1 = (uint32_t)-2048173461;
+    constexpr uint32_t kMul2 = (uint32_t)-1028477387;
+    int32_t z = (int32_t)z0;
+    z = (int32_t)((uint32_t)(z ^ (z >> 16)) * kMul1);
+    return (int32_t)((uint32_t)(z ^ (z >> 13)) * kMul2);
+}
+
+__device__ __forceinline__ int32_t prng(uint32_t z0) {
+    const int32_t z = prng_mixed(z0);
+    return z ^ (z >> 16);
+}
+
+// prng.rs:137-160 on the hardware converter (sr_bf16_hw in lv_exact.h): the noise
+// prng(z0) & 0xFFFF goes in the high half of the converter's random operand. Returns an f32
+// whose HIGH half holds the bf16 bits (the low half is not zero: store it, do not compute with it).
+__device__ __forceinline__ float sr_bf16(float v, uint32_t z0) {
+    return sr_bf16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)));
+}
+
+// prng.rs:162-178
+__device__ __forceinline__ float rne_bf16(float v) {
+    uint32_t b = f_bits(v);
+    uint32_t a = b & 0x7FFFFFFFu;
+    uint32_t r = (a + 0x7FFFu + ((a >> 16) & 1u)) & 0xFFFF0000u;
+    r = r > 0x7F7F0000u ? 0x7F7F0000u : r;
+    uint32_t fin = (b & 0x80000000u) | r;
+    uint32_t nan = (b | 0x00400000u) & 0xFFFF0000u;
+    return bits_f(a > 0x7F800000u ? nan : fin);
+}
+
+// f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
+
+// prng.rs:98-130
+__device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
+    int32_t p = (int32_t)f_bits(v);
+    int32_t a = p & 0x7FFFFFFF;
+    int32_t ex = (a >> 23) & 0xFF;
+    int32_t sub = 113 - ex;
+    sub = sub > 0 ? sub : 0;
+    sub = sub < 11 ? sub : 11;
+    int32_t mask = (int32_t)((1u << (13 + sub)) - 1u);
+    int32_t noise = prng(z0) & mask;
+    int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
+    int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
+    // The reference converts sign | r to fp16 and back (prng.rs:129). That is the identity here,
+    // because sign | r is already an fp16 value. r is one of:
+    // - 0, or 65504;
+    // - the sign bit alone (-0.0), when a NaN's magnitude plus the noise wraps past 2^31;
+    // - a value with its (13 + sub) low bits clear. For ex >= 113 that leaves 10 fraction bits
+    //   below 65504 (an fp16 normal). For 103 <= ex <= 112 it leaves a multiple of 2^-24 below
+    //   2^-13 (fp16 subnormals and the lowest normal binade).
+    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
+}
+
+__device__ __forceinline__ float rne_fp16(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
+
+// prng.rs:180-195; dtype is a compile-time constant at every call site. z0 is the element's
+// hash input for the buffer's seed (offset + seed + kPrngAdd).
+template <int DT>
+__device__ __forceinline__ float quantize(float v, uint32_t z0, bool sr) {
+    if constexpr (DT == LV_DTYPE_BF16) {
+        return sr ? sr_bf16(v, z0) : rne_bf16(v);
+    } else if constexpr (DT == LV_DTYPE_F16) {
+        return sr ? sr_fp16(v, z0) : rne_fp16(v);
+    } else {
+        return v;
+    }
+}
+
+// Wave-uniform fast paths. Each exact helper below has a cheap common case (an input in the range
+// where the helper is the identity, or needs no rescaling); when every active lane of the wave is
+// in it, one compare per element and a scalar branch replace the general sequence. The general
+// sequence still runs, for the whole wave, whenever any lane needs it, so results are unchanged.
+__device__ __forceinline__ bool wave_all(bool c) { return __builtin_amdgcn_ballot_w64(!c) == 0; }
+
+// math.rs:4-11. |g| < 1e38 is false for NaN and +-inf, so one compare also covers is_finite;
+// on that path g is not NaN and med3 is exactly the clamp. |g| <= 1e18 (false for NaN) leaves g
+// unchanged.
+__device__ __forceinline__ float sanitize(float g) {
+    if (__builtin_expect(wave_all(fabsf(g) <= 1.0e18f), 1)) return g;
+    return fabsf(g) < 1.0e38f ? __builtin_amdgcn_fmed3f(g, -1.0e18f, 1.0e18f) : 0.0f;
+}
+
+// math.rs:13-16 (clamp_defect): NaN passes through like Rust's f32::clamp; |d| <= 1e18 is the
+// identity.
+__device__ __forceinline__ float clamp_defect(float d) {
+    if (__builtin_expect(wave_all(fabsf(d) <= 1.0e18f), 1)) return d;
+    return __builtin_isnan(d) ? d : __builtin_amdgcn_fmed3f(d, -1.0e18f, 1.0e18f);
+}
+
+// Correctly rounded sqrt (sqrt_rn in lv_exact.h) with its small-input rescaling skipped when no
+// lane of the wave needs it (x >= 2^-96, +-0, +inf and NaN need none).
+__device__ __forceinline__ float sqrt_cr(float x) {
+    if (__builtin_expect(wave_all(!(x < 0x1p-96f) || x == 0.0f), 1)) return sqrt_rn_normal(x);
+    return sqrt_rn(x);
+}
+
+// math.rs:83-118 -- [13/6] Pade tanh, Horner with fma.
+__device__ __forceinline__ float tanh_pade(float x_in) {
+    if (__builtin_isnan(x_in)) return bits_f(0x7FC00000u);  // Rust f32::NAN
+    float x = rclamp(x_in, -7.9988117f, 7.9988117f);
+    float x2 = x * x;
+    float p = __builtin_fmaf(-2.7607684e-16f, x2, 2.000188e-13f);
+    float q = __builtin_fmaf(1.1982584e-6f, x2, 1.1853471e-4f);
+    p = __builtin_fmaf(p, x2, -8.604672e-11f);
+    q = __builtin_fmaf(q, x2, 2.2684346e-3f);
+    p = __builtin_fmaf(p, x2, 5.122297e-8f);
+    q = __builtin_fmaf(q, x2, 4.8935246e-3f);
+    p = __builtin_fmaf(p, x2, 1.4857224e-5f);
+    p = __builtin_fmaf(p, x2, 6.3726193e-4f);
+    p = __builtin_fmaf(p, x2, 4.8935246e-3f);
+    return (x * p) / q;
+}
+
+// math.rs:162-186
+template <bool TRI>
+__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio) {
+    if constexpr (TRI) {
+        float b = ratio * (fabsf(p_init) + 1.0e-2f);
+        float bb = b * (b + fabsf(step));
+        return (bb * step) / __builtin_fmaf(step, step, bb);
+    } else {
+        float b = ratio * sqrt_cr(__builtin_fmaf(p_init, p_init, 1.0e-4f));
+        return b * tanh_pade(step / b);
+    }
+}
+
+template <bool TRI>
+__device__ __forceinline__ float fp16_safety_bound(float step, float p_init) {
+    float b = __builtin_fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);
+    if constexpr (TRI) {
+        float bb = b * (b + fabsf(step));
+        return (bb * step) / __builtin_fmaf(step, step, bb);
+    } else {
+        return b * tanh_pade(step / b);
+    }
+}
+
+// math.rs:120-125
+__device__ __forceinline__ float cautious_scale(float mask_sum, float total, float clamp_min) {
+    float denom = __builtin_fmaxf(total, 1.0f);
+    return 1.0f / rclamp(mask_sum / denom, clamp_min, 1.0f);
+}
+
+// math.rs:127-160: radial trust-region scale from the squared norms. TRI selects the rational
+// form of the triangle family (T1/T2), otherwise tanh(r)/r.
+template <bool TRI>
+__device__ __forceinline__ float radial_scale(float u_sq, float p_sq, float cs, float lr, float ratio) {
+    float norm_p = __builtin_sqrtf(__builtin_fmaxf(p_sq, 0.0f));
+    float norm_d = __builtin_sqrtf(__builtin_fmaxf(u_sq, 0.0f)) * cs;
+    float radius = ratio * __builtin_fmaxf(norm_p, 1.0f);
+    if constexpr (TRI) {
+        float r = (lr * norm_d) / __builtin_fmaxf(radius, 1.0e-12f);
+        float one_plus_r = 1.0f + r;
+        return one_plus_r / __builtin_fmaf(r, r, one_plus_r);
+    } else {
+        float r = (lr * norm_d) / radius;
+        if (r < 1.0e-4f) return 1.0f;
+        return tanh_pade(r) / __builtin_fmaxf(r, 1.0e-8f);
+    }
+}
+
+// Round-to-nearest-even u64 -> f32 (Rust `as f32`), exact integer algorithm.
+__device__ __forceinline__ float u64_to_f32_rn(uint64_t x) {
+    if ((x >> 24) == 0) return (float)(uint32_t)x;
+    int bits = 64 - __clzll((long long)x);
+    int sh = bits - 24;
+    uint64_t mant = x >> sh;
+    uint64_t rem = x & ((1ull << sh) - 1ull);
+    uint64_t half = 1ull << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1ull))) mant += 1ull;
+    return ldexpf((float)(uint32_t)mant, sh);
+}
+
+// u, m_new, v_new for one element.
+// CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
+template <int MODE>
+__device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g, float m, float v,
+                                           float &m_new, float &v_new) {
+    m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
+    if constexpr (MODE == LV_BUFFER_DUAL) {
+        float clm = __builtin_fmaf(a.b1, m_new, a.omb1 * g);
+        float diff = clamp_defect(g - m_new);
+        v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
+        if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
+        float sigma = __builtin_fmaf(sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
+        return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
+    } else if constexpr (MODE == LV_BUFFER_T2) {
+        float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        float diff = clamp_defect(g - m);
+        v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
+        if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+        float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
+        float env = __builtin_fmaf(a.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
+        return clm / env;
+    } else {
+        float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        float diff = clamp_defect(g - m);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+        float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
+        v_new = 0.0f;
+        return clm / env;
+    }
+}
+
+// ------------------------------------------------------------------ loads / stores
+
+template <int DT>
+__device__ __forceinline__ float load1(const void *base, uint64_t i) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        return static_cast<const float *>(base)[i];
+    } else if constexpr (DT == LV_DTYPE_BF16) {
+        return bits_f((uint32_t) static_cast<const uint16_t *>(base)[i] << 16);
+    } else {
+        return f16_to_f32(static_cast<const uint16_t *>(base)[i]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store1(void *base, uint64_t i, float x) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        static_cast<float *>(base)[i] = x;
+    } else if constexpr (DT == LV_DTYPE_BF16) {
+        static_cast<uint16_t *>(base)[i] = (uint16_t)(f_bits(x) >> 16);
+    } else {
+        static_cast<uint16_t *>(base)[i] = (uint16_t)pack_f16_exact(x, x);  // x is an f16 value
+    }
+}
+
+__device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i) {
+    if (dt == LV_DTYPE_BF16) return load1<LV_DTYPE_BF16>(base, i);
+    if (dt == LV_DTYPE_F32) return load1<LV_DTYPE_F32>(base, i);
+    return load1<LV_DTYPE_F16>(base, i);
+}
+
+// One thread's 4 or 8 elements as raw vectors, kept undecoded while the loads are in flight.
+// Vector-path loads and stores are non-temporal: the step streams every byte exactly once, so
+// nothing is worth keeping in L2 or the MALL, and streaming hints measurably raise HBM
+// throughput for this 4-read/3-write pattern.
+// Layout of a work unit of H 1024-element halves: thread t owns elements [4t, 4t+4) of each
+// half, so every wave-wide load or store instruction covers one contiguous span (1 KiB for
+// f32, 512 B for 16-bit types). 32-bit types use `a` (first half) and `b` (second half);
+// 16-bit types pack both halves into `a` (.xy first half, .zw second half).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Raw8 {
+    u32x4 a, b;
+};
+
+// H (1 or 2) is the number of 1024-element halves in the unit: a thread moves 4 * H elements.
+template <int DT, int H>
+__device__ __forceinline__ Raw8 load_raw(const void *base, uint64_t h0) {
+    Raw8 r;
+    if constexpr (DT == LV_DTYPE_F32) {
+        const float *f = static_cast<const float *>(base);
+        r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0));
+        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + kHalf));
+        else r.b = u32x4{0, 0, 0, 0};
+    } else {
+        const uint16_t *h = static_cast<const uint16_t *>(base);
+        u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
+        u32x2 y = u32x2{0, 0};
+        if constexpr (H == 2) y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + kHalf));
+        r.a = u32x4{x.x, x.y, y.x, y.y};
+        r.b = u32x4{0, 0, 0, 0};
+    }
+    return r;
+}
+
+template <int H>
+__device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t h0) {
+    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32, H>(base, h0);
+    return load_raw<LV_DTYPE_BF16, H>(base, h0);  // 16-bit types share the raw layout
+}
+
+// Stores 4 * H values in the same layout; 16-bit values are already exact in the target
+// type (quantised), so bf16 is a truncation of the high half (worker.rs:55-63) and f16 an exact
+// conversion (pack_f16_exact).
+template <int DT, int H>
+__device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        float *f = static_cast<float *>(base);
+        __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4 *>(f + h0));
+        if constexpr (H == 2)
+            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + kHalf));
+    } else {
+        uint32_t ws[4];
+#pragma unroll
+        for (int k = 0; k < 2 * H; k++) {
+            if constexpr (DT == LV_DTYPE_BF16) {
+                ws[k] = (f_bits(in[2 * k]) >> 16) | (f_bits(in[2 * k + 1]) & 0xFFFF0000u);
+            } else {
+                ws[k] = pack_f16_exact(in[2 * k], in[2 * k + 1]);
+            }
+        }
+        uint16_t *h = static_cast<uint16_t *>(base);
+        __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
+        if constexpr (H == 2) __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + kHalf));
+    }
+}
+
+template <int DT, int H>
+__device__ __forceinline__ void decode_raw(const Raw8 &r, float out[8]) {
+    if constexpr (DT == LV_DTYPE_F32) {
+        out[0] = bits_f(r.a.x); out[1] = bits_f(r.a.y); out[2] = bits_f(r.a.z); out[3] = bits_f(r.a.w);
+        if constexpr (H == 2) {
+            out[4] = bits_f(r.b.x); out[5] = bits_f(r.b.y); out[6] = bits_f(r.b.z); out[7] = bits_f(r.b.w);
+        }
+    } else {
+        uint32_t ws[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int k = 0; k < 2 * H; k++) {
+            if constexpr (DT == LV_DTYPE_BF16) {
+                out[2 * k] = bits_f(ws[k] << 16);
+                out[2 * k + 1] = bits_f(ws[k] & 0xFFFF0000u);
+            } else {
+                out[2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                out[2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    }
+}
+
+template <int H>
+__device__ __forceinline__ void decode_raw_dyn(int dt, const Raw8 &r, float out[8]) {
+    if (dt == LV_DTYPE_BF16) decode_raw<LV_DTYPE_BF16, H>(r, out);
+    else if (dt == LV_DTYPE_F32) decode_raw<LV_DTYPE_F32, H>(r, out);
+    else decode_raw<LV_DTYPE_F16, H>(r, out);
+}
+
+// The loads of one work unit that are in flight while the previous unit computes.
+// p holds the param or, with master weights, the f32 master: one field for both, so that the
+// run-time choice never becomes a select between two register arrays (which the compiler would
+// place in scratch memory).
+struct Inflight {
+    Raw8 p, g, m, v;
+};
+
+// ------------------------------------------------------------------ element update
+
+struct Seeds {
+    int32_t m, p, v;
+};
+
+// Hash inputs of one element offset for the m, p and v streams.
+struct HashIn {
+    uint32_t m, p, v;
+};
+
+__device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
+    return {off + (uint32_t)sd.m + kPrngAdd, off + (uint32_t)sd.p + kPrngAdd, off + (uint32_t)sd.v + kPrngAdd};
+}
+
+// Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
+// Returns the cautious mask bit; u_eff is the (masked) direction whose square feeds the radial
+// norm (dual.rs:176-180).
+template <int MODE, int PT, int ST>
+__device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const HashIn &z,
+                                               float cs, float bs, float p_init, float g_raw, float &m_io,
+                                               float &v_io, float &p_out, float &mp_out, float &u_eff) {
+    constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    const bool sr = flags & kFSR;
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    bool active = (u * g) > 0.0f;
+    float m_mask = active ? 1.0f : 0.0f;
+    m_io = quantize<ST>(m_new, z.m, sr);
+    if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
+    u_eff = (flags & kFCautious) ? u * m_mask : u;
+    float delta = (flags & kFCautious) ? u_eff * cs : u;
+    float step = a.lr * delta;
+    if (flags & kFRadial) step *= bs;
+    else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio);
+    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init);
+    float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
+    float p_upd = p_dec - step;
+    if (flags & kFMaster) {
+        mp_out = p_upd;
+        p_out = quantize<PT>(p_upd, z.p, false);
+    } else {
+        p_out = quantize<PT>(p_upd, z.p, sr);
+    }
+    return active ? 1u : 0u;
+}
+
+// Counting path for one element (dual.rs:279-303, dual.rs:720-746, tdclm.rs:232-248).
+template <int MODE>
+__device__ __forceinline__ uint32_t count_elem(const Args &a, uint32_t flags, float g_raw, float m, float v,
+                                               float &u_eff) {
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, flags & kFClampV, g, m, v, m_new, v_new);
+    bool active = (u * g) > 0.0f;
+    u_eff = (flags & kFCautious) ? u * (active ? 1.0f : 0.0f) : u;
+    return active ? 1u : 0u;
+}
+
+// ------------------------------------------------------------------ scratch finalisation
+
+// Last block of tensor t: dual.rs:255-259 + math.rs:188-239 (fused), dual.rs:330-351 +
+// dual.rs:436-438 (two-pass count).  Thread 0 only. Slots 3/4 end at 1.0 when cautious /
+// radial is off, the value the reference's host layer forces before every step
+// (luminav.py:1748-1751).
+template <int MODE, int PASS>
+__device__ void finalize_scratch(const Args &a, bool radial, const Desc &D, unsigned long long mask_count,
+                                 float u_sq, float p_sq) {
+    constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
+    float *s = D.scratch;
+    const bool cautious = a.flags & kFCautious;
+    float mask_sum = u64_to_f32_rn(mask_count);
+    float total = u64_to_f32_rn(D.n);
+    float s3, s4 = 1.0f;
+    if constexpr (PASS == kFused) {
+        s3 = cautious ? __builtin_fmaf(a.ema, s[3], a.ema_c * cautious_scale(mask_sum, total, a.clamp_min)) : 1.0f;
+        if (radial)
+            s4 = __builtin_fmaf(a.ema, s[4], a.ema_c * radial_scale<kTri>(u_sq, p_sq, s3, a.lr, a.ratio));
+    } else {
+        s3 = cautious ? cautious_scale(mask_sum, total, a.clamp_min) : 1.0f;
+        if (radial) s4 = radial_scale<kTri>(u_sq, p_sq, s3, a.lr, a.ratio);
+    }
+    s[0] = 0.0f;
+    s[1] = 0.0f;
+    s[2] = 0.0f;
+    s[3] = s3;
+    s[4] = s4;
+    s[5] = 0.0f;
+}
+
+// Butterfly sum over the 64 lanes; every lane ends with the same, order-fixed value.
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+__device__ __forceinline__ unsigned long long wave_sum(unsigned long long x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)x, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), off, 64);
+        x += ((unsigned long long)hi << 32) | lo;
+    }
+    return x;
+}
+
+// Block-wide sums in a fixed order (lanes by butterfly, then the 4 waves in order); the result
+// is valid in thread 0, which reads the shared slots after the barrier: a second call by the
+// same block needs a barrier in between.
+struct BlockSums {
+    double su[kThreads / 64];
+    double sp[kThreads / 64];
+    unsigned long long cnt[kThreads / 64];
+};
+
+template <typename C>
+__device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp, C &cnt) {
+    su = wave_sum(su);
+    sp = wave_sum(sp);
+    cnt = wave_sum(cnt);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sh.su[w] = su;
+        sh.sp[w] = sp;
+        sh.cnt[w] = cnt;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        su = sh.su[0];
+        sp = sh.sp[0];
+        cnt = (C)sh.cnt[0];
+#pragma unroll
+        for (int k = 1; k < kThreads / 64; k++) {
+            su += sh.su[k];
+            sp += sh.sp[k];
+            cnt += (C)sh.cnt[k];
+        }
+    }
+}
+
+__device__ __forceinline__ double load_relaxed(const double *p) {
+    uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __longlong_as_double((long long)b);
+}
+
+// ------------------------------------------------------------------ per-unit work
+
+// The descriptor of tensor t of an inline or a table launch.
+template <bool TABLE>
+__device__ __forceinline__ const Desc &desc_of(const Args &a, int t) {
+    if constexpr (TABLE) return a.dtab[t].d;
+    else return a.d[t];
+}
+
+// What a block needs to know about the tensor that owns its current unit.
+struct View {
+    uint32_t t_begin, t_end;  // the tensor's unit range in the launch
+    uint32_t slot_base;       // its first count slot (64-byte index into Args::slots)
+    uint64_t n;
+    bool vec_ok;              // every pointer 16-byte aligned: whole units take the vector path
+    float cs, bs;             // cautious / radial scale read from the scratch (fused, apply)
+    Seeds sd;
+    uint32_t ibase;
+};
+
+template <int MODE, int PASS, bool TABLE>
+__device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, uint32_t flags, uint32_t unit) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    View tv;
+    tv.t_begin = D.unit_begin;
+    if constexpr (TABLE) {
+        tv.t_end = a.dtab[t].unit_end;
+        tv.slot_base = a.dtab[t].slot_base;
+    } else {
+        tv.t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+        tv.slot_base = (uint32_t)t * kSlotWords;
+    }
+    tv.n = D.n;
+    uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
+    if (kDual) al |= (uintptr_t)D.v;
+    if (flags & kFMaster) al |= (uintptr_t)D.mp;
+    tv.vec_ok = (al & 15u) == 0;
+    tv.ibase = D.ibase;
+    uint32_t raw = a.seed_base + D.pidx * 10007u;
+    tv.sd.m = (int32_t)(raw & 0x7FFFFFFFu);
+    tv.sd.p = (int32_t)(((uint32_t)tv.sd.m + 0x55555555u) & 0x7FFFFFFFu);
+    tv.sd.v = (int32_t)(((uint32_t)tv.sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
+    tv.cs = 1.0f;
+    tv.bs = 1.0f;
+    if constexpr (PASS == kFused || PASS == kApply) {
+        tv.cs = D.scratch[3];
+        tv.bs = D.scratch[4];
+    }
+    if constexpr (PASS == kSingle) {
+        // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
+        // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
+        if (unit == tv.t_begin && threadIdx.x == 0) {
+            float *sc = D.scratch;
+            sc[0] = 0.0f; sc[1] = 0.0f; sc[2] = 0.0f; sc[3] = 1.0f; sc[4] = 1.0f; sc[5] = 0.0f;
+        }
+    }
+    return tv;
+}
+
+// Vector loads of H 1024-element halves for one thread: elements [e, e + 4) and, with H = 2,
+// [e + kHalf, e + kHalf + 4).
+template <int MODE, int PT, int ST, int PASS, int H>
+__device__ __forceinline__ Inflight issue_at(const Desc &D, uint32_t flags, bool radial, uint64_t e) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    const int gdt = (int)((flags >> 8) & 3u);
+    Inflight f;
+    f.g = load_raw_dyn<H>(gdt, D.g, e);
+    f.m = load_raw<ST, H>(D.m, e);
+    if constexpr (kDual) f.v = load_raw<ST, H>(D.v, e);
+    if (PASS != kCount || radial) {  // the count pass reads p only for the radial norm
+        if (flags & kFMaster) f.p = load_raw<LV_DTYPE_F32, H>(D.mp, e);
+        else f.p = load_raw<PT, H>(D.p, e);
+    }
+    return f;
+}
+
+// Update (or count) the 4 * H elements loaded by issue_at(e0) and store them. BALLOT: every lane
+// of the wave is here, and cnt accumulates the wave's count (the same in every lane) from ballots;
+// otherwise cnt accumulates the lane's own count.
+template <int MODE, int PT, int ST, int PASS, int H, bool BALLOT>
+__device__ __forceinline__ void process_at(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
+                                           const Inflight &cur, uint64_t e0, uint32_t &cnt, double &su, double &sp) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    const int gdt = (int)((flags >> 8) & 3u);
+    const bool master = flags & kFMaster;
+    float g[8], m[8], v[8];
+    decode_raw_dyn<H>(gdt, cur.g, g);
+    decode_raw<ST, H>(cur.m, m);
+    if constexpr (kDual) decode_raw<ST, H>(cur.v, v);
+    if constexpr (PASS == kCount) {
+        float pin[8];
+        if (radial) {
+            if (master) decode_raw<LV_DTYPE_F32, H>(cur.p, pin);
+            else decode_raw<PT, H>(cur.p, pin);
+        }
+#pragma unroll
+        for (int j = 0; j < 4 * H; j++) {
+            float ue;
+            const uint32_t act = count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
+            if constexpr (BALLOT) cnt += (uint32_t)__popcll(__ballot(act));
+            else cnt += act;
+            if (radial) {
+                su += (double)(ue * ue);
+                sp += (double)(pin[j] * pin[j]);
+            }
+        }
+    } else {
+        float pin[8], pout[8], mpout[8];
+        if (master) decode_raw<LV_DTYPE_F32, H>(cur.p, pin);
+        else decode_raw<PT, H>(cur.p, pin);
+        // the thread's hash inputs at its first element (offsets wrap at 2^32 as (int32)idx does)
+        const HashIn zb = hash_in(tv.sd, (uint32_t)e0 + tv.ibase);
+#pragma unroll
+        for (int j = 0; j < 4 * H; j++) {
+            float vj = kDual ? v[j] : 0.0f;
+            float ue;
+            const uint32_t jj = j < 4 ? (uint32_t)j : kHalf + (uint32_t)j - 4u;  // a constant once unrolled
+            const HashIn zj = {zb.m + jj, zb.p + jj, zb.v + jj};
+            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+                                                    mpout[j], ue);
+            if constexpr (kDual) v[j] = vj;
+            if constexpr (kCounting) {
+                if constexpr (BALLOT) cnt += (uint32_t)__popcll(__ballot(act));
+                else cnt += act;
+                if (radial) {
+                    su += (double)(ue * ue);
+                    sp += (double)(pin[j] * pin[j]);
+                }
+            }
+        }
+        store_raw<PT, H>(D.p, e0, pout);
+        if (master) store_raw<LV_DTYPE_F32, H>(D.mp, e0, mpout);
+        store_raw<ST, H>(D.m, e0, m);
+        if constexpr (kDual) store_raw<ST, H>(D.v, e0, v);
+    }
+}
+
+// Per-element path for the elements [e_begin, e_end) of one thread (partially inactive units,
+// unaligned tensors, and the last few elements of a tensor). nskip > 0: the tensor's inactive
+// ranges, `first` the first range that ends after the unit's first element. Inactive elements are
+// computed with a zero gradient (they count in the statistics) and not stored. cnt accumulates the
+// lane's own count.
+template <int MODE, int PT, int ST, int PASS>
+__device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
+                                             uint64_t e_begin, uint64_t e_end, uint32_t &cnt, double &su, double &sp,
+                                             uint32_t nskip = 0, uint32_t first = 0) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    const int gdt = (int)((flags >> 8) & 3u);
+    const bool master = flags & kFMaster;
+    uint32_t r = first;
+    for (uint64_t i = e_begin; i < e_end; i++) {
+        bool inactive = false;
+        if (nskip) {
+            while (r < nskip && D.skip[2 * r + 1] <= i) r++;
+            inactive = r < nskip && D.skip[2 * r] <= i;
+        }
+        float g = inactive ? 0.0f : load1_dyn(gdt, D.g, i);
+        float m = load1<ST>(D.m, i);
+        float v = kDual ? load1<ST>(D.v, i) : 0.0f;
+        if constexpr (PASS == kCount) {
+            float ue;
+            cnt += count_elem<MODE>(a, flags, g, m, v, ue);
+            if (radial) {
+                float pin = master ? D.mp[i] : load1<PT>(D.p, i);
+                su += (double)(ue * ue);
+                sp += (double)(pin * pin);
+            }
+        } else {
+            float pin = master ? D.mp[i] : load1<PT>(D.p, i);
+            float pout, mpout, ue;
+            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs,
+                                                    pin, g, m, v, pout, mpout, ue);
+            if (!inactive) {
+                store1<PT>(D.p, i, pout);
+                if (master) D.mp[i] = mpout;
+                store1<ST>(D.m, i, m);
+                if constexpr (kDual) store1<ST>(D.v, i, v);
+            }
+            if constexpr (kCounting) {
+                cnt += act;
+                if (radial) {
+                    su += (double)(ue * ue);
+                    sp += (double)(pin * pin);
+                }
+            }
+        }
+    }
+}
+
+// How the tensor's inactive ranges cover the elements [e0, e1): 0 not at all, 1 partly, 2 fully.
+// `first` receives the first range that ends after e0. Block-uniform.
+__device__ __forceinline__ int inactive_cover(const Desc &D, uint64_t e0, uint64_t e1, uint32_t &first) {
+    uint32_t lo = 0, hi = D.nskip;
+    while (lo < hi) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (D.skip[2 * mid + 1] <= e0) lo = mid + 1;
+        else hi = mid;
+    }
+    first = lo;
+    if (lo == D.nskip) return 0;
+    const uint64_t b = D.skip[2 * lo], e = D.skip[2 * lo + 1];
+    if (b >= e1) return 0;
+    return (b <= e0 && e >= e1) ? 2 : 1;
+}
+
+// Index of the tensor that owns `unit`: binary search of the unit ranges. Table launches search
+// the heads in the kernel arguments, then (groups of more than one tensor) the head's group in
+// the device table. Every tensor of a launch has at least one unit, so the ranges are strictly
+// increasing.
+template <bool TABLE>
+__device__ __forceinline__ int find_tensor(const Args &a, uint32_t unit) {
+    if constexpr (!TABLE) {
+        int lo = 0, hi = a.ndesc - 1;
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (a.d[mid].unit_begin <= unit) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    } else {
+        int lo = 0, hi = (int)a.nheads - 1;
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (a.ubegin[mid] <= unit) lo = mid;
+            else hi = mid - 1;
+        }
+        if (a.group == 1) return lo;
+        int tlo = lo * (int)a.group;
+        int thi = tlo + (int)a.group - 1;
+        if (thi > a.ndesc - 1) thi = a.ndesc - 1;
+        while (tlo < thi) {
+            int mid = (tlo + thi + 1) >> 1;
+            if (a.dtab[mid].d.unit_begin <= unit) tlo = mid;
+            else thi = mid - 1;
+        }
+        return tlo;
+    }
+}
+
+// ------------------------------------------------------------------ the kernels
+
+// Counting unit launches: thread 0 of every block reports its exact mask count and the block's
+// completion in ONE 64-bit atomic (count << kTicketBits | 1) on one of the tensor's S count slots
+// (slot = unit index in the tensor mod S, 64 B apart, so the atomics spread over L2 channels;
+// S = kSlots inline, table_count_slots(units) in table launches). The block whose report
+// completes a slot (its ticket reaches the slot's block count) holds that slot's whole count in
+// the value its own atomic returned, re-zeroes the slot and reports count << kFoldBits | 1 on the
+// tensor's fold slot (the one after its count slots); the block that completes the fold slot
+// holds the tensor's exact count and finalises the scratch. Every decision reads only the value
+// returned by an atomic on that same word, so no fence is needed (a device-scope release fence
+// per block measured 7x slower); integer sums are exact in any order, so the result is
+// deterministic. Wholly inactive units report a zero count.
+template <int MODE, int PASS, bool TABLE>
+__device__ __forceinline__ void report_count(const Args &a, const Desc &D, const View &tv, uint32_t unit,
+                                             uint32_t count) {
+    const uint32_t n_units = tv.t_end - tv.t_begin;
+    const uint32_t k = unit - tv.t_begin;
+    // slot s of S takes units k = s (mod S): n_units / S blocks, plus one for s < n_units % S
+    const uint32_t S = TABLE ? table_count_slots(n_units) : kSlots;  // a power of two
+    const uint32_t s = k & (S - 1u);
+    const uint32_t nslots = n_units < S ? n_units : S;
+    unsigned long long *words = a.slots + (size_t)tv.slot_base * kSlotStride;
+    unsigned long long *slot = words + (size_t)s * kSlotStride;
+    constexpr unsigned long long kTicketMask = (1ull << kTicketBits) - 1ull;
+    const unsigned long long old = __hip_atomic_fetch_add(slot, ((unsigned long long)count << kTicketBits) | 1ull,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t expect = (n_units >> __builtin_ctz(S)) + (s < (n_units & (S - 1u)) ? 1u : 0u);
+    if ((uint32_t)(old & kTicketMask) + 1u != expect) return;
+    const unsigned long long slot_count = (old >> kTicketBits) + count;
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long *fold = words + (size_t)nslots * kSlotStride;
+    const unsigned long long prev = __hip_atomic_fetch_add(fold, (slot_count << kFoldBits) | 1ull, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)(prev & ((1ull << kFoldBits) - 1ull)) + 1u != nslots) return;
+    __hip_atomic_store(fold, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finalize_scratch<MODE, PASS>(a, false, D, (prev >> kFoldBits) + slot_count, 0.0f, 0.0f);
+}
+
+// Unit launch: each block updates exactly one work unit (1024 or 2048 elements, unit_halves) and
+// exits.
+// The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
+// arithmetic of others without a software pipeline; on MI355X this launch shape streams HBM
+// faster than any persistent grid-stride loop over the same buffers (measured: 23.4 vs 26.5 ms
+// for the 6.7e9-element T2 step; 2048-element units: 23.7 ms). Counting passes report each
+// block's exact mask count (report_count), and the last block of each tensor finalises its
+// scratch, so a step is one launch. Radial counting passes instead store each unit's record
+// (mask count and f64 squared-norm sums) for fold_kernel.
+// A tensor's partial last unit keeps the vector layout: each thread's 4-element groups that lie
+// wholly inside the tensor take the vector path, and only the one group that straddles the end
+// goes element by element.
+// FL is either kFDynamic (flags read at run time) or the exact flag word of the launch, in
+// which case every option test folds at compile time and the per-element code is straight-line.
+// TABLE: the tensor table is in device memory (a.dtab) and the heads in a.ubegin.
+template <int MODE, int PT, int ST, int PASS, uint32_t FL, bool TABLE>
+__global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
+    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    __shared__ BlockSums sh;
+
+    const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
+    const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
+    // Workgroups are dispatched to the XCDs round-robin (block b runs on XCD b mod X). Map them so
+    // that each XCD streams one contiguous range of units (measured ~1% faster than b -> b).
+    // Every block is short-lived, so its prologue is on the critical path: b / X comes from the
+    // host's reciprocal (exact for b < 2^23 and X <= 64) instead of an integer division, which
+    // measured 1.3% of the cfg5 step.
+    const uint32_t b = blockIdx.x;
+    const uint32_t i = (uint32_t)(((uint64_t)b * a.xcd_recip) >> 40);
+    const uint32_t x = b - i * a.xcds;
+    const uint32_t unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
+    const int t = find_tensor<TABLE>(a, unit);
+    const Desc &D = desc_of<TABLE>(a, t);
+    const View tv = open_view<MODE, PASS, TABLE>(a, D, t, flags, unit);
+    uint32_t cnt = 0;
+    double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
+    constexpr int H = unit_halves(MODE, PT, ST);
+    constexpr uint64_t kUnit = (uint64_t)kHalf * H;
+    const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit;
+    int cover = 0;
+    uint32_t first = 0;
+    if (D.nskip) {
+        cover = inactive_cover(D, ubase, ubase + kUnit < tv.n ? ubase + kUnit : tv.n, first);
+        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
+        // its elements still enter the radial norms.
+        if (!kCounting && cover == 2) return;
+    }
+    // Vector path over a whole unit: cnt ends as the wave's count (the same in every lane, from
+    // ballots); every other path: cnt is the lane's count.
+    const bool fast = cover == 0 && tv.vec_ok;
+    const bool vec = fast && ubase + kUnit <= tv.n;
+    const uint64_t e0 = ubase + (uint64_t)threadIdx.x * 4u;
+    if (vec) {
+        const Inflight f = issue_at<MODE, PT, ST, PASS, H>(D, flags, radial, e0);
+        // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
+        // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
+        __builtin_amdgcn_s_setprio(1);
+        process_at<MODE, PT, ST, PASS, H, true>(a, D, tv, flags, radial, f, e0, cnt, su, sp);
+    } else if (fast) {
+        // the partial last unit of an aligned tensor
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const uint64_t e = e0 + (uint64_t)h * kHalf;
+            if (e + 4u <= tv.n) {
+                const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
+                process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
+            } else if (e < tv.n) {
+                scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
+            }
+        }
+    } else if (cover != 2 || radial) {
+        const uint64_t eb = ubase + (uint64_t)threadIdx.x * (4u * H);
+        const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
+        scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
+    }
+    if constexpr (kCounting) {
+        if (radial) {
+            uint32_t lane_cnt = vec ? ((threadIdx.x & 63) == 0 ? cnt : 0u) : cnt;
+            block_sums(sh, su, sp, lane_cnt);
+            cnt = lane_cnt;
+            if (threadIdx.x == 0) {
+                const uint32_t k = unit - a.unit_base;  // < piece_units
+                a.unit_sq[2 * (size_t)k] = su;
+                a.unit_sq[2 * (size_t)k + 1] = sp;
+                a.unit_cnt[k] = cnt;
+            }
+        } else {
+            if (!vec) cnt = wave_sum(cnt);  // block-uniform branch
+            if ((threadIdx.x & 63) == 0) sh.cnt[threadIdx.x >> 6] = cnt;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                uint32_t tot = 0;
+#pragma unroll
+                for (int k = 0; k < kThreads / 64; k++) tot += (uint32_t)sh.cnt[k];
+                report_count<MODE, PASS, TABLE>(a, D, tv, unit, tot);
+            }
+        }
+    }
+}
+
+// Units of tensor t inside the piece [ub, ue) of the launch's unit space: [lo, hi).
+__host__ __device__ inline void piece_span(const Args &a, int t, uint32_t ub, uint32_t ue, uint32_t &lo, uint32_t &hi) {
+    const uint32_t tb = a.d[t].unit_begin;
+    const uint32_t te = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+    lo = tb > ub ? tb : ub;
+    hi = te < ue ? te : ue;
+    if (hi < lo) hi = lo;
+}
+
+// Radial fold, one launch after each piece of a radial counting launch. The piece's units are
+// cut, per tensor, into chunks of kFoldChunk; block j sums the unit records of chunk j into
+// chunk record j (thread k adds records k, k + 256, ... in order, kFoldBatch loads in flight,
+// then the fixed block order), and the block that completes a tensor's chunks (per-tensor
+// ticket, release/acquire fences: <= 1072 blocks per piece, after a kernel boundary that already
+// wrote the L2 back) sums the tensor's chunk records in order, adds them after the running sum
+// of the earlier pieces, and either stores the new running sum or, in the piece that holds the
+// tensor's last unit, finalises the scratch. Every sum runs in an order fixed by the unit and
+// piece sizes. Every record is zeroed once it has been read, so the call leaves the whole
+// workspace zero (a later call may use the same bytes as count words).
+template <int MODE, int PASS>
+__global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
+    __shared__ BlockSums sh;
+    __shared__ uint32_t last;
+    const uint32_t ub = a.unit_base, ue = a.unit_base + a.piece_units;
+    uint32_t j = blockIdx.x, cbase = 0, lo = 0, hi = 0, nc = 0;
+    int t = 0;
+    for (; t < a.ndesc; t++) {  // block-uniform; the grid is exactly the piece's chunk count
+        piece_span(a, t, ub, ue, lo, hi);
+        nc = (hi - lo + kFoldChunk - 1) / kFoldChunk;
+        if (j < nc) break;
+        j -= nc;
+        cbase += nc;
+    }
+    if (t == a.ndesc) return;
+    const uint32_t u0 = lo + j * kFoldChunk;
+    const uint32_t u1 = (hi - u0 > kFoldChunk) ? u0 + kFoldChunk : hi;
+    double su = 0.0, sp = 0.0;
+    uint32_t cnt = 0;
+    const uint32_t k0 = u0 - ub, k1 = u1 - ub;  // piece-relative record indices, <= kRadialPiece
+    double2 *sq = reinterpret_cast<double2 *>(a.unit_sq);
+    for (uint32_t kb = k0; kb < k1; kb += kFoldBatch * kThreads) {  // block-uniform
+        double2 x[kFoldBatch];
+        uint32_t c[kFoldBatch];
+#pragma unroll
+        for (int r = 0; r < kFoldBatch; r++) {
+            const uint32_t k = kb + r * kThreads + threadIdx.x;
+            const uint32_t kc = k < k1 ? k : k0;  // always in range, so every load can issue at once
+            x[r] = sq[kc];
+            c[r] = a.unit_cnt[kc];
+        }
+#pragma unroll
+        for (int r = 0; r < kFoldBatch; r++) {
+            const uint32_t k = kb + r * kThreads + threadIdx.x;
+            if (k < k1) {
+                su += x[r].x;
+                sp += x[r].y;
+                cnt += c[r];
+                sq[k] = double2{0.0, 0.0};
+                a.unit_cnt[k] = 0u;
+            }
+        }
+    }
+    block_sums(sh, su, sp, cnt);
+    if (threadIdx.x == 0) {
+        RadialSum *r = a.chunks + cbase + j;
+        r->su = su;
+        r->sp = sp;
+        r->cnt = cnt;
+        __threadfence();
+        const unsigned long long prev = atomicAdd(&a.tickets[t], 1ull);
+        last = (prev + 1ull == (unsigned long long)nc) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;  // block-uniform
+    __threadfence();
+    su = 0.0;
+    sp = 0.0;
+    unsigned long long total = 0;
+    for (uint32_t k = threadIdx.x; k < nc; k += kThreads) {
+        RadialSum *r = a.chunks + cbase + k;
+        su += load_relaxed(&r->su);
+        sp += load_relaxed(&r->sp);
+        total += __hip_atomic_load(&r->cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        r->su = 0.0;
+        r->sp = 0.0;
+        r->cnt = 0ull;
+    }
+    block_sums(sh, su, sp, total);
+    if (threadIdx.x == 0) {
+        RadialSum &run = a.run[t];
+        if (lo != a.d[t].unit_begin) {  // earlier pieces hold the tensor's first units
+            su = run.su + su;
+            sp = run.sp + sp;
+            total += run.cnt;
+        }
+        const uint32_t te = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
+        if (hi == te) {
+            finalize_scratch<MODE, PASS>(a, true, a.d[t], total, (float)su, (float)sp);
+            run.su = 0.0;
+            run.sp = 0.0;
+            run.cnt = 0ull;
+        } else {
+            run.su = su;
+            run.sp = sp;
+            run.cnt = total;
+        }
+        __hip_atomic_store(&a.tickets[t], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ------------------------------------------------------------------ kernel pickers
+
+using KernelFn = void (*)(Args);
+
+// Flag word of the specialised ("static") instantiation: the reference defaults (cautious in
+// the counting passes, stochastic rounding, weight decay, coordinate bound, no master, grad
+// dtype = param dtype, v clamp for fp16 params).
+constexpr uint32_t static_flags(int PT, int PASS) {
+    return (PASS != kSingle ? (uint32_t)kFCautious : 0u) | (uint32_t)kFSR | (uint32_t)kFWeightDecay |
+           (uint32_t)kFCoordinate | (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8);
+}
+
+// The same defaults with bound_type="radial" (the radial passes never run SINGLE).
+constexpr uint32_t radial_flags(int PT) {
+    return ((uint32_t)kFCautious | (uint32_t)kFSR | (uint32_t)kFWeightDecay | (uint32_t)kFRadial |
+            (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8));
+}
+
+// Table launches (many small tensors, launch-bound) use the run-time-flag kernel only.
+template <int MODE, int PT, int ST, int PASS>
+KernelFn pick_flags(uint32_t flags, bool table) {
+    constexpr uint32_t kStatic = static_flags(PT, PASS);
+    constexpr uint32_t kRadial = radial_flags(PT);
+    if (table) return unit_kernel<MODE, PT, ST, PASS, kFDynamic, true>;
+    if (flags == kStatic) return unit_kernel<MODE, PT, ST, PASS, kStatic, false>;
+    if (flags == kRadial) return unit_kernel<MODE, PT, ST, PASS, kRadial, false>;
+    if constexpr (PASS == kFused) {
+        // The steady step of common departures from the defaults: master weights, no stochastic
+        // rounding, no weight decay. Where the step is VALU-bound the run-time-flag kernel costs
+        // more: T2 with master weights and bf16 m/v on the cfg5 shape, 25.3 -> 23.2 ms.
+        constexpr uint32_t kMaster = kStatic | kFMaster;
+        constexpr uint32_t kNoSR = kStatic & ~(uint32_t)kFSR;
+        constexpr uint32_t kNoWD = kStatic & ~(uint32_t)kFWeightDecay;
+        if (flags == kMaster) return unit_kernel<MODE, PT, ST, PASS, kMaster, false>;
+        if (flags == kNoSR) return unit_kernel<MODE, PT, ST, PASS, kNoSR, false>;
+        if (flags == kNoWD) return unit_kernel<MODE, PT, ST, PASS, kNoWD, false>;
+    }
+    return unit_kernel<MODE, PT, ST, PASS, kFDynamic, false>;
+}
+
+template <int MODE, int PT, int ST>
+KernelFn pick_pass(int pass, uint32_t flags, bool table) {
+    switch (pass) {
+    case kSingle: return pick_flags<MODE, PT, ST, kSingle>(flags, table);
+    case kFused: return pick_flags<MODE, PT, ST, kFused>(flags, table);
+    case kCount: return pick_flags<MODE, PT, ST, kCount>(flags, table);
+    default: return pick_flags<MODE, PT, ST, kApply>(flags, table);
+    }
+}
+
+template <int MODE, int PT>
+KernelFn pick_state(int st, int pass, uint32_t flags, bool table) {
+    return st == LV_DTYPE_F32 ? pick_pass<MODE, PT, LV_DTYPE_F32>(pass, flags, table)
+                              : pick_pass<MODE, PT, LV_DTYPE_BF16>(pass, flags, table);
+}
+
+template <int MODE>
+KernelFn pick_param(int pt, int st, int pass, uint32_t flags, bool table) {
+    switch (pt) {
+    case LV_DTYPE_F32: return pick_state<MODE, LV_DTYPE_F32>(st, pass, flags, table);
+    case LV_DTYPE_BF16: return pick_state<MODE, LV_DTYPE_BF16>(st, pass, flags, table);
+    default: return pick_state<MODE, LV_DTYPE_F16>(st, pass, flags, table);
+    }
+}
+
+template <int MODE>
+KernelFn pick_fold_pass(int pass) {
+    return pass == kFused ? fold_kernel<MODE, kFused> : fold_kernel<MODE, kCount>;
+}
+
+// One per buffer mode, each defined in its own kernel unit (lv_kernels.hip built with LV_MODE).
+KernelFn pick_kernel_tdclm(int pt, int st, int pass, uint32_t flags, bool table);
+KernelFn pick_kernel_clm(int pt, int st, int pass, uint32_t flags, bool table);
+KernelFn pick_kernel_t1(int pt, int st, int pass, uint32_t flags, bool table);
+KernelFn pick_kernel_t2(int pt, int st, int pass, uint32_t flags, bool table);
+KernelFn pick_fold_tdclm(int pass);
+KernelFn pick_fold_clm(int pass);
+KernelFn pick_fold_t1(int pass);
+KernelFn pick_fold_t2(int pass);
+
+}  // namespace lv

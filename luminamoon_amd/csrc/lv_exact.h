@@ -19,6 +19,19 @@
 //
 // xor_fold16(z) = (z ^ (z >> 16)) & 0xFFFF, the low half of the reference PRNG's last mixing
 // step (prng.rs:25) that bf16 stochastic rounding uses as noise, in one SDWA instruction.
+// xor_fold16_hi(z) is the same 16 bits placed in the high half (low half zero).
+//
+// sr_bf16_hw: bf16 stochastic rounding (prng.rs:137-160) on gfx950's v_cvt_sr_bf16_f32. The
+// converter adds the high 16 bits of its random operand to the 16 bits it truncates (its top
+// random bit lines up with the first truncated bit), so the reference's 16-bit noise goes in the
+// high half. It then equals the reference's integer recipe on every input -- zeros, denormals and
+// NaNs included (a NaN becomes its quietened upper half, as in the reference) -- except that it
+// overflows to +-inf where the reference saturates to the largest finite bf16 (0x7F7F). A
+// magnitude above that largest value (inf included, NaN excluded) always rounds to 0x7F7F in the
+// reference, so such inputs are replaced by +-0x7F7F0000 first, which converts to itself for any
+// noise; the replacement only runs when a lane of the wave needs it (one compare per element).
+// The result is returned as an f32 whose high half holds the bf16 bits; its low half is NOT
+// zero, so it is only good for storing the high half.
 //
 // The fp16 conversions need fp16 denormals enabled, the HIP default for gfx950 code objects.
 #pragma once
@@ -41,16 +54,22 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);  // v_cvt_f32_f16: exact
 }
 
+// The neighbour test alone: correctly rounded for x >= 2^-96, +-0, +inf and NaN (no rescaling).
+__device__ __forceinline__ float sqrt_rn_normal(float x) {
+    float s = __builtin_amdgcn_sqrtf(x);  // v_sqrt_f32, within 1 ulp
+    const float sd = __uint_as_float(__float_as_uint(s) - 1u);
+    const float su = __uint_as_float(__float_as_uint(s) + 1u);
+    const float rd = __builtin_fmaf(-sd, s, x);
+    const float ru = __builtin_fmaf(-su, s, x);
+    s = rd <= 0.0f ? sd : s;
+    s = ru > 0.0f ? su : s;
+    return s;
+}
+
 __device__ __forceinline__ float sqrt_rn(float x) {
     const bool small = x < 0x1p-96f;
     const float xs = small ? x * 0x1p32f : x;
-    float s = __builtin_amdgcn_sqrtf(xs);  // v_sqrt_f32, within 1 ulp
-    const float sd = __uint_as_float(__float_as_uint(s) - 1u);
-    const float su = __uint_as_float(__float_as_uint(s) + 1u);
-    const float rd = __builtin_fmaf(-sd, s, xs);
-    const float ru = __builtin_fmaf(-su, s, xs);
-    s = rd <= 0.0f ? sd : s;
-    s = ru > 0.0f ? su : s;
+    const float s = sqrt_rn_normal(xs);
     return small ? s * 0x1p-16f : s;
 }
 
@@ -60,6 +79,35 @@ __device__ __forceinline__ uint32_t xor_fold16(uint32_t z) {
         : "=v"(r)
         : "v"(z));
     return r;
+}
+
+__device__ __forceinline__ uint32_t xor_fold16_hi(uint32_t z) {
+    uint32_t r;
+    asm("v_xor_b32_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
+        : "=v"(r)
+        : "v"(z));
+    return r;
+}
+
+// Two f32 values that are already f16 values (every result of the reference's fp16 quantisation:
+// finite f16 values, +-65504, signed zeros, subnormals, or the canonical quiet NaN +-0x7FC00000)
+// packed as f16 bits, low half first, with one v_cvt_pkrtz_f16_f32: for such values rounding
+// toward zero is exact, and the canonical NaN becomes the reference's +-0x7E00.
+__device__ __forceinline__ uint32_t pack_f16_exact(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+// Largest finite bf16 as an f32.
+constexpr uint32_t kBf16MaxBits = 0x7F7F0000u;
+
+__device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
+    const bool big = __builtin_fabsf(v) > __uint_as_float(kBf16MaxBits);  // false for NaN
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(big) != 0, 0))
+        v = big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    v2s d = __builtin_bit_cast(v2s, v);  // the low half keeps v's bits (never read)
+    d = __builtin_amdgcn_cvt_sr_bf16_f32(d, v, noise_hi, true);
+    return __builtin_bit_cast(float, d);
 }
 
 }  // namespace lv

@@ -70,7 +70,12 @@ class LvTensor(ctypes.Structure):
     ]
 
 
-EXPORTED_SYMBOLS = ("lv_version", "lv_workspace_bytes", "lv_step_multi", "lv_step_f32", "lv_last_error")
+EXPORTED_SYMBOLS = (
+    "lv_version", "lv_workspace_bytes", "lv_workspace_bytes_for", "lv_step_multi", "lv_step_f32", "lv_last_error",
+    # the reference's standalone C API (luminav_triton_standalone.h:37-111)
+    "luminav_triton_engine_create", "luminav_triton_engine_destroy", "luminav_triton_get_platform",
+    "luminav_triton_get_arch", "luminav_triton_step_f32",
+)
 
 _lib: Optional[ctypes.CDLL] = None
 _lib_lock = threading.Lock()
@@ -96,6 +101,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         L.lv_version.argtypes = []
         L.lv_workspace_bytes.restype = ctypes.c_size_t
         L.lv_workspace_bytes.argtypes = [ctypes.c_int]
+        L.lv_workspace_bytes_for.restype = ctypes.c_size_t
+        L.lv_workspace_bytes_for.argtypes = [ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int]
         L.lv_step_multi.restype = ctypes.c_int
         L.lv_step_multi.argtypes = [
             ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
@@ -107,6 +114,17 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                   ctypes.c_int, f, ctypes.c_uint64, ctypes.c_uint32, P]
         L.lv_last_error.restype = ctypes.c_char_p
         L.lv_last_error.argtypes = []
+        L.luminav_triton_engine_create.restype = P
+        L.luminav_triton_engine_create.argtypes = []
+        L.luminav_triton_engine_destroy.restype = None
+        L.luminav_triton_engine_destroy.argtypes = [P]
+        L.luminav_triton_get_platform.restype = ctypes.c_char_p
+        L.luminav_triton_get_platform.argtypes = [P]
+        L.luminav_triton_get_arch.restype = ctypes.c_char_p
+        L.luminav_triton_get_arch.argtypes = [P]
+        L.luminav_triton_step_f32.restype = ctypes.c_int
+        L.luminav_triton_step_f32.argtypes = [P, P, P, P, P, P, P, ctypes.c_size_t, f, f, f, f, f, f, f, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_int, f, ctypes.c_uint64, ctypes.c_uint32]
         _lib = L
         return L
 
@@ -124,31 +142,25 @@ def make_config(group: Dict[str, Any]) -> LvConfig:
 
 
 class _Workspace:
-    """Per-device workspace (count words, radial records, table-launch descriptors), allocated
-    zero-filled; the kernels leave its count words zeroed after each call."""
+    """Per-device workspace (cautious count slots, radial records), allocated zero-filled and
+    grown to the largest call seen; every call leaves all of it zero again, so calls of any
+    layout share it."""
 
     def __init__(self) -> None:
         self._bufs: Dict[Any, torch.Tensor] = {}
-        self._ok: Dict[Any, int] = {}  # largest tensor count the device's buffer is known to fit
 
-    def get(self, device: torch.device, n_tensors: int) -> torch.Tensor:
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
         buf = self._bufs.get(device)
-        if buf is not None and self._ok[device] >= n_tensors:
-            return buf
-        need = int(load_library().lv_workspace_bytes(max(1, n_tensors)))
-        if buf is None or buf.numel() < need:
-            cap = max(need, 4096)
-            buf = torch.zeros(cap, dtype=torch.uint8, device=device)
+        if buf is None or buf.numel() < nbytes:
+            # torch's caching allocator returns 512-byte aligned blocks (the library needs 256)
+            buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
             self._bufs[device] = buf
-            self._ok[device] = 0
-        self._ok[device] = max(self._ok[device], n_tensors)
         return buf
 
     def discard(self, device: torch.device) -> None:
-        """Drops the device's buffer: after a failed launch its count words may hold a partial
+        """Drops the device's buffer: after a failed launch its count slots may hold a partial
         launch's counts, so the next call starts from a fresh zero-filled one."""
         self._bufs.pop(device, None)
-        self._ok.pop(device, None)
 
 
 # lv_tensor packed little-endian: 6 pointers, numel, step, param_index, 4 x int32, index_base,
@@ -165,7 +177,7 @@ class PreparedStep:
     swap a tensor's grad (same shape/dtype/device, contiguous; checked) and set step counters;
     everything else stays as validated."""
 
-    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index", "_steps")
+    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index", "_steps", "ws_need")
 
     def __init__(self, buf: bytearray, n: int, device: torch.device, numels: List[int], gdtypes: List[Any]):
         self.buf = buf
@@ -177,6 +189,7 @@ class PreparedStep:
         self.numels = numels
         self.gdtypes = gdtypes
         self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.ws_need: Dict[bool, int] = {}  # workspace bytes, by whether the radial bound is on
 
     def set_grad(self, i: int, g: torch.Tensor) -> bool:
         """Point descriptor i at grad g; False (nothing changed) if g does not fit it."""
@@ -303,7 +316,11 @@ class HipStepper:
             return
         lib = load_library()
         cfg = make_config(group)
-        ws = self.workspace.get(prep.device, prep.n)
+        radial = bool(cfg.bound) and cfg.bound_type == 1 and cfg.bound_ratio > 0.0
+        need = prep.ws_need.get(radial)
+        if need is None:
+            need = prep.ws_need[radial] = int(lib.lv_workspace_bytes_for(ctypes.byref(cfg), prep.items, prep.n))
+        ws = self.workspace.get(prep.device, need)
         if _get_device() == prep.index:
             stream = _current_stream_handle(prep.index)
             rc = lib.lv_step_multi(ctypes.byref(cfg), prep.items, prep.n, ws.data_ptr(), ws.numel(), stream)

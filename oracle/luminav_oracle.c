@@ -730,7 +730,10 @@ static int process_item(const lvo_config *cfg, const lvo_tensor *it, int threads
     memcpy(scratch, it->scratch, sizeof scratch);
     lvo_config item_cfg = *cfg;
     if (p_mode == 0 && w.mp == NULL) item_cfg.master_weights = 0; /* worker.rs:153-156 */
-    rc = core_step(&item_cfg, &w, scratch, n, it->step, it->param_index, p_mode, it->state_dtype, threads,
+    /* The core sees the promoted state mode (worker.rs:107-113 builds the view with
+     * eff_state_dtype_mode, worker.rs:141-150), so an fp16 state container never reaches the
+     * core as Float16: the v <= 65000 clamp (dual.rs:68) then follows the param dtype alone. */
+    rc = core_step(&item_cfg, &w, scratch, n, it->step, it->param_index, p_mode, s_mode, threads,
                    it->index_base);
     if (rc != LVO_OK) goto done;
 

@@ -3,7 +3,12 @@
 //   f32 -> f16 against the reference's integer algorithm (prng.rs:29-67, restated here), 2^32;
 //   f16 -> f32 against prng.rs:69-96 (restated here), 2^16;
 //   sqrt_rn against the compiler's correctly rounded square root (IEEE, as Rust's f32::sqrt), 2^32;
-//   xor_fold16 against (z ^ (z >> 16)) & 0xFFFF with the arithmetic shift of prng.rs:25, 2^32.
+//   xor_fold16 against (z ^ (z >> 16)) & 0xFFFF with the arithmetic shift of prng.rs:25, 2^32;
+//   xor_fold16_hi against the same 16 bits in the high half, 2^32;
+//   sr_bf16_hw against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
+//     with 6 noise values per input (0, 1, 0x7FFF, 0x8000, 0xFFFF and a hash of the input), 6 x 2^32;
+//   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN);
+//   pack_f16_exact on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16.
 // Test infrastructure: built by __graft_entry__.build() into tests/gpu_checks/libexactcheck.so
 // and run by tests/test_gpu_exact_exhaustive.py.
 #include <hip/hip_runtime.h>
@@ -50,6 +55,23 @@ __device__ uint32_t ref_f16_to_f32(uint32_t h) {
 
 __device__ bool is_nan(uint32_t b) { return (b & 0x7FFFFFFFu) > 0x7F800000u; }
 
+// prng.rs:137-160 with the 16-bit noise given: the bf16 bits
+__device__ uint32_t ref_sr_bf16(uint32_t p, uint32_t noise) {
+    const uint32_t a = p & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return ((p | 0x00400000u) & 0xFFFF0000u) >> 16;
+    uint32_t added = (a + noise) & 0xFFFF0000u;
+    if (added > 0x7F7F0000u) added = 0x7F7F0000u;
+    return ((p & 0x80000000u) | added) >> 16;
+}
+
+__device__ uint32_t mix32(uint32_t z) {
+    z ^= z >> 16;
+    z *= 0x7FEB352Du;
+    z ^= z >> 15;
+    z *= 0x846CA68Bu;
+    return z ^ (z >> 16);
+}
+
 __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) {
     const unsigned long long k = atomicAdd(count, 1ull);
     if (k < 8) ex[k] = input;
@@ -57,7 +79,9 @@ __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) 
 
 // Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
 // NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
-// [4] xor_fold16 mismatches; ex[8 * c + k] holds the first inputs of counter c.
+// [4] xor_fold16 mismatches, [5] xor_fold16_hi, [6] sr_bf16_hw (input, any noise),
+// [7] sqrt_rn_normal on its domain, [8] pack_f16_exact; ex[8 * c + k] holds the first inputs of
+// counter c.
 __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex) {
     const uint32_t i = base + blockIdx.x * blockDim.x + threadIdx.x;
     if (lv::f32_to_f16_rne(__uint_as_float(i)) != ref_f32_to_f16(i)) record(&out[0], ex + 0, i);
@@ -65,6 +89,33 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     const uint32_t s_ref = __float_as_uint(__builtin_sqrtf(__uint_as_float(i)));
     if (s != s_ref && !(is_nan(s) && is_nan(s_ref))) record(&out[3], ex + 24, i);
     if (lv::xor_fold16(i) != ((i ^ (uint32_t)((int32_t)i >> 16)) & 0xFFFFu)) record(&out[4], ex + 32, i);
+    if (lv::xor_fold16_hi(i) != (((i ^ (i >> 16)) & 0xFFFFu) << 16)) record(&out[5], ex + 40, i);
+    const uint32_t h = mix32(i);
+    const uint32_t noises[6] = {0u, 1u, 0x7FFFu, 0x8000u, 0xFFFFu, h & 0xFFFFu};
+#pragma unroll
+    for (int k = 0; k < 6; k++) {
+        const uint32_t got = __float_as_uint(lv::sr_bf16_hw(__uint_as_float(i), noises[k] << 16)) >> 16;
+        if (got != ref_sr_bf16(i, noises[k])) record(&out[6], ex + 48, i);
+    }
+    const float x = __uint_as_float(i);
+    if (!(x < 0x1p-96f) || x == 0.0f) {
+        const uint32_t n = __float_as_uint(lv::sqrt_rn_normal(x));
+        if (n != s_ref && !(is_nan(n) && is_nan(s_ref))) record(&out[7], ex + 56, i);
+    }
+}
+
+// pack_f16_exact: every finite f16 value h (as f32), and the canonical quiet NaNs, against the
+// reference's f32 -> f16 RNE; the packed word holds the value in both halves. The infinities are
+// not in the domain: the reference's fp16 quantisation saturates them to +-65504 (prng.rs:29-67,
+// prng.rs:98-130), so no quantised value is infinite.
+__global__ void check_pack_f16(unsigned long long *out, uint32_t *ex) {
+    const uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;  // grid covers exactly 2^16
+    if ((h & 0x7FFFu) == 0x7C00u) return;
+    uint32_t xb = ref_f16_to_f32(h);
+    if (is_nan(xb)) xb = (xb & 0x80000000u) | 0x7FC00000u;  // quantisation yields canonical NaNs only
+    const float x = __uint_as_float(xb);
+    const uint32_t want = ref_f32_to_f16(xb);
+    if (lv::pack_f16_exact(x, x) != (want | (want << 16))) record(&out[8], ex + 64, h);
 }
 
 __global__ void check_f16_to_f32(unsigned long long *out, uint32_t *ex) {
@@ -81,20 +132,25 @@ __global__ void check_f16_to_f32(unsigned long long *out, uint32_t *ex) {
 
 }  // namespace
 
-extern "C" int exact_check(unsigned long long *host_counts /* 5 */, uint32_t *host_examples /* 40 */) {
+constexpr int kCounters = 9;
+
+extern "C" int exact_check(unsigned long long *host_counts /* kCounters */, uint32_t *host_examples /* 8 x kCounters */) {
     unsigned long long *out = nullptr;
     uint32_t *ex = nullptr;
-    if (hipMalloc(&out, 5 * sizeof(unsigned long long)) != hipSuccess) return -1;
-    if (hipMalloc(&ex, 40 * sizeof(uint32_t)) != hipSuccess) return -1;
-    if (hipMemset(out, 0, 5 * sizeof(unsigned long long)) != hipSuccess) return -1;
-    if (hipMemset(ex, 0, 40 * sizeof(uint32_t)) != hipSuccess) return -1;
+    if (hipMalloc(&out, kCounters * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMalloc(&ex, 8 * kCounters * sizeof(uint32_t)) != hipSuccess) return -1;
+    if (hipMemset(out, 0, kCounters * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMemset(ex, 0, 8 * kCounters * sizeof(uint32_t)) != hipSuccess) return -1;
     const uint32_t per = 1u << 24;  // 65536 blocks of 256 per launch; 256 launches cover 2^32
     for (uint64_t base = 0; base < (1ull << 32); base += per) check_2_32<<<per / 256, 256>>>((uint32_t)base, out, ex);
     check_f16_to_f32<<<(1u << 16) / 256, 256>>>(out, ex);
+    check_pack_f16<<<(1u << 16) / 256, 256>>>(out, ex);
     int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -2;
-    if (rc == 0 && hipMemcpy(host_counts, out, 5 * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
+    if (rc == 0 &&
+        hipMemcpy(host_counts, out, kCounters * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
         rc = -3;
-    if (rc == 0 && hipMemcpy(host_examples, ex, 40 * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) rc = -3;
+    if (rc == 0 && hipMemcpy(host_examples, ex, 8 * kCounters * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess)
+        rc = -3;
     (void)hipFree(out);
     (void)hipFree(ex);
     return rc;

@@ -19,7 +19,8 @@ HEADER = os.path.join(ROOT, "include", "luminav_hip.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(lv_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b((?:lv|luminav_triton)_\w+)\s*\(", text,
+                                 flags=re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -40,18 +41,227 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, name), name
 
 
+INLINE = 48 * 65 * 64          # inline count slots: 48 tensors x 65 slots, 64 B apart
+FIXED = INLINE + 512 + 48 * 32  # + radial tickets and running sums
+
+
+def _chunk_bytes(units):
+    return ((-(-units // 4096) + 48) * 32 + 255) // 256 * 256 if units else 0
+
+
 def test_version_and_workspace(lib):
-    assert lib.lv_version() >= 100
+    assert lib.lv_version() >= 300
     ws = lib.lv_workspace_bytes(1)
     assert ws % 256 == 0
-    # the launches of a call reuse per-launch regions, so the size does not grow with the count
+    # the launches of a call reuse per-launch regions, so the size does not grow up to 48 tensors
     assert lib.lv_workspace_bytes(48) == ws
-    # 48 x 65 count words 64 B apart, 48 tickets, and the radial records of one 2^22-unit piece
-    # (2 doubles + a u32 count per unit)
-    assert ws >= 48 * 65 * 64 + 48 * 8 + (1 << 22) * 20
-    # more than 48 tensors: table launches add count words and a descriptor table for 960 tensors
-    assert lib.lv_workspace_bytes(49) == ws + 960 * 65 * 64 + 960 * 80
-    assert lib.lv_workspace_bytes(100_000) == lib.lv_workspace_bytes(49)
+    # the upper bound holds one full radial piece of 2^22 unit records (2 doubles + a u32 count)
+    assert ws == FIXED + _chunk_bytes(1 << 22) + (1 << 22) * 16 + (1 << 22) * 4
+    # more than 48 tensors: table launches add up to 65 count slots of 64 B per tensor
+    assert lib.lv_workspace_bytes(49) == ws + (49 * 65 * 64 + 255) // 256 * 256
+
+
+def table_count_slots(units):
+    """Count slots of a table-launch tensor: the smallest power of two keeping every slot at
+    <= 64 blocks, at most 64."""
+    c = (units + 63) // 64
+    return 1 if c <= 1 else 64 if c >= 64 else 1 << (c - 1).bit_length()
+
+
+def test_table_count_slots_bound_blocks_per_slot():
+    for u in list(range(1, 5000)) + [65_536, 1 << 20, 6_580_484]:
+        s = table_count_slots(u)
+        assert s & (s - 1) == 0 and 1 <= s <= 64 and s <= u
+        assert -(-u // s) <= 64 or s == 64
+
+
+def _tensors(sizes, radial=False, base=1 << 20):
+    ts = (H.LvTensor * len(sizes))()
+    for k, n in enumerate(sizes):
+        ts[k].numel, ts[k].step = n, 1
+        off = base * (k + 1) * 16
+        ts[k].param, ts[k].grad, ts[k].exp_avg, ts[k].exp_avg_sq, ts[k].scratch = (
+            off, off + base * 4, off + base * 8, off + base * 12, off + base * 15)
+    return ts
+
+
+def test_workspace_bytes_for_a_call(lib):
+    """The per-call size: without the radial bound no radial records at all (a 6.7e9-element
+    bucket needs 197 KiB); with it, one record per 1024-element unit up to a 2^22-unit piece;
+    above 48 tensors, table_count_slots(units) + 1 count slots per tensor."""
+    cfg = _cfg(buffer="T2")
+    rcfg = _cfg(buffer="T2", bound_type="radial")
+    big = _tensors([6_738_415_616])
+    assert lib.lv_workspace_bytes_for(ctypes.byref(cfg), big, 1) == FIXED
+    assert FIXED < 5 << 20
+    units = -(-6_738_415_616 // 1024)
+    assert units > 1 << 22
+    assert lib.lv_workspace_bytes_for(ctypes.byref(rcfg), big, 1) == (
+        FIXED + _chunk_bytes(1 << 22) + (1 << 22) * 16 + (1 << 22) * 4)
+    small = _tensors([1000, 5000])
+    u = 1 + 5
+    assert lib.lv_workspace_bytes_for(ctypes.byref(rcfg), small, 2) == (
+        FIXED + _chunk_bytes(u) + u * 16 + (u * 4 + 255) // 256 * 256)
+    sizes = [1 + 997 * k for k in range(2000)]
+    many = _tensors(sizes, base=1 << 24)
+    slots = sum(table_count_slots(-(-n // 1024)) + 1 for n in sizes)
+    got = lib.lv_workspace_bytes_for(ctypes.byref(cfg), many, len(sizes))
+    assert got == FIXED + (slots * 64 + 255) // 256 * 256
+    assert got < 5 << 20  # 2000 tensors without the radial bound
+
+
+def _run(lib, cfg, ts, n=None, ws_bytes=None):
+    n = len(ts) if n is None else n
+    nb = lib.lv_workspace_bytes_for(ctypes.byref(cfg), ts, n) if ws_bytes is None else ws_bytes
+    ws = (ctypes.c_uint8 * (nb + 256))()
+    addr = (ctypes.addressof(ws) + 255) // 256 * 256
+    return lib.lv_step_multi(ctypes.byref(cfg), ts, n, addr, nb, None)
+
+
+def test_host_side_rejections_without_device(lib):
+    cfg = _cfg(buffer="T2")
+    t = H.LvTensor()
+    WS = lib.lv_workspace_bytes_for(ctypes.byref(cfg), ctypes.byref(t), 1)
+    ws = (ctypes.c_uint8 * (WS + 256))()
+    wsa = (ctypes.addressof(ws) + 255) // 256 * 256
+    assert lib.lv_step_multi(None, ctypes.byref(t), 1, wsa, WS, None) == -1
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 0, wsa, WS, None) == 0  # nothing to do
+    assert lib.lv_step_multi(ctypes.byref(cfg), None, 1, wsa, WS, None) == -1
+    bad = _cfg(buffer="T2")
+    bad.lr = float("nan")
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, wsa, WS, None) == -3
+    assert b"learning rate" in lib.lv_last_error()
+    bad = _cfg(buffer="T2")
+    bad.beta2 = 1.0
+    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, wsa, WS, None) == -3
+    # a misaligned workspace
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa + 16, WS, None) == -3
+    assert b"aligned" in lib.lv_last_error()
+    # a tensor with numel but no pointers
+    t.numel, t.step = 10, 1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa, WS, None) == -1
+    assert b"null" in lib.lv_last_error()
+    # missing exp_avg_sq in a dual-state mode, missing master for bf16 with master weights
+    t.param, t.grad, t.exp_avg, t.scratch = 0x10000, 0x30000, 0x20000, 0x50000
+    t.param_dtype = t.grad_dtype = 1
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa, WS, None) == -1
+    assert b"exp_avg_sq" in lib.lv_last_error()
+    t.exp_avg_sq = 0x40000
+    mcfg = _cfg(buffer="T2", master_weights="full")
+    assert lib.lv_step_multi(ctypes.byref(mcfg), ctypes.byref(t), 1, wsa, WS, None) == -1
+    assert b"master_param" in lib.lv_last_error()
+    # a too-small workspace
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa, 8, None) == -3
+    assert b"workspace too small" in lib.lv_last_error()
+    # inactive ranges: a count without a table
+    t.n_inactive = 2
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa, WS, None) == -1
+    assert b"inactive" in lib.lv_last_error()
+    t.n_inactive = 0
+    # more than 48 tensors need table count slots in the workspace
+    many = _tensors([10] * 49)
+    assert lib.lv_step_multi(ctypes.byref(cfg), many, 49, wsa, WS, None) == -3
+    assert b"workspace too small" in lib.lv_last_error()
+    # a dtype code out of range
+    t.grad_dtype = 7
+    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, wsa, WS, None) == -3
+    assert b"dtype" in lib.lv_last_error()
+
+
+ALIAS = b"Pointer aliasing detected"
+
+
+def test_aliasing_rules_of_step_pyo3(lib):
+    """optimizer/src/python_ffi/mod.rs:131-173, rule by rule, with the reference's messages; the
+    call is rejected (-3) on the host before anything reaches the device."""
+    cfg = _cfg(buffer="T2")
+    ts = _tensors([100, 200, 300])
+    assert ts[0].param != ts[1].param
+    # an item's grad equal to its own param or exp_avg
+    ts[1].grad = ts[1].param
+    assert _run(lib, cfg, ts) == -3 and b"grad_ptr" in lib.lv_last_error() and ALIAS in lib.lv_last_error()
+    ts = _tensors([100, 200, 300])
+    ts[1].grad = ts[1].exp_avg
+    assert _run(lib, cfg, ts) == -3 and b"grad_ptr" in lib.lv_last_error()
+    # a mutable pointer referenced twice across items: param, exp_avg, scratch
+    for field in ("param", "exp_avg", "scratch"):
+        ts = _tensors([100, 200, 300])
+        setattr(ts[2], field, getattr(ts[0], field))
+        assert _run(lib, cfg, ts) == -3, field
+        assert b"mutable pointer" in lib.lv_last_error() and b"referenced multiple times" in lib.lv_last_error()
+    # exp_avg_sq and master_param have their own messages
+    ts = _tensors([100, 200, 300])
+    ts[2].exp_avg_sq = ts[0].exp_avg_sq
+    assert _run(lib, cfg, ts) == -3 and b"mutable exp_avg_sq pointer" in lib.lv_last_error()
+    ts = _tensors([100, 200, 300])
+    ts[0].master_param = ts[0].param + 0x1000  # inside no other buffer
+    ts[2].master_param = ts[0].master_param
+    assert _run(lib, cfg, ts) == -3 and b"mutable master_param pointer" in lib.lv_last_error()
+    # an fp32 param's master may be the param itself (worker.rs:95-98)
+    ts = _tensors([100, 200, 300])
+    for k in range(3):
+        ts[k].master_param = ts[k].param
+    assert _run(lib, _cfg(buffer="T2", master_weights="full"), ts, ws_bytes=8) == -3
+    assert b"workspace too small" in lib.lv_last_error()  # got past the aliasing checks
+    # a grad equal to another item's mutable pointer
+    ts = _tensors([100, 200, 300])
+    ts[2].grad = ts[0].exp_avg
+    assert _run(lib, cfg, ts) == -3 and b"grad_ptr" in lib.lv_last_error()
+    # grads may be shared between items (they are only read)
+    ts = _tensors([100, 200, 300])
+    ts[2].grad = ts[1].grad = ts[0].grad
+    assert _run(lib, cfg, ts, ws_bytes=8) == -3 and b"workspace too small" in lib.lv_last_error()
+
+
+def test_overlapping_buffers_are_rejected(lib):
+    """Beyond the reference's equal-pointer rule: a launch runs every tensor of a class at once,
+    so buffers that merely overlap are rejected too (and so is a grad overlapping a mutable
+    buffer)."""
+    cfg = _cfg(buffer="T2")
+    ts = _tensors([1000, 1000])
+    ts[1].param = ts[0].param + 400  # bf16? no: f32, 4000 bytes long
+    assert _run(lib, cfg, ts) == -3 and b"overlap" in lib.lv_last_error()
+    ts = _tensors([1000, 1000])
+    ts[1].grad = ts[0].exp_avg_sq + 8
+    assert _run(lib, cfg, ts) == -3 and b"grad_ptr" in lib.lv_last_error()
+    # the scratch (6 floats) is a buffer too
+    ts = _tensors([1000, 1000])
+    ts[1].scratch = ts[0].scratch + 12
+    assert _run(lib, cfg, ts) == -3 and b"overlap" in lib.lv_last_error()
+    # adjacent but disjoint buffers are fine
+    ts = _tensors([1000, 1000])
+    ts[1].param = ts[0].param + 4000
+    assert _run(lib, cfg, ts, ws_bytes=8) == -3 and b"workspace too small" in lib.lv_last_error()
+
+
+def test_duplicate_tensor_is_rejected_whatever_the_mode(lib):
+    """The same tensor twice in one call (LuminaV([w, w]) unfused) is a rejected call, not two
+    steps in one launch."""
+    for kw in (dict(buffer=1), dict(buffer=2), dict(buffer="T1"), dict(buffer="T2", bound_type="radial"),
+               dict(buffer=2, cautious=False)):
+        cfg = _cfg(**kw)
+        ts = _tensors([4096, 4096])
+        ts[1] = ts[0]
+        assert _run(lib, cfg, ts) == -3, kw
+        assert ALIAS in lib.lv_last_error()
+
+
+def test_f32_and_standalone_entry_points_without_device(lib):
+    """lv_step_f32 and the reference's standalone API answer on the host as the reference does:
+    a null pointer is -1 before anything else; with no device, engine_create is NULL, and a NULL
+    engine reports platform "none" and arch "unknown" (c_api.rs:9-68)."""
+    f = 1e-3
+    args = (f, 0.9, 0.999, 1e-8, 0.08, 0.8, 0.3, 2, 1, 2, 0.05, 1, 7)
+    assert lib.lv_step_f32(None, 0x1000, 0x2000, 0x3000, None, 0x4000, 10, *args, None) == -1
+    assert lib.lv_step_f32(0x1000, 0x2000, 0x3000, 0x3400, None, None, 10, *args, None) == -1
+    assert lib.luminav_triton_step_f32(None, 0x1000, 0x2000, 0x3000, 0x3400, None, 0x4000, 10, *args) == -1
+    assert lib.luminav_triton_get_platform(None) == b"none"
+    assert lib.luminav_triton_get_arch(None) == b"unknown"
+    lib.luminav_triton_engine_destroy(None)
+    import torch
+
+    if not torch.cuda.is_available():
+        assert not lib.luminav_triton_engine_create()
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -82,62 +292,6 @@ def _cfg(**kw):
     from tests.parity_util import group_dict
 
     return H.make_config(group_dict(**kw))
-
-
-def test_host_side_rejections_without_device(lib):
-    cfg = _cfg(buffer="T2")
-    WS = lib.lv_workspace_bytes(1)
-    ws = (ctypes.c_uint8 * WS)()
-    t = H.LvTensor()
-    assert lib.lv_step_multi(None, ctypes.byref(t), 1, ws, WS, None) == -1
-    assert lib.lv_step_multi(ctypes.byref(cfg), None, 0, ws, WS, None) == 0  # nothing to do
-    assert lib.lv_step_multi(ctypes.byref(cfg), None, 1, ws, WS, None) == -1
-    bad = _cfg(buffer="T2")
-    bad.lr = float("nan")
-    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, WS, None) == -3
-    assert b"learning rate" in lib.lv_last_error()
-    bad = _cfg(buffer="T2")
-    bad.beta2 = 1.0
-    assert lib.lv_step_multi(ctypes.byref(bad), ctypes.byref(t), 1, ws, WS, None) == -3
-    # a tensor with numel but no pointers
-    t.numel, t.step = 10, 1
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
-    assert b"null" in lib.lv_last_error()
-    # missing exp_avg_sq in a dual-state mode, missing master for bf16 with master weights
-    t.param = t.grad = t.exp_avg = t.scratch = 0x1000
-    t.param_dtype = t.grad_dtype = 1
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
-    assert b"exp_avg_sq" in lib.lv_last_error()
-    t.exp_avg_sq = 0x2000
-    mcfg = _cfg(buffer="T2", master_weights="full")
-    assert lib.lv_step_multi(ctypes.byref(mcfg), ctypes.byref(t), 1, ws, WS, None) == -1
-    assert b"master_param" in lib.lv_last_error()
-    # step 0, a too-small workspace, grad aliasing param
-    t.step = 0
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -3
-    t.step = 1
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, 8, None) == -3
-    t.grad = t.param
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -3
-    # inactive ranges: a count without a table
-    t.grad = 0x3000
-    t.n_inactive = 2
-    assert lib.lv_step_multi(ctypes.byref(cfg), ctypes.byref(t), 1, ws, WS, None) == -1
-    assert b"inactive" in lib.lv_last_error()
-    t.n_inactive = 0
-    t.grad = t.param
-    # more than 48 tensors need the table-launch regions of the workspace
-    many = (H.LvTensor * 49)()
-    for k in range(49):
-        many[k].numel, many[k].step = 10, 1
-        many[k].param, many[k].grad, many[k].exp_avg, many[k].exp_avg_sq, many[k].scratch = (
-            0x1000, 0x3000, 0x2000, 0x2400, 0x2800)
-    assert lib.lv_step_multi(ctypes.byref(cfg), many, 49, ws, WS, None) == -3
-    assert b"workspace too small" in lib.lv_last_error()
-    # radial: same host checks (the call is never launched here)
-    rcfg = _cfg(buffer="T2", bound_type="radial")
-    assert lib.lv_step_multi(ctypes.byref(rcfg), ctypes.byref(t), 1, ws, WS, None) == -3
-    assert b"aliases" in lib.lv_last_error()
 
 
 def test_xcd_block_mapping_is_exact_and_bijective():

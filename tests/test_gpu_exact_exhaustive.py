@@ -7,7 +7,13 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   (the hardware returns them quietened, same sign);
 * sqrt_rn against the IEEE square root (the compiler's correctly rounded one, as Rust's
   f32::sqrt): all 2^32 inputs bit for bit, NaN for NaN;
-* xor_fold16 against (z ^ (z >> 16)) & 0xFFFF: all 2^32 inputs.
+* xor_fold16 against (z ^ (z >> 16)) & 0xFFFF, and xor_fold16_hi against the same bits in the
+  high half: all 2^32 inputs;
+* sr_bf16_hw (the hardware stochastic-rounding converter with the reference's saturation)
+  against the reference's integer recipe (prng.rs:137-160): all 2^32 inputs x 6 noise values;
+* sqrt_rn_normal (no rescaling) against the IEEE square root on every input of its domain;
+* pack_f16_exact against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
+  reference's fp16 quantisation never yields an infinity).
 """
 from __future__ import annotations
 
@@ -34,9 +40,9 @@ def _lib():
 def test_exact_helpers_on_every_input():
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
-    counts = (ctypes.c_ulonglong * 5)()
-    ex = (ctypes.c_uint32 * 40)()
-    print("[case] exact helpers, 3 x 2^32 + 2^16 inputs", flush=True)
+    counts = (ctypes.c_ulonglong * 9)()
+    ex = (ctypes.c_uint32 * 72)()
+    print("[case] exact helpers, 2^32 inputs x 11 checks + 2 x 2^16", flush=True)
     assert _lib().exact_check(counts, ex) == 0
     assert counts[0] == 0, ("f32->f16", [hex(x) for x in ex[0:8]])
     assert counts[1] == 0, ("f16->f32", [hex(x) for x in ex[8:16]])
@@ -44,3 +50,7 @@ def test_exact_helpers_on_every_input():
     assert counts[2] <= 2 * 511
     assert counts[3] == 0, ("sqrt_rn", [hex(x) for x in ex[24:32]])
     assert counts[4] == 0, ("xor_fold16", [hex(x) for x in ex[32:40]])
+    assert counts[5] == 0, ("xor_fold16_hi", [hex(x) for x in ex[40:48]])
+    assert counts[6] == 0, ("sr_bf16_hw", [hex(x) for x in ex[48:56]])
+    assert counts[7] == 0, ("sqrt_rn_normal", [hex(x) for x in ex[56:64]])
+    assert counts[8] == 0, ("pack_f16_exact", [hex(x) for x in ex[64:72]])

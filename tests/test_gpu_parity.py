@@ -7,6 +7,7 @@ stricter than the 1e-6 relative / 1 bf16 ULP tolerance of the target.
 """
 from __future__ import annotations
 
+import contextlib
 import sys
 
 import pytest
@@ -42,12 +43,15 @@ def _run_case(oracle_mod, sizes, pdt, gdt, sdt, steps=5, seed=7, **gkw):
     st = _stepper()
     label = f"{gkw} {pdt}/{gdt}/{sdt}"
     print(f"[case] {label} sizes={len(sizes)}", flush=True)
-    for s in range(1, steps + 1):
-        grads = host.grads(s, seed)
-        host.oracle_step(O, cfg, grads, s)
-        dev.hip_step(st, group, [g.cuda() for g in grads], s)
-        torch.cuda.synchronize()
-        host.assert_equal(dev, f"{label} step {s}")
+    # radial sums: the kernels' f64 sums, bitwise against the oracle's f64 sum mode (test_gpu_radial.py)
+    radial = group["bound"] and group["bound_type"] == 1
+    with (O.radial_sum_f64() if radial else contextlib.nullcontext()):
+        for s in range(1, steps + 1):
+            grads = host.grads(s, seed)
+            host.oracle_step(O, cfg, grads, s)
+            dev.hip_step(st, group, [g.cuda() for g in grads], s)
+            torch.cuda.synchronize()
+            host.assert_equal(dev, f"{label} step {s}")
 
 
 CASES = [
@@ -91,39 +95,114 @@ def test_many_tensors_multiple_launches(oracle_mod):
     _run_case(oracle_mod, sizes, "f32", "f32", "f32", steps=4, buffer=1, lr=8e-4)
 
 
-# Leading workspace bytes that must be zero between calls (48 x 65 count words 64 B apart and
-# 512 B of radial tickets), and the count words of table launches (960 tensors) that follow the
-# fixed regions.
-ZERO_BYTES = 48 * 65 * 64 + 512
-TABLE_SLOT_BYTES = 960 * 65 * 64
+def assert_workspace_zero(stepper, label):
+    """Every call leaves the whole workspace zero (count slots, tickets and radial records)."""
+    for ws in stepper.workspace._bufs.values():
+        nz = int(torch.count_nonzero(ws))
+        assert nz == 0, f"{label}: {nz} workspace bytes left set"
 
 
 @pytest.mark.parametrize("count,buffer,pdt,sdt,extra", [
     (1000, "T2", "bf16", "f32", {}),
     (2000, 1, "f32", "f32", {"lam": 0.3}),
+    (5000, 1, "f32", "f32", {"lam": 0.3, "cautious": True}),
     (1000, 2, "bf16", "f32", {"master_weights": "full"}),
     (1000, 2, "f32", "f32", {"cautious": False}),
     (1000, "T1", "bf16", "bf16", {"state_precision": "param", "fused_single_pass": False}),
-], ids=["T2-bf16-1000", "TDCLM-f32-2000", "CLM-master-1000", "CLM-nocautious-1000", "T1-bf16state-twopass-1000"])
+], ids=["T2-bf16-1000", "TDCLM-f32-2000", "TDCLM-f32-5000", "CLM-master-1000", "CLM-nocautious-1000",
+        "T1-bf16state-twopass-1000"])
 def test_table_launches_thousands_of_tensors(oracle_mod, count, buffer, pdt, sdt, extra):
-    """More tensors than the kernel-argument table holds: the descriptors go to the workspace
-    (up to 960 per launch, the first units stay in the kernel arguments), so 1000 ragged tensors
-    are one table launch and an inline launch of 40, and 2000 are 960 + 960 + 80. Every buffer
-    and scratch bit for bit over the two-pass first step and fused steps; the count words of both
-    kinds of launch are left zero."""
+    """More tensors than the kernel-argument table holds: every class is ONE table launch (pair)
+    whatever its tensor count, its descriptors in a device table and every group-th tensor's first
+    unit in the kernel arguments (2000 tensors: groups of 3; 5000: groups of 6, a second binary
+    search in the device table). Every buffer and scratch bit for bit over the two-pass first step
+    and fused steps; the whole workspace is left zero."""
     _table_case(oracle_mod, count, buffer, pdt, sdt, extra)
+
+
+def test_table_upload_skipped_and_reused(oracle_mod):
+    """Descriptor tables stay on the device: a step whose table equals one already uploaded
+    launches with no upload. Grads alternate between two buffer sets (tables A, B, A, B, ...) and
+    a third set appears once (a fresh upload into the least recently used slot); every step bit
+    for bit against the oracle."""
+    import numpy as np
+
+    _need_gpu()
+    O = oracle_mod
+    group = group_dict(buffer="T2", lr=1e-3)
+    cfg = oracle_config(O, group)
+    rng = np.random.default_rng(8)
+    sizes = [int(np.exp(rng.uniform(0, np.log(9000)))) + 1 for _ in range(120)]
+    host = TensorSet(sizes, "bf16", "bf16", "f32", True, False, 21)
+    dev = host.to("cuda")
+    st = _stepper()
+    bufs = [[torch.empty(n, dtype=torch.bfloat16, device="cuda") for n in sizes] for _ in range(3)]
+    print("[case] table upload skip", flush=True)
+    for s, which in enumerate((0, 1, 0, 1, 2, 0, 0, 1), start=1):
+        grads = host.grads(s, 21)
+        for b, g in zip(bufs[which], grads):
+            b.copy_(g)
+        host.oracle_step(O, cfg, grads, s)
+        dev.hip_step(st, group, bufs[which], s)
+        torch.cuda.synchronize()
+        host.assert_equal(dev, f"step {s} (grad set {which})")
+        assert_workspace_zero(st, f"step {s}")
+
+
+PARTIAL = [1, 3, 4, 5, 1021, 1023, 1024, 1025, 1027, 2045, 2047, 2048, 2049, 3075, 4097, 6143, 65541]
+
+
+@pytest.mark.parametrize("buffer,pdt,sdt,extra", [
+    ("T2", "bf16", "f32", {}),
+    ("T2", "bf16", "bf16", {"state_precision": "param"}),
+    (2, "f32", "f32", {}),
+    (1, "f16", "f16", {"state_precision": "param"}),
+    ("T1", "bf16", "f32", {"bound_type": "radial"}),
+])
+def test_partial_units_keep_the_vector_layout(oracle_mod, buffer, pdt, sdt, extra):
+    """A tensor's last, partial unit: every thread's 4-element groups that lie wholly inside the
+    tensor take the vector path and only the group straddling the end goes element by element
+    (1024-element units with f32 state, 2048 with 16-bit state: sizes around both)."""
+    kw = dict(extra)
+    kw.setdefault("lr", 1e-3)
+    _run_case(oracle_mod, PARTIAL, pdt, pdt, sdt, steps=4, buffer=buffer, **kw)
+
+
+def test_v_clamp_follows_param_dtype_with_fp16_state_container(oracle_mod):
+    """dual.rs:68 clamps v at 65000 for fp16 params only on the reference's native path: the FFI
+    worker hands an fp16 state container to the core as bitwise bf16 (worker.rs:107-113). A bf16
+    param with an fp16 state container and gradients large enough that v exceeds 65000 keeps the
+    unclamped v; an fp16 param is clamped. Through the C ABI, bitwise against the oracle."""
+    _need_gpu()
+    O = oracle_mod
+    for buffer in (2, "T2"):
+        for pdt in ("bf16", "f32", "f16"):
+            group = group_dict(buffer=buffer, lr=1e-3)
+            cfg = oracle_config(O, group)
+            host = TensorSet([5000, 2048], pdt, pdt, "f16", True, False, 3)
+            dev = host.to("cuda")
+            st = _stepper()
+            print(f"[case] v clamp buffer={buffer} {pdt} + fp16 state container", flush=True)
+            for s in range(1, 4):
+                grads = host.grads(s, 3, scale=1.0e4, zero_frac=0.0)
+                host.oracle_step(O, cfg, grads, s)
+                dev.hip_step(st, group, [g.cuda() for g in grads], s)
+                torch.cuda.synchronize()
+                host.assert_equal(dev, f"buffer={buffer} {pdt} step {s}")
+            vmax = float(dev.v[0].view(torch.bfloat16).float().max())
+            assert (vmax <= 65024.0) == (pdt == "f16"), (buffer, pdt, vmax)
 
 
 def test_table_launch_split_into_pieces(oracle_mod, monkeypatch):
     """A table launch cut into pieces of 37 blocks (LV_MAX_GRID_BLOCKS): each piece finds its
-    tensors through the first units in the kernel arguments, and counts fold across pieces."""
+    tensors through the heads in the kernel arguments, and counts fold across pieces."""
     monkeypatch.setenv("LV_MAX_GRID_BLOCKS", "37")
     _table_case(oracle_mod, 100, "T2", "bf16", "f32", {})
 
 
 def test_table_launches_from_two_host_threads(oracle_mod):
     """Two host threads, each with its own stepper (workspace) and stream, step 100-tensor sets
-    at the same time: table launches share the device's pinned staging ring, whose slots are
+    at the same time: table launches share the device's descriptor-table ring, whose slots are
     leased to one call at a time. Both end bit for bit equal to the oracle."""
     import threading
 
@@ -170,7 +249,7 @@ def test_table_launches_from_two_host_threads(oracle_mod):
 
 def _table_case(oracle_mod, count, buffer, pdt, sdt, extra):
     """`count` ragged tensors (plus three larger ones) stepped three times, bitwise against the
-    oracle, with the count words of inline and table launches checked zero after every step."""
+    oracle, with the whole workspace checked zero after every step."""
     import numpy as np
 
     _need_gpu()
@@ -193,14 +272,7 @@ def _table_case(oracle_mod, count, buffer, pdt, sdt, extra):
         dev.hip_step(st, group, [g.cuda() for g in grads], s)
         torch.cuda.synchronize()
         host.assert_equal(dev, f"{count} tensors step {s}")
-        for ws in st.workspace._bufs.values():
-            assert int(torch.count_nonzero(ws[:ZERO_BYTES])) == 0, f"count words left set (step {s})"
-            from luminamoon_amd.optimizer import hip_backend
-
-            fixed = int(hip_backend.load_library().lv_workspace_bytes(1))
-            table_words = ws[fixed:fixed + TABLE_SLOT_BYTES]
-            assert table_words.numel() == TABLE_SLOT_BYTES
-            assert int(torch.count_nonzero(table_words)) == 0, f"table count words left set (step {s})"
+        assert_workspace_zero(st, f"{count} tensors step {s}")
 
 
 def test_mixed_steps_in_one_call(oracle_mod):
@@ -385,18 +457,18 @@ def test_unit_launch_split_into_pieces(oracle_mod, monkeypatch, buffer, pdt, sdt
             dev.hip_step(st, group, [g.cuda() for g in grads], s)
             torch.cuda.synchronize()
             host.assert_equal(dev, f"cap {cap} step {s}")
-            for ws in st.workspace._bufs.values():  # count words + radial tickets
-                zero = ws[:48 * 65 * 64 + 512]
-                assert int(torch.count_nonzero(zero)) == 0, f"workspace not left zeroed (cap {cap} step {s})"
+            assert_workspace_zero(st, f"cap {cap} step {s}")
 
 
-@pytest.mark.parametrize("buffer", [1, 2, 3, 4])
-@pytest.mark.parametrize("cautious,bound_mode", [(1, 2), (0, 2), (1, 0)])
-def test_lv_step_f32_matches_oracle(oracle_mod, buffer, cautious, bound_mode):
-    """lv_step_f32, the argument-for-argument twin of the reference's luminav_triton_step_f32
-    (luminav_triton_standalone.h:89-111), called through the C ABI on device pointers: four steps
-    (two-pass, then fused) bitwise equal to the oracle with the reference's defaults for the
-    rest (ema_decay per buffer mode, clamp_min 0.5, SR and fused single pass on)."""
+@pytest.mark.parametrize("buffer", [1, 2])
+@pytest.mark.parametrize("cautious,bound_mode", [(1, 2), (0, 2), (1, 0), (1, 5)])
+@pytest.mark.parametrize("master", [False, True])
+def test_lv_step_f32_matches_oracle(oracle_mod, buffer, cautious, bound_mode, master):
+    """lv_step_f32 with the argument mapping of the reference's luminav_triton_step_f32
+    (c_api.rs:108-199) on device pointers: buffer_mode 1 TD-CLM, 2 the dual buffer; bound_mode 1
+    radial, 2 coordinate, anything else none; master weights iff a master buffer is passed;
+    ema_decay per buffer mode, clamp_min 0.5, stochastic rounding off, fused single pass on. Four
+    steps (two-pass, then fused) bitwise equal to the oracle with that configuration."""
     _need_gpu()
     import ctypes
 
@@ -407,32 +479,114 @@ def test_lv_step_f32_matches_oracle(oracle_mod, buffer, cautious, bound_mode):
     O = oracle_mod
     L = hip_backend.load_library()
     n = 70_001
-    dual = buffer in (2, 4)
-    rng = np.random.default_rng(31 + buffer)
+    dual = buffer == 2
+    rng = np.random.default_rng(31 + buffer + 2 * bound_mode)
     p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
     hp, hm = torch.from_numpy(p0.copy()), torch.zeros(n)
     hv = torch.zeros(n) if dual else None
+    hmp = torch.from_numpy((p0 + 1e-4).astype(np.float32)) if master else None
     hs = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
     dp, dm = hp.clone().cuda(), hm.clone().cuda()
     dv = hv.clone().cuda() if dual else None
+    dmp = hmp.clone().cuda() if master else None
     ds = hs.clone().cuda()
-    code = {1: 1, 2: 2, 3: "T1", 4: "T2"}[buffer]
-    cfg = O.make_config(lr=1e-3, buffer=code, cautious=bool(cautious), bound_type=bound_mode, seed=77)
+    cfg = O.make_config(lr=1e-3, buffer=buffer, cautious=bool(cautious), bound=bound_mode > 0,
+                        bound_type=bound_mode if bound_mode in (1, 2) else 0, seed=77, stochastic_rounding=False,
+                        master_weights=2 if master else 0)
     stream = torch.cuda.current_stream().cuda_stream
     for t in range(1, 5):
         g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32))
         dg = g.cuda()
-        rc = L.lv_step_f32(dp.data_ptr(), dg.data_ptr(), dm.data_ptr(), dv.data_ptr() if dual else None, None,
-                           ds.data_ptr(), n, 1e-3, 0.9, 0.999, 1e-8, 0.08, 0.8, 0.3, buffer, cautious, bound_mode,
-                           0.05, t, 77, ctypes.c_void_p(stream))
+        rc = L.lv_step_f32(dp.data_ptr(), dg.data_ptr(), dm.data_ptr(), dv.data_ptr() if dual else None,
+                           dmp.data_ptr() if master else None, ds.data_ptr(), n, 1e-3, 0.9, 0.999, 1e-8, 0.08, 0.8,
+                           0.3, buffer, cautious, bound_mode, 0.05, t, 77, ctypes.c_void_p(stream))
         assert rc == 0, L.lv_last_error()
-        O.step(cfg, [hp], [g], [hm], [hv], [None], [hs], [t], [0])
+        O.step(cfg, [hp], [g], [hm], [hv], [hmp], [hs], [t], [0])
         torch.cuda.synchronize()
         assert_bitwise(hp, dp, f"step {t} p")
         assert_bitwise(hm, dm, f"step {t} m")
         if dual:
             assert_bitwise(hv, dv, f"step {t} v")
+        if master:
+            assert_bitwise(hmp, dmp, f"step {t} master")
         assert_bitwise(hs, ds, f"step {t} scratch")
+
+
+def test_lv_step_f32_reference_mode_mapping(oracle_mod):
+    """Every buffer_mode other than 1 is the dual buffer, which needs exp_avg_sq, and exp_avg_sq
+    is taken only for buffer_mode 2 (c_api.rs:120-146): modes 3, 4 and 7, and mode 2 without
+    exp_avg_sq, fail with -4 and leave the buffers untouched; an invalid hyper-parameter is -4 too
+    (c_api.rs:178-181)."""
+    _need_gpu()
+    import ctypes
+
+    from luminamoon_amd.optimizer import hip_backend
+
+    L = hip_backend.load_library()
+    n = 4096
+    p = torch.randn(n, device="cuda") * 0.02
+    g, m, v = torch.randn(n, device="cuda") * 1e-3, torch.zeros(n, device="cuda"), torch.zeros(n, device="cuda")
+    sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32, device="cuda")
+    p0 = p.clone()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for mode, vv in ((3, v), (4, v), (7, v), (2, None)):
+        rc = L.lv_step_f32(p.data_ptr(), g.data_ptr(), m.data_ptr(), vv.data_ptr() if vv is not None else None, None,
+                           sc.data_ptr(), n, 1e-3, 0.9, 0.999, 1e-8, 0.08, 0.8, 0.3, mode, 1, 2, 0.05, 1, 7, stream)
+        assert rc == -4, (mode, rc)
+        assert b"exp_avg_sq" in L.lv_last_error()
+    rc = L.lv_step_f32(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), None, sc.data_ptr(), n, -1.0, 0.9, 0.999,
+                       1e-8, 0.08, 0.8, 0.3, 2, 1, 2, 0.05, 1, 7, stream)
+    assert rc == -4 and b"learning rate" in L.lv_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(p, p0) and int(torch.count_nonzero(m)) == 0
+
+
+def test_standalone_engine_host_buffers(oracle_mod):
+    """The reference's standalone C API (luminav_triton_standalone.h:37-111) on this library:
+    engine_create on the current device, platform "rocm", arch the device's gfx name, and
+    luminav_triton_step_f32 on HOST buffers (copied to the device, stepped, copied back) for both
+    buffer modes, bitwise equal to the oracle over three steps; a NULL engine is -1."""
+    _need_gpu()
+    import ctypes
+
+    import numpy as np
+
+    from luminamoon_amd.optimizer import hip_backend
+
+    O = oracle_mod
+    L = hip_backend.load_library()
+    eng = L.luminav_triton_engine_create()
+    assert eng
+    try:
+        assert L.luminav_triton_get_platform(eng) == b"rocm"
+        arch = L.luminav_triton_get_arch(eng)
+        assert arch.startswith(b"gfx"), arch
+        print(f"[case] standalone engine on {arch.decode()}", flush=True)
+        P = lambda a: a.ctypes.data_as(ctypes.c_void_p) if a is not None else None  # noqa: E731
+        for buffer in (1, 2):
+            n = 50_003
+            rng = np.random.default_rng(buffer)
+            p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+            m = np.zeros(n, np.float32)
+            v = np.zeros(n, np.float32) if buffer == 2 else None
+            sc = np.array([0, 0, 0, 1, 1, 0], np.float32)
+            hp, hm, hv, hs = (torch.from_numpy(x.copy()) if x is not None else None for x in (p, m, v, sc))
+            cfg = O.make_config(lr=1e-3, buffer=buffer, cautious=True, bound_type=2, seed=5, stochastic_rounding=False)
+            for t in range(1, 4):
+                g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+                rc = L.luminav_triton_step_f32(eng, P(p), P(g), P(m), P(v), None, P(sc), n, 1e-3, 0.9, 0.999, 1e-8,
+                                               0.08, 0.8, 0.3, buffer, 1, 2, 0.05, t, 5)
+                assert rc == 0, L.lv_last_error()
+                O.step(cfg, [hp], [torch.from_numpy(g)], [hm], [hv], [None], [hs], [t], [0])
+                assert_bitwise(hp, torch.from_numpy(p), f"buffer {buffer} step {t} p")
+                assert_bitwise(hm, torch.from_numpy(m), f"buffer {buffer} step {t} m")
+                if v is not None:
+                    assert_bitwise(hv, torch.from_numpy(v), f"buffer {buffer} step {t} v")
+                assert_bitwise(hs, torch.from_numpy(sc), f"buffer {buffer} step {t} scratch")
+        assert L.luminav_triton_step_f32(None, P(p), P(g), P(m), None, None, P(sc), n, 1e-3, 0.9, 0.999, 1e-8, 0.08,
+                                         0.8, 0.3, 1, 1, 2, 0.05, 1, 5) == -1
+    finally:
+        L.luminav_triton_engine_destroy(eng)
 
 
 if __name__ == "__main__":

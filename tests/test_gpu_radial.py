@@ -40,9 +40,6 @@ def _stepper():
     return HipStepper()
 
 
-# Leading workspace bytes that must be zero between calls: 48 x 65 count words 64 B apart, then
-# the radial fold's 512 B of per-tensor tickets (the rest holds records and needs no clearing).
-WORKSPACE_ZERO_BYTES = 48 * 65 * 64 + 512
 
 
 def _run_bitwise(O, sizes, pdt, gdt, sdt, steps=4, seed=31, threads=1, check_workspace=False, **gkw):
@@ -63,9 +60,10 @@ def _run_bitwise(O, sizes, pdt, gdt, sdt, steps=4, seed=31, threads=1, check_wor
             dev.hip_step(st, group, [g.cuda() for g in grads], s)
             torch.cuda.synchronize()
             host.assert_equal(dev, f"{label} step {s}")
-            if check_workspace:
+            if check_workspace:  # every call leaves the whole workspace zero, radial records included
                 for ws in st.workspace._bufs.values():
-                    assert int(torch.count_nonzero(ws[:WORKSPACE_ZERO_BYTES])) == 0, f"{label} step {s}: words left set"
+                    nz = int(torch.count_nonzero(ws))
+                    assert nz == 0, f"{label} step {s}: {nz} workspace bytes left set"
     return host
 
 
@@ -139,6 +137,10 @@ def test_radial_is_deterministic(oracle_mod):
 
 # differential_parity.rs: 131,072 elements, 5 steps, the reference's own configurations
 REF_N, REF_STEPS, REF_TOL = 131_072, 5, 1.5e-6
+# Relative error of fp32 p is taken against max(|p|, REL_FLOOR): the radial scale's summation
+# error moves p by at most lr * |u| * |scale error|, an absolute quantity, so relative error is
+# meaningless for p near zero; 1e-3 is the learning rate of these configurations (one step's size).
+REL_FLOOR = 1e-3
 REF_CONFIGS = [
     # label, buffer, lr, seed, dtype, state dtype, init seed, grad seed base
     ("tdclm_fp32", 1, 1e-3, 1337, "f32", "f32", 42, 1000),   # differential_parity.rs:80-98
@@ -183,6 +185,12 @@ def test_radial_reference_configs_within_reference_tolerance(oracle_mod, label, 
         ph, pd = p_h.float(), p_d.cpu().float()
         if pdt == "f32":
             assert float((ph - pd).abs().max()) <= REF_TOL, f"{label} step {s}"
+            # the north star's per-element bound: 1e-6 relative, with |p| floored at REL_FLOOR
+            rel = ((ph - pd).abs() / ph.abs().clamp_min(REL_FLOOR)).double()
+            k = int(rel.argmax())
+            print(f"[radial] {label} step {s}: max rel {float(rel[k]):.3e} at |p| = {abs(float(ph[k])):.3e}, "
+                  f"max abs {float((ph - pd).abs().max()):.3e}", flush=True)
+            assert float(rel[k]) <= 1e-6, f"{label} step {s}: element {k} rel {float(rel[k]):.3e}"
         else:
             bh, bd = bits(p_h), bits(p_d)
             off = np.abs(bh - bd)

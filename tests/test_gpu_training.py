@@ -257,3 +257,44 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     opt.param_groups[0]["master_weights"] = "full"  # the state layout changes: slow path, new plan
     run(13, "new", False)
     run(14, "new", True)
+    # a state entry replaced by a new tensor of the same values (what device-moving helpers do,
+    # state[k] = v.to(device)): the plan is dropped, and the new tensor is the one stepped
+    st0 = opt.state[params[0]]
+    st0["exp_avg"] = st0["exp_avg"].clone()
+    run(15, "new", False)
+    run(16, "new", True)
+    # a parameter's whole state dict replaced (opt.state[p] = {...})
+    opt.state[params[1]] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in opt.state[params[1]].items()}
+    run(17, "new", False)
+    run(18, "new", True)
+    # the optimizer's state map replaced wholesale
+    from collections import defaultdict
+
+    opt.state = defaultdict(dict, {k: dict(v) for k, v in opt.state.items()})
+    run(19, "new", False)
+    run(20, "new", True)
+
+
+def test_unfused_duplicate_param_raises_like_the_native_seam():
+    """LuminaV([w, w]) unfused lists one tensor twice. The reference's native seam rejects it
+    (step_pyo3: "Pointer aliasing detected", python_ffi/mod.rs:141-147); here the C ABI does the
+    same before any launch, step() raises ValueError, and neither the parameter nor its step
+    counter moves. (Fused buckets keep one slice per tied weight instead.)"""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import warnings
+
+    from luminamoon_amd import LuminaV
+
+    w = torch.nn.Parameter(torch.randn(5000, device="cuda") * 0.02)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")  # torch warns about duplicate parameters in a group
+        opt = LuminaV([w, w], lr=1e-3, buffer="T2")
+    w.grad = torch.randn_like(w) * 1e-3
+    before = w.detach().clone()
+    print("[case] unfused duplicate parameter", flush=True)
+    with pytest.raises(ValueError, match="Pointer aliasing detected"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(w.detach(), before)
+    assert int(opt.state[w]["step"]) == 0

@@ -33,6 +33,14 @@ MUTATIONS = {
     "radial_norm_ignores_cautious_mask": ("float u_eff = k->cautious ? u * (active ? 1.0f : 0.0f) : u;",
                                           "float u_eff = u; (void)active;"),
     "radial_norm_uses_updated_param": ("*p_sq_out = p_init * p_init;", "*p_sq_out = p_upd * p_upd;"),
+    # v clamp keyed on the raw fp16 state container instead of the worker's promoted mode
+    "v_clamp_on_fp16_state_container": ("p_mode, s_mode, threads,\n                   it->index_base);",
+                                        "p_mode, it->state_dtype, threads,\n                   it->index_base);"),
+    # the fp16 safety bound with the other mode's form, or with a different floor
+    "fp16_safety_tanh_form_swapped": ("    float b = fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);\n    return b * lvo_tanh_pade(step / b);",
+                                      "    float b = fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);\n    float bb = b * (b + fabsf(step));\n    return (bb * step) / fmaf(step, step, bb);"),
+    "fp16_safety_floor_1e4": ("float lvo_fp16_safety_bound_t2(float step, float p_init) {\n    float b = fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);",
+                              "float lvo_fp16_safety_bound_t2(float step, float p_init) {\n    float b = fmaxf(fabsf(p_init) * 0.01f, 1.0e-4f);"),
 }
 
 

@@ -383,6 +383,60 @@ def test_coordinate_bounds_are_bounded_and_tangent(oracle_mod):
             assert abs(L.lvo_fp16_safety_bound_t2(s, p)) <= b * (1 + 1e-6)
 
 
+def test_fp16_safety_bounds_closed_form_per_mode(oracle_mod):
+    """apply_fp16_safety_bound{,_t2} (math.rs:175-186): b = max(|p| * 0.01, 1.5e-4), then the
+    tanh form b * tanh(s / b) for TD-CLM/CLM and the rational form b(b+|s|) s / (s^2 + b(b+|s|))
+    for the triangle family. At |s| = b the two forms differ by 12% (0.762 b vs 0.667 b), and a
+    different floor or scale moves b, so swapped forms or a wrong b fail here."""
+    L = oracle_mod.lib()
+    for p in (0.0, 1e-3, -0.015, 0.02, 3.0, -250.0):
+        b = max(abs(p) * 0.01, 1.5e-4)
+        for s in (b * 1e-3, -0.5 * b, b, -2.0 * b, 7.5 * b, 1e3 * b):
+            t = L.lvo_fp16_safety_bound(s, p)
+            r = L.lvo_fp16_safety_bound_t2(s, p)
+            bb = b * (b + abs(s))
+            assert abs(t - b * math.tanh(s / b)) <= 2e-6 * b, (p, s, t)
+            assert abs(r - bb * s / (s * s + bb)) <= 2e-6 * b, (p, s, r)
+            assert math.copysign(1, t) == math.copysign(1, s) == math.copysign(1, r)
+    # at |s| = b the tanh form is tanh(1) b and the rational one 2/3 b
+    assert abs(L.lvo_fp16_safety_bound(1.5e-4, 0.0) - math.tanh(1.0) * 1.5e-4) <= 1e-10
+    assert abs(L.lvo_fp16_safety_bound_t2(1.5e-4, 0.0) - 1.0e-4) <= 1e-10
+
+
+@pytest.mark.parametrize("buffer", [2, "T2"])
+def test_v_clamp_follows_the_param_dtype_only(oracle_mod, buffer):
+    """The v <= 65000 clamp of the dual-state modes (dual.rs:68-71, dual.rs:160-163) tests
+    view.dtype_mode == Float16 || view.state_dtype_mode == Float16. The FFI worker builds that view
+    with eff_state_dtype_mode, which maps an fp16 state container to BFloat16 before the core runs
+    (worker.rs:107-113 and the view at worker.rs:141-150), so on the reference's native path the
+    clamp follows the param dtype alone: a bf16 (or fp32) param with an fp16 state container is
+    not clamped, an fp16 param is."""
+    O = oracle_mod
+    n = 256
+    cfg = O.make_config(lr=1e-3, buffer=buffer, cautious=False, stochastic_rounding=False)
+    g = torch.full((n,), 1.0e4)  # d^2 = 1e8, so v_new = (1 - beta2) * 1e8 = 1e5 > 65000
+    g[1::2] = -1.0e4
+    for pdt, clamped in ((torch.bfloat16, False), (torch.float32, False), (torch.float16, True)):
+        p = (torch.arange(n, dtype=torch.float32) * 1e-3).to(pdt)
+        m = torch.zeros(n, dtype=torch.float16)  # fp16 containers holding bf16 bits
+        v = torch.zeros(n, dtype=torch.float16)
+        sc = torch.tensor([0, 0, 0, 1, 1, 0], dtype=torch.float32)
+        O.step(cfg, [p], [g.to(pdt)], [m], [v], [None], [sc], [1], [0], dtypes=[(
+            {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[pdt],) * 2 + (2,)])
+        vv = v.view(torch.bfloat16).float()
+        assert torch.isfinite(vv).all()
+        # unclamped v_new in f32: d = g - m_new (CLM) or g - m (T2) with m = 0, v = (1 - b2) * d^2
+        b1, omb2 = np.float32(0.9), np.float32(1.0) - np.float32(0.999)
+        gf = np.float32(1.0e4)
+        d = gf - (np.float32(1.0) - b1) * gf if buffer == 2 else gf
+        want = float(torch.tensor(float(omb2 * (d * d))).to(torch.bfloat16))  # RNE, SR off
+        assert want > 65000.0
+        if clamped:
+            assert torch.equal(vv, torch.full((n,), 65024.0)), pdt  # min(v, 65000) rounded to bf16
+        else:
+            assert torch.equal(vv, torch.full((n,), want)), (pdt, vv[:4], want)
+
+
 # --------------------------------------------------------------------------- whole step
 
 def _f64_step(mode, p, g, m, v, step, lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, wd=0.08, tau=0.8, lam=0.3, ratio=0.05,
