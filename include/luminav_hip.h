@@ -134,6 +134,21 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count,
                   void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * lv_step_multi without allocation: no counterpart in the reference. For callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments, validation, launches and results (bit for bit) as
+ * lv_step_multi, with no workspace argument: it uses a scratch array the library holds on each
+ * device (1,514,496 bytes, kept until the process ends) and calls no allocating routine.
+ * Limits, refused with LV_STATUS_INVALID_CONFIG: at most 256 tensors per call, and radial-bound
+ * counting launches of at most 65,536 work units (about 67M elements with fp32 state). Classes
+ * above 48 tensors run as several inline launches (no descriptor tables). Every call on a device
+ * shares that device's array: calls that overlap in time on one device (two streams, two host
+ * threads) race and must not be issued; stream-ordered calls are fine. Each call leaves the array
+ * zero; after a call that failed part-way the next call clears it first.
+ */
+int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int count, void *stream);
+
+/*
  * Single fp32 tensor step with luminav_triton_step_f32's argument mapping
  * (optimizer/crates/luminav-triton-aot/src/c_api.rs:108-199): buffer_mode 1 is TD-CLM and every
  * other value the dual buffer (c_api.rs:143-146); exp_avg_sq is used only when buffer_mode == 2

@@ -145,15 +145,14 @@ static int validate_config(const lv_config *c) {
 // XCDs of the current device (hipDeviceAttributeNumberOfXccs; 1 if unknown).
 static uint32_t device_xcds() {
     static std::mutex mu;
-    static std::vector<std::pair<int, uint32_t>> cache;
+    static uint32_t cache[64] = {0};  // per device; 0 = not queried yet (no allocation here)
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     std::lock_guard<std::mutex> lk(mu);
-    for (const auto &e : cache)
-        if (e.first == dev) return e.second;
+    if (cache[dev]) return cache[dev];
     int x = 0;
     if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x < 1 || x > 64) x = 1;
-    cache.push_back({dev, (uint32_t)x});
+    cache[dev] = (uint32_t)x;
     return (uint32_t)x;
 }
 
@@ -301,7 +300,7 @@ static_assert(kSlotBytes % 256 == 0 && kRunBytes % 256 == 0, "region alignment")
 static_assert(kMaxDesc * sizeof(unsigned long long) <= kTicketBytes, "ticket region");
 static_assert(sizeof(RadialSum) == 32, "radial record layout");
 
-static size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
     unsigned long long *slots = nullptr;   // inline count slots
@@ -315,12 +314,12 @@ struct Layout {
     bool radial_split = true;    // a radial launch above radial_units runs in pieces (else: refused)
 };
 
-static size_t chunk_bytes(uint32_t radial_units) {
+constexpr size_t chunk_bytes(uint32_t radial_units) {
     return radial_units ? round256(((size_t)(radial_units + kFoldChunk - 1) / kFoldChunk + kMaxDesc) * sizeof(RadialSum))
                         : 0;
 }
 
-static size_t layout_bytes(uint64_t table_slots, uint32_t radial_units) {
+constexpr size_t layout_bytes(uint64_t table_slots, uint32_t radial_units) {
     return kSlotBytes + kTicketBytes + kRunBytes + chunk_bytes(radial_units) +
            round256(table_slots * kSlotStride * sizeof(unsigned long long)) + (size_t)radial_units * 16u +
            round256((size_t)radial_units * 4u);
@@ -838,6 +837,33 @@ static int step_f32_device(OwnedWorkspace &ws, float *param, const float *grad, 
     return rc == LV_STATUS_SUCCESS || rc == LV_STATUS_NULL_POINTER ? rc : LV_STATUS_EXECUTION_FAILED;
 }
 
+// ------------------------------------------------------------------ no-allocation entry point
+
+// lv_step_multi_noalloc's workspace: inline count slots for 48 tensors per launch and radial
+// records for launches of up to kNoAllocRadialUnits units (one piece, so its radial sums follow
+// the same summation tree as lv_step_multi's). No table slots: classes above 48 tensors run as
+// several inline launches, which give the same bits. One copy per device, zero at load; every
+// call leaves it zero again, and a call that failed part-way marks it for a clearing kernel
+// before the next call.
+constexpr uint32_t kNoAllocRadialUnits = 1u << 16;
+constexpr int kNoAllocMaxTensors = 256;
+constexpr size_t kNoAllocBytes = layout_bytes(0, kNoAllocRadialUnits);
+static_assert(kNoAllocBytes == 1514496, "no-allocation scratch size");
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+__global__ void __launch_bounds__(kThreads) zero_fill(uint4 *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (size_t)gridDim.x * kThreads)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+struct NoAllocScratch {
+    std::mutex mu;
+    void *ptr[64] = {nullptr};  // `scratch` on each device (hipGetSymbolAddress)
+    bool dirty[64] = {false};   // a call failed part-way: clear before the next one
+};
+static NoAllocScratch g_noalloc;
+
 }  // namespace lv
 
 // The reference's standalone engine handle (luminav_triton_standalone.h:21-22): a device, a stream
@@ -900,6 +926,54 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     if (rc != LV_STATUS_SUCCESS || nitems == 0) return rc;
     const Layout L = make_layout(static_cast<char *>(workspace), tslots, runits);
     return run_call(cfg, tensors, items.data(), nitems, L, static_cast<hipStream_t>(stream_ptr));
+}
+
+int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int count, void *stream_ptr) {
+    using namespace lv;
+    g_err[0] = 0;
+    if (!cfg) return fail(LV_STATUS_NULL_POINTER, "config is NULL");
+    if (count < 0) return fail(LV_STATUS_INVALID_CONFIG, "negative tensor count");
+    if (count == 0) return LV_STATUS_SUCCESS;
+    if (!tensors) return fail(LV_STATUS_NULL_POINTER, "tensor list is NULL");
+    if (count > kNoAllocMaxTensors)
+        return fail(LV_STATUS_INVALID_CONFIG, "%d tensors exceed the %d of lv_step_multi_noalloc (use lv_step_multi)",
+                    count, kNoAllocMaxTensors);
+    int rc = validate_config(cfg);
+    if (rc != LV_STATUS_SUCCESS) return rc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(LV_STATUS_NO_DRIVER, "no HIP device");
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    char *ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc.mu);
+        if (!g_noalloc.ptr[dev]) {
+            void *p = nullptr;
+            // with this device current: its own copy of the array
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+                return fail(LV_STATUS_EXECUTION_FAILED, "cannot resolve the no-allocation scratch on device %d", dev);
+            g_noalloc.ptr[dev] = p;
+        }
+        ws = static_cast<char *>(g_noalloc.ptr[dev]);
+        if (g_noalloc.dirty[dev]) {
+            hipLaunchKernelGGL(zero_fill, dim3(64), dim3(kThreads), 0, stream, reinterpret_cast<uint4 *>(ws),
+                               kNoAllocBytes / sizeof(uint4));
+            if (hipGetLastError() != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "scratch clearing failed");
+            g_noalloc.dirty[dev] = false;
+        }
+    }
+    Item items[kNoAllocMaxTensors];
+    Span spans[kNoAllocMaxTensors * 5];
+    int nitems = 0;
+    rc = prepare_call(cfg, tensors, count, items, nitems, spans);
+    if (rc != LV_STATUS_SUCCESS || nitems == 0) return rc;
+    Layout L = make_layout(ws, 0, kNoAllocRadialUnits);
+    L.radial_split = false;
+    rc = run_call(cfg, tensors, items, nitems, L, stream);
+    if (rc == LV_STATUS_EXECUTION_FAILED) {
+        std::lock_guard<std::mutex> lk(g_noalloc.mu);
+        g_noalloc.dirty[dev] = true;
+    }
+    return rc;
 }
 
 int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq, float *master_param,

@@ -71,7 +71,8 @@ class LvTensor(ctypes.Structure):
 
 
 EXPORTED_SYMBOLS = (
-    "lv_version", "lv_workspace_bytes", "lv_workspace_bytes_for", "lv_step_multi", "lv_step_f32", "lv_last_error",
+    "lv_version", "lv_workspace_bytes", "lv_workspace_bytes_for", "lv_step_multi", "lv_step_multi_noalloc",
+    "lv_step_f32", "lv_last_error",
     # the reference's standalone C API (luminav_triton_standalone.h:37-111)
     "luminav_triton_engine_create", "luminav_triton_engine_destroy", "luminav_triton_get_platform",
     "luminav_triton_get_arch", "luminav_triton_step_f32",
@@ -108,6 +109,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
             ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
             ctypes.c_void_p,
         ]
+        L.lv_step_multi_noalloc.restype = ctypes.c_int
+        L.lv_step_multi_noalloc.argtypes = [ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int,
+                                            ctypes.c_void_p]
         f, P = ctypes.c_float, ctypes.c_void_p
         L.lv_step_f32.restype = ctypes.c_int
         L.lv_step_f32.argtypes = [P, P, P, P, P, P, ctypes.c_size_t, f, f, f, f, f, f, f, ctypes.c_int, ctypes.c_int,
