@@ -197,11 +197,15 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
 
     def make(n, seed=5):
         # a 2^24-value random block repeated over the sample: the same value mix at any size, and
-        # generating a billion normals would take longer than the timed steps
+        # generating a billion draws would take longer than the timed steps. Grads follow the
+        # workload's distribution (1e-3 * t(df=3) for cfg5, 1e-3 * N(0,1) otherwise, 5% zeros for cfg2).
         rng = np.random.default_rng(seed)
         k = min(n, 1 << 24)
         p = torch.from_numpy(np.resize((rng.standard_normal(k) * 0.02).astype(np.float32), n)).to(pdt)
-        g = torch.from_numpy(np.resize((rng.standard_normal(k) * 1e-3).astype(np.float32), n)).to(pdt)
+        z = rng.standard_t(3, k) if workload["grad"] == "student_t3" else rng.standard_normal(k)
+        if workload["grad"] == "normal_zeros":
+            z[rng.random(k) < 0.05] = 0.0
+        g = torch.from_numpy(np.resize((z * 1e-3).astype(np.float32), n)).to(pdt)
         m = torch.zeros(n, dtype=sdt)
         v = torch.zeros(n, dtype=sdt) if dual else None
         mp = p.float().clone() if master else None
@@ -227,6 +231,7 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
             "sample": f"the whole workload: {k} tensors, {n} elements (median of 10 steady steps, "
                       f"{t * 1e3:.2f} ms/step), {threads} threads",
             "gb_per_s": n * workload["bytes_per_param"] / t / 1e9,
+            "grads": workload["grad"],
         }
 
     # calibrate on 2^25 elements (16 chunks: memory-bound like the full size), then size the timed
@@ -265,7 +270,49 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
         "sample": f"{n} elements of the same workload (median of 3 steady steps, {t * 1e3:.1f} ms/step), "
                   f"{threads} threads on '{cpu_model}'",
         "gb_per_s": n * workload["bytes_per_param"] / t / 1e9,
+        "grads": workload["grad"],
     }
+
+
+def cpu_threads() -> dict:
+    """Threads for the CPU baseline: os.cpu_count() (BASELINE.md's rule), lowered to what this
+    process may actually use -- its CPU affinity, the cgroup CPU quota, and the host share the GPU
+    box grants one GPU (OMP_NUM_THREADS, which the box sets) -- each stated in the result, with
+    the host's logical CPUs and physical cores reported separately."""
+    host = os.cpu_count() or 1
+    limits = {"os.cpu_count": host}
+    try:
+        limits["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            limits["cgroup cpu.max"] = max(1, math.ceil(int(quota) / int(period)))
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        limits["OMP_NUM_THREADS"] = int(omp)
+    threads = min(limits.values())
+    physical = set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            pid = cid = None
+            for line in f:
+                if line.startswith("physical id"):
+                    pid = line.split(":", 1)[1].strip()
+                elif line.startswith("core id"):
+                    cid = line.split(":", 1)[1].strip()
+                elif not line.strip() and pid is not None:
+                    physical.add((pid, cid))
+                    pid = cid = None
+    except OSError:
+        pass
+    binding = min(limits, key=limits.get)
+    return {"threads": threads, "host_cpus": host, "physical_cores": len(physical) or None,
+            "limited_by": binding, "limits": limits}
 
 
 def main() -> int:
@@ -376,9 +423,16 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
-        log(f"timing the CPU oracle with {threads} threads")
+        ct = cpu_threads()
+        threads = args.cpu_threads or ct["threads"]
+        log(f"timing the CPU oracle with {threads} threads (host: {ct['host_cpus']} CPUs, "
+            f"{ct['physical_cores']} physical cores; limits {ct['limits']})")
         cpu = cpu_baseline(wl, threads)
+        cpu["host_cpus"] = ct["host_cpus"]
+        cpu["physical_cores"] = ct["physical_cores"]
+        cpu["thread_limits"] = ct["limits"]
+        cpu["sample"] += (f"; threads = min({', '.join(f'{k} {v}' for k, v in ct['limits'].items())})"
+                          if not args.cpu_threads else f"; threads set by --cpu-threads")
 
     out = {
         "metric": "optimizer params updated/sec + achieved HBM GB/s (% of peak), 1 MI355X",

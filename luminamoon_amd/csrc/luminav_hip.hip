@@ -42,6 +42,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstddef>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -614,6 +615,14 @@ static int launch_class(Args &args, const lv_config *cfg, const Item &h, hipStre
     return launch(args, cfg->buffer, h.pt, h.st, h.pass, stream, table, radial_piece);
 }
 
+// An item's step count and first pass: dual.rs:52, dual.rs:122, dual.rs:260; tdclm.rs:67-68.
+static void set_step(Item &it, const lv_config *cfg, int bound, uint64_t step) {
+    it.step = step;
+    if (!cfg->cautious && bound != LV_BOUND_RADIAL) it.pass = kSingle;
+    else if (cfg->fused_single_pass && step > 1) it.pass = kFused;
+    else it.pass = kCount;
+}
+
 // Validates a call and forms its items (tensors with elements), in the caller's order.
 // `items` has room for `count` entries and `spans` for 5 per entry.
 static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int count, Item *items, int &nitems,
@@ -646,11 +655,7 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
         it.gt = T.grad_dtype;
         it.st = T.state_dtype == LV_DTYPE_F32 ? LV_DTYPE_F32 : LV_DTYPE_BF16;  // fp16 state -> bf16 bits (worker.rs:107-113)
         it.master = master;
-        it.step = T.step;
-        // dual.rs:52, dual.rs:122, dual.rs:260; tdclm.rs:67-68
-        if (!cfg->cautious && bound != LV_BOUND_RADIAL) it.pass = kSingle;
-        else if (cfg->fused_single_pass && T.step > 1) it.pass = kFused;
-        else it.pass = kCount;
+        set_step(it, cfg, bound, T.step);
         items[nitems++] = it;
     }
     return check_aliasing(tensors, items, nitems, spans);
@@ -661,22 +666,22 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
 // slots (radial counting classes stay inline: their fold walks the launch's tensor list), else
 // inline launches of up to kMaxDesc tensors.
 static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items, int nitems, const Layout &L,
-                    hipStream_t stream) {
+                    hipStream_t stream, std::vector<TDesc> *tab_buf) {
     const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;
     std::sort(items, items + nitems, item_less);
-    std::vector<TDesc> tab;
     for (int begin = 0; begin < nitems;) {
         const Item &h = items[begin];
         int cls_end = begin + 1;
         while (cls_end < nitems && same_class(items[cls_end], h)) cls_end++;
         const uint32_t unit_elems = kHalf * unit_halves(cfg->buffer, h.pt, h.st);
         const bool radial = bound == LV_BOUND_RADIAL && h.pass != kSingle;
-        const bool table = !radial && L.table_slots > 0 && cls_end - begin > kMaxDesc;
+        const bool table = !radial && L.table_slots > 0 && tab_buf && cls_end - begin > kMaxDesc;
         if (table) {
             const int n = cls_end - begin;
             Args args;
             fill_args_common(args, cfg, h, bound);
-            tab.resize((size_t)n);
+            std::vector<TDesc> &tab = *tab_buf;
+            if (tab.size() < (size_t)n) tab.resize((size_t)n);
             uint64_t units = 0, slot = 0;
             for (int k = 0; k < n; k++) {
                 const lv_tensor &T = tensors[items[begin + k].idx];
@@ -744,6 +749,44 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
     }
     return LV_STATUS_SUCCESS;
 }
+
+// lv_step_multi's host scratch, one per thread, grown on demand and reused (no allocation per
+// call in the steady state), and the last call it validated: a call whose config and tensors
+// (every field but the step counters, which only set the passes) are byte for byte those of that
+// call takes its items without validating again. Validation depends on nothing else.
+struct CallScratch {
+    std::vector<Item> items;
+    std::vector<Span> spans;
+    std::vector<TDesc> tab;
+    std::vector<lv_tensor> last;  // step fields zeroed
+    std::vector<Item> last_items;
+    lv_config last_cfg;
+    int last_nitems = -1;
+
+    static bool same_but_step(const lv_tensor &a, const lv_tensor &b) {
+        constexpr size_t s0 = offsetof(lv_tensor, step), s1 = s0 + sizeof(uint64_t);
+        const char *x = reinterpret_cast<const char *>(&a), *y = reinterpret_cast<const char *>(&b);
+        return std::memcmp(x, y, s0) == 0 && std::memcmp(x + s1, y + s1, sizeof(lv_tensor) - s1) == 0;
+    }
+
+    bool same_as_last(const lv_config *cfg, const lv_tensor *t, int count) const {
+        if (last_nitems < 0 || last.size() != (size_t)count || std::memcmp(&last_cfg, cfg, sizeof *cfg) != 0) return false;
+        for (int i = 0; i < count; i++)
+            if (!same_but_step(last[(size_t)i], t[i])) return false;
+        return true;
+    }
+
+    void remember(const lv_config *cfg, const lv_tensor *t, int count, int nitems) {
+        last.assign(t, t + count);
+        for (lv_tensor &x : last) x.step = 0;
+        last_items.assign(items.begin(), items.begin() + nitems);
+        last_cfg = *cfg;
+        last_nitems = nitems;
+    }
+};
+static thread_local CallScratch t_call;
+static_assert(sizeof(lv_config) == 18 * 4, "lv_config has no padding (compared with memcmp)");
+static_assert(sizeof(lv_tensor) == 112, "lv_tensor layout (compared with memcmp)");
 
 // The configuration luminav_triton_step_f32 builds from its arguments (c_api.rs:143-176).
 static void f32_config(lv_config &c, float lr, float beta1, float beta2, float eps, float weight_decay, float tau,
@@ -828,7 +871,7 @@ static int step_f32_device(OwnedWorkspace &ws, float *param, const float *grad, 
     int rc = prepare_call(&c, &t, 1, &it, nitems, spans);
     if (rc == LV_STATUS_SUCCESS && nitems) {
         Layout L = make_layout(static_cast<char *>(ws.p), tslots, runits);
-        rc = run_call(&c, &t, &it, nitems, L, stream);
+        rc = run_call(&c, &t, &it, nitems, L, stream, nullptr);
         if (rc == LV_STATUS_EXECUTION_FAILED) {
             // a launch failed part-way: its count words may hold partial counts; start clean
             if (hipStreamSynchronize(stream) == hipSuccess) (void)hipMemset(ws.p, 0, ws.bytes);
@@ -919,13 +962,29 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     if (workspace_bytes < need)
         return fail(LV_STATUS_INVALID_CONFIG, "workspace too small: %zu < %zu (lv_workspace_bytes_for)", workspace_bytes,
                     need);
-    std::vector<Item> items((size_t)count);
-    std::vector<Span> spans((size_t)count * 5);
+    CallScratch &cs = t_call;
+    if (cs.items.size() < (size_t)count) cs.items.resize((size_t)count);
     int nitems = 0;
-    rc = prepare_call(cfg, tensors, count, items.data(), nitems, spans.data());
-    if (rc != LV_STATUS_SUCCESS || nitems == 0) return rc;
+    if (cs.same_as_last(cfg, tensors, count)) {
+        // validated before: the items again, with this call's step counters
+        const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;
+        nitems = cs.last_nitems;
+        for (int k = 0; k < nitems; k++) {
+            cs.items[(size_t)k] = cs.last_items[(size_t)k];
+            set_step(cs.items[(size_t)k], cfg, bound, tensors[cs.items[(size_t)k].idx].step);
+        }
+    } else {
+        if (cs.spans.size() < (size_t)count * 5) cs.spans.resize((size_t)count * 5);
+        rc = prepare_call(cfg, tensors, count, cs.items.data(), nitems, cs.spans.data());
+        if (rc != LV_STATUS_SUCCESS) {
+            cs.last_nitems = -1;
+            return rc;
+        }
+        cs.remember(cfg, tensors, count, nitems);
+    }
+    if (nitems == 0) return LV_STATUS_SUCCESS;
     const Layout L = make_layout(static_cast<char *>(workspace), tslots, runits);
-    return run_call(cfg, tensors, items.data(), nitems, L, static_cast<hipStream_t>(stream_ptr));
+    return run_call(cfg, tensors, cs.items.data(), nitems, L, static_cast<hipStream_t>(stream_ptr), &cs.tab);
 }
 
 int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int count, void *stream_ptr) {
@@ -968,7 +1027,7 @@ int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int co
     if (rc != LV_STATUS_SUCCESS || nitems == 0) return rc;
     Layout L = make_layout(ws, 0, kNoAllocRadialUnits);
     L.radial_split = false;
-    rc = run_call(cfg, tensors, items, nitems, L, stream);
+    rc = run_call(cfg, tensors, items, nitems, L, stream, nullptr);
     if (rc == LV_STATUS_EXECUTION_FAILED) {
         std::lock_guard<std::mutex> lk(g_noalloc.mu);
         g_noalloc.dirty[dev] = true;

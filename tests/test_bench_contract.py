@@ -85,3 +85,33 @@ def test_cpu_baseline_reports_its_fields():
     assert out["value"] > 0 and out["gb_per_s"] > 0
     assert "elements of the same workload" in out["sample"]
     assert "AVX-512" in out["sample"] or "scalar core" in out["sample"]
+
+
+def test_cpu_threads_follow_the_host_limits(monkeypatch):
+    """The CPU baseline uses os.cpu_count() threads unless this process may use fewer (affinity,
+    cgroup quota, the box's OMP_NUM_THREADS share), and reports which limit decided, next to the
+    host's logical CPUs and physical cores."""
+    import os
+
+    import bench
+
+    monkeypatch.delenv("OMP_NUM_THREADS", raising=False)
+    ct = bench.cpu_threads()
+    assert ct["host_cpus"] == os.cpu_count()
+    assert 1 <= ct["threads"] <= os.cpu_count()
+    assert ct["threads"] == min(ct["limits"].values()) and ct["limits"]["os.cpu_count"] == os.cpu_count()
+    monkeypatch.setenv("OMP_NUM_THREADS", "3")
+    ct = bench.cpu_threads()
+    assert ct["threads"] == min(3, os.cpu_count()) and ct["limits"]["OMP_NUM_THREADS"] == 3
+    if os.cpu_count() > 3:
+        assert ct["limited_by"] == "OMP_NUM_THREADS"
+
+
+def test_cpu_baseline_draws_student_t_grads_for_cfg5():
+    """cfg5's sample grads are 1e-3 * t(df=3), like the GPU workload's."""
+    import bench
+
+    wl = bench.workload(5)
+    assert wl["grad"] == "student_t3"
+    out = bench.cpu_baseline(wl, threads=2, target_s=0.3)
+    assert out["grads"] == "student_t3" and out["value"] > 0

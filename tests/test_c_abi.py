@@ -313,3 +313,26 @@ def test_xcd_block_mapping_is_exact_and_bijective():
             q, r = G // X, G % X
             unit = x * q + np.minimum(x, r) + i.astype(np.int64)
             assert np.array_equal(np.sort(unit), bb), (X, G)
+
+
+def test_validation_cache_never_hides_a_changed_call(lib):
+    """lv_step_multi skips validation for a call equal, byte for byte except the step counters, to
+    the last validated one on the thread. Any other change is validated again: a valid call (here
+    stopped at its launch, with no device) followed by the same call with an aliased pointer is
+    rejected, and the valid call again goes back to its launch."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("launches fake pointers when valid: host-only test")
+    cfg = _cfg(buffer="T2")
+    ts = _tensors([100, 200, 300])
+    assert _run(lib, cfg, ts) == -4  # validated, then the launch fails without a device
+    ts[2].step = 7                    # the step counters alone: same validation
+    assert _run(lib, cfg, ts) == -4
+    ts[2].grad = ts[0].param          # aliasing: validated again and rejected
+    assert _run(lib, cfg, ts) == -3 and ALIAS in lib.lv_last_error()
+    ts = _tensors([100, 200, 300])
+    assert _run(lib, cfg, ts) == -4
+    cfg2 = _cfg(buffer="T2", master_weights="full")  # a config change is validated again
+    ts[0].param_dtype = ts[0].grad_dtype = 1
+    assert _run(lib, cfg2, ts) == -1 and b"master_param" in lib.lv_last_error()
