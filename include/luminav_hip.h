@@ -134,6 +134,33 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count,
                   void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Graph-capture-safe stepping (the reference keeps per-parameter scratch pointers stable for CUDA
+ * graph capture, changelogs/LUMINAV_ALGORITHM_CHANGELOG.md:283-284; its kernels still take the
+ * step count and coefficients as launch arguments). lv_step_multi_graph takes the step count
+ * from a caller-owned record in DEVICE memory instead: each call first advances record->step on
+ * the device and writes that step's bias-correction coefficients and seed base into the record
+ * (a one-thread kernel, the same f64 arithmetic as the host path), then runs lv_step_multi's
+ * launches reading them from there. So a HIP graph captured around a call replays one correct
+ * step per replay. The call uses inline launches only (no descriptor upload, no event, no memset,
+ * no allocation); the tensors' `step` fields are ignored: every tensor of the call shares the
+ * record's count. Passes are those of a step >= 2: with cautious or radial and the fused single
+ * pass, a first step (record->step == 0 before the call) is refused on the device (status 1, the
+ * counter and every buffer unchanged); take it through lv_step_multi and set record->step to 1.
+ * Results are bit for bit lv_step_multi's for the same step counts. Workspace: as lv_step_multi
+ * without table count slots.
+ */
+typedef struct lv_step_record {
+    uint64_t step;          /* steps taken; each call adds one on the device before stepping */
+    float c1, c2, c_sigma;  /* written by each call: its step's coefficients (math.rs:27-81) */
+    uint32_t seed_base;     /* written by each call: seed + step * 0x9E3779B9 (prng.rs:4-13) */
+    uint32_t status;        /* 0, or 1 when the last call refused a first step */
+    uint32_t reserved;
+} lv_step_record;
+
+int lv_step_multi_graph(const lv_config *cfg, const lv_tensor *tensors, int count, lv_step_record *record,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * lv_step_multi without allocation: no counterpart in the reference. For callers that cannot
  * allocate device memory -- code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc. Same arguments, validation, launches and results (bit for bit) as

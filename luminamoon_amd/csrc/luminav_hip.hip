@@ -84,39 +84,6 @@ static int fail(int code, const char *fmt, ...) {
     return code;
 }
 
-// compiler-builtins' __powidf2 (the lowering of Rust f64::powi): repeated squaring.
-static double powi_rs(double a, int32_t b) {
-    bool recip = b < 0;
-    uint32_t pw = recip ? (uint32_t)(-(int64_t)b) : (uint32_t)b;
-    double mul = 1.0;
-    for (;;) {
-        if (pw & 1u) mul *= a;
-        pw >>= 1;
-        if (pw == 0) break;
-        a *= a;
-    }
-    return recip ? 1.0 / mul : mul;
-}
-
-struct StepCoeffs {
-    float c1, c2, c_sigma;
-};
-
-// math.rs:27-81
-static StepCoeffs step_coeffs(uint64_t step, float beta1, float beta2, float eps, float tau, float lam) {
-    uint64_t safe = step > 1 ? step : 1;
-    double b1 = (double)beta1, b2 = (double)beta2;
-    double bc1 = safe < 2147483647ull ? 1.0 - powi_rs(b1, (int32_t)(safe + 1)) : 1.0 - std::pow(b1, (double)(safe + 1));
-    double bc2_raw = safe <= 2147483647ull ? 1.0 - powi_rs(b2, (int32_t)safe) : 1.0 - std::pow(b2, (double)safe);
-    double bc2 = std::fmax(bc2_raw, 1.0e-15);
-    StepCoeffs c;
-    c.c1 = (float)((bc1 * (double)tau) / std::sqrt(bc2));
-    c.c2 = (float)((double)eps * bc1 * (double)tau);
-    float bc2f = (float)bc2;
-    c.c_sigma = (0.5f * lam) / std::sqrt(std::fmax(bc2f, 1.0e-15f));
-    return c;
-}
-
 static int validate_config(const lv_config *c) {
     auto fin = [](float x) { return std::isfinite(x); };
     if (!fin(c->lr) || c->lr < 0.0f) return fail(LV_STATUS_INVALID_CONFIG, "Invalid learning rate: %g", c->lr);
@@ -588,7 +555,7 @@ static void fill_args_common(Args &args, const lv_config *cfg, const Item &h, in
     args.ema = cfg->ema_decay;
     args.ema_c = 1.0f - cfg->ema_decay;
     args.clamp_min = cfg->cautious_clamp_min;
-    args.seed_base = (uint32_t)((uint64_t)cfg->seed + h.step * 0x9E3779B9ull);
+    args.seed_base = step_seed_base(cfg->seed, h.step);
     uint32_t flags = 0;
     if (cfg->cautious) flags |= kFCautious;
     if (cfg->stochastic_rounding) flags |= kFSR;
@@ -666,7 +633,7 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
 // slots (radial counting classes stay inline: their fold walks the launch's tensor list), else
 // inline launches of up to kMaxDesc tensors.
 static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items, int nitems, const Layout &L,
-                    hipStream_t stream, std::vector<TDesc> *tab_buf) {
+                    hipStream_t stream, std::vector<TDesc> *tab_buf, const lv_step_record *rec = nullptr) {
     const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;
     std::sort(items, items + nitems, item_less);
     for (int begin = 0; begin < nitems;) {
@@ -680,6 +647,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             const int n = cls_end - begin;
             Args args;
             fill_args_common(args, cfg, h, bound);
+            args.step_rec = rec;
             std::vector<TDesc> &tab = *tab_buf;
             if (tab.size() < (size_t)n) tab.resize((size_t)n);
             uint64_t units = 0, slot = 0;
@@ -721,6 +689,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             const int end = begin + std::min(cls_end - begin, kMaxDesc);
             Args args;
             fill_args_common(args, cfg, h, bound);
+            args.step_rec = rec;
             args.ndesc = end - begin;
             uint64_t units = 0;
             for (int k = begin; k < end; k++) {
@@ -900,6 +869,27 @@ __global__ void __launch_bounds__(kThreads) zero_fill(uint4 *p, size_t n) {
         p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
+// Graph launches: advances the call's step record on the device and writes that step's
+// coefficients for the unit kernels that follow on the stream (one thread). A call whose passes
+// assume a lagged scale (need_two: cautious or radial with the fused single pass) refuses a first
+// step: status 1, counter unchanged, and the unit kernels then change nothing.
+__global__ void __launch_bounds__(64) step_record_kernel(lv_step_record *r, float b1, float b2, float eps, float tau,
+                                                         float lam, uint32_t seed, int need_two) {
+    if (threadIdx.x != 0) return;
+    const uint64_t s = r->step + 1;
+    if (need_two && s < 2) {
+        r->status = 1u;
+        return;
+    }
+    const StepCoeffs k = step_coeffs(s, b1, b2, eps, tau, lam);
+    r->step = s;
+    r->c1 = k.c1;
+    r->c2 = k.c2;
+    r->c_sigma = k.c_sigma;
+    r->seed_base = step_seed_base(seed, s);
+    r->status = 0u;
+}
+
 struct NoAllocScratch {
     std::mutex mu;
     void *ptr[64] = {nullptr};  // `scratch` on each device (hipGetSymbolAddress)
@@ -1033,6 +1023,45 @@ int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int co
         g_noalloc.dirty[dev] = true;
     }
     return rc;
+}
+
+int lv_step_multi_graph(const lv_config *cfg, const lv_tensor *tensors, int count, lv_step_record *record,
+                        void *workspace, size_t workspace_bytes, void *stream_ptr) {
+    using namespace lv;
+    g_err[0] = 0;
+    if (!cfg) return fail(LV_STATUS_NULL_POINTER, "config is NULL");
+    if (!record) return fail(LV_STATUS_NULL_POINTER, "step record is NULL");
+    if (count < 0) return fail(LV_STATUS_INVALID_CONFIG, "negative tensor count");
+    if (count == 0) return LV_STATUS_SUCCESS;
+    if (!tensors) return fail(LV_STATUS_NULL_POINTER, "tensor list is NULL");
+    int rc = validate_config(cfg);
+    if (rc != LV_STATUS_SUCCESS) return rc;
+    if (!workspace) return fail(LV_STATUS_NULL_POINTER, "workspace is NULL");
+    if (((uintptr_t)workspace & 255u) != 0) return fail(LV_STATUS_INVALID_CONFIG, "workspace must be 256-byte aligned");
+    if (((uintptr_t)record & 7u) != 0) return fail(LV_STATUS_INVALID_CONFIG, "step record must be 8-byte aligned");
+    uint64_t tslots;
+    uint32_t runits;
+    call_needs(cfg, tensors, count, tslots, runits);
+    const size_t need = layout_bytes(0, runits);  // inline launches only
+    if (workspace_bytes < need)
+        return fail(LV_STATUS_INVALID_CONFIG, "workspace too small: %zu < %zu", workspace_bytes, need);
+    CallScratch &cs = t_call;
+    if (cs.items.size() < (size_t)count) cs.items.resize((size_t)count);
+    if (cs.spans.size() < (size_t)count * 5) cs.spans.resize((size_t)count * 5);
+    int nitems = 0;
+    rc = prepare_call(cfg, tensors, count, cs.items.data(), nitems, cs.spans.data());
+    cs.last_nitems = -1;  // items below get graph passes: not a cache entry for lv_step_multi
+    if (rc != LV_STATUS_SUCCESS || nitems == 0) return rc;
+    // Every step a replay takes is a later one: passes as for step >= 2, one class per dtype set.
+    const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;
+    for (int k = 0; k < nitems; k++) set_step(cs.items[(size_t)k], cfg, bound, 2);
+    const bool need_two = (cfg->cautious || bound == LV_BOUND_RADIAL) && cfg->fused_single_pass;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    hipLaunchKernelGGL(step_record_kernel, dim3(1), dim3(64), 0, stream, record, cfg->beta1, cfg->beta2, cfg->eps,
+                       cfg->tau, cfg->lam, cfg->seed, need_two ? 1 : 0);
+    if (hipGetLastError() != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "step record launch failed");
+    const Layout L = make_layout(static_cast<char *>(workspace), 0, runits);
+    return run_call(cfg, tensors, cs.items.data(), nitems, L, stream, nullptr, record);
 }
 
 int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq, float *master_param,

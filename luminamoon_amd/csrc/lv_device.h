@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 
 #include "luminav_hip.h"
@@ -125,6 +126,7 @@ struct Args {
     double *unit_sq;              // radial: per unit of the piece, (sum u_eff^2, sum p^2)
     uint32_t *unit_cnt;           // radial: per unit of the piece, the mask count
     const TDesc *dtab;            // table launches: the tensor table in device memory
+    const lv_step_record *step_rec;  // graph launches: this step's coefficients (else c1..seed_base above)
     union {
         Desc d[kMaxDesc];  // inline launches: the tensor table
         uint32_t ubegin[kMaxDesc * sizeof(Desc) / sizeof(uint32_t)];  // table launches: first unit per head
@@ -139,6 +141,50 @@ constexpr int kTableHeads = kMaxDesc * (int)(sizeof(Desc) / sizeof(uint32_t));  
 static_assert(sizeof(Desc) == 80, "descriptor layout");
 static_assert(sizeof(TDesc) == 88, "table descriptor layout");
 static_assert(sizeof(Args) <= 4096, "kernel arguments must fit in 4 KiB");
+
+// ------------------------------------------------------------------ per-step coefficients
+
+// compiler-builtins' __powidf2 (the lowering of Rust f64::powi): repeated squaring.
+__host__ __device__ inline double powi_rs(double a, int32_t b) {
+    bool recip = b < 0;
+    uint32_t pw = recip ? (uint32_t)(-(int64_t)b) : (uint32_t)b;
+    double mul = 1.0;
+    for (;;) {
+        if (pw & 1u) mul *= a;
+        pw >>= 1;
+        if (pw == 0) break;
+        a *= a;
+    }
+    return recip ? 1.0 / mul : mul;
+}
+
+struct StepCoeffs {
+    float c1, c2, c_sigma;
+};
+
+// math.rs:27-81, on the host for every launch and on the device for graph launches (the step
+// record kernel): IEEE f64 products, quotient and square root (correctly rounded on both sides),
+// so both give the same bits. Above 2^31 - 1 steps the reference switches to f64::powf, here the
+// platform's pow (not pinned against the reference's).
+__host__ __device__ inline StepCoeffs step_coeffs(uint64_t step, float beta1, float beta2, float eps, float tau,
+                                                  float lam) {
+    uint64_t safe = step > 1 ? step : 1;
+    double b1 = (double)beta1, b2 = (double)beta2;
+    double bc1 = safe < 2147483647ull ? 1.0 - powi_rs(b1, (int32_t)(safe + 1)) : 1.0 - pow(b1, (double)(safe + 1));
+    double bc2_raw = safe <= 2147483647ull ? 1.0 - powi_rs(b2, (int32_t)safe) : 1.0 - pow(b2, (double)safe);
+    double bc2 = fmax(bc2_raw, 1.0e-15);
+    StepCoeffs c;
+    c.c1 = (float)((bc1 * (double)tau) / sqrt(bc2));
+    c.c2 = (float)((double)eps * bc1 * (double)tau);
+    float bc2f = (float)bc2;
+    c.c_sigma = (0.5f * lam) / sqrtf(fmaxf(bc2f, 1.0e-15f));
+    return c;
+}
+
+// Seed base of a step: low 32 bits of seed + step * 0x9E3779B9 (prng.rs:4-13).
+__host__ __device__ inline uint32_t step_seed_base(uint32_t seed, uint64_t step) {
+    return (uint32_t)((uint64_t)seed + step * 0x9E3779B9ull);
+}
 
 // ------------------------------------------------------------------ device math
 
@@ -337,7 +383,7 @@ __device__ __forceinline__ float u64_to_f32_rn(uint64_t x) {
 // u, m_new, v_new for one element.
 // CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
 template <int MODE>
-__device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g, float m, float v,
+__device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, bool clamp_v, float g, float m, float v,
                                            float &m_new, float &v_new) {
     m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
     if constexpr (MODE == LV_BUFFER_DUAL) {
@@ -345,7 +391,7 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
         float diff = clamp_defect(g - m_new);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
-        float sigma = __builtin_fmaf(sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), a.c1, a.c2);
+        float sigma = __builtin_fmaf(sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), k.c1, k.c2);
         return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
     } else if constexpr (MODE == LV_BUFFER_T2) {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
@@ -355,7 +401,7 @@ __device__ __forceinline__ float compute_u(const Args &a, bool clamp_v, float g,
         float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
-        float env = __builtin_fmaf(a.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
+        float env = __builtin_fmaf(k.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
         return clm / env;
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
@@ -522,7 +568,7 @@ __device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
 // Returns the cautious mask bit; u_eff is the (masked) direction whose square feeds the radial
 // norm (dual.rs:176-180).
 template <int MODE, int PT, int ST>
-__device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, const HashIn &z,
+__device__ __forceinline__ uint32_t apply_elem(const Args &a, const StepCoeffs &k, uint32_t flags, const HashIn &z,
                                                float cs, float bs, float p_init, float g_raw, float &m_io,
                                                float &v_io, float &p_out, float &mp_out, float &u_eff) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
@@ -530,7 +576,7 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
     const bool sr = flags & kFSR;
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    float u = compute_u<MODE>(a, k, flags & kFClampV, g, m_io, v_io, m_new, v_new);
     bool active = (u * g) > 0.0f;
     float m_mask = active ? 1.0f : 0.0f;
     m_io = quantize<ST>(m_new, z.m, sr);
@@ -554,11 +600,11 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, uint32_t flags, co
 
 // Counting path for one element (dual.rs:279-303, dual.rs:720-746, tdclm.rs:232-248).
 template <int MODE>
-__device__ __forceinline__ uint32_t count_elem(const Args &a, uint32_t flags, float g_raw, float m, float v,
+__device__ __forceinline__ uint32_t count_elem(const Args &a, const StepCoeffs &k, uint32_t flags, float g_raw, float m, float v,
                                                float &u_eff) {
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, flags & kFClampV, g, m, v, m_new, v_new);
+    float u = compute_u<MODE>(a, k, flags & kFClampV, g, m, v, m_new, v_new);
     bool active = (u * g) > 0.0f;
     u_eff = (flags & kFCautious) ? u * (active ? 1.0f : 0.0f) : u;
     return active ? 1u : 0u;
@@ -675,6 +721,8 @@ struct View {
     float cs, bs;             // cautious / radial scale read from the scratch (fused, apply)
     Seeds sd;
     uint32_t ibase;
+    StepCoeffs k;             // this step's c1, c2, c_sigma (kernel arguments, or the step record)
+    bool skip;                // graph launch whose step record refused the step: change nothing
 };
 
 template <int MODE, int PASS, bool TABLE>
@@ -695,7 +743,16 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
     if (flags & kFMaster) al |= (uintptr_t)D.mp;
     tv.vec_ok = (al & 15u) == 0;
     tv.ibase = D.ibase;
-    uint32_t raw = a.seed_base + D.pidx * 10007u;
+    uint32_t seed_base = a.seed_base;
+    tv.k = {a.c1, a.c2, a.c_sigma};
+    tv.skip = false;
+    if (a.step_rec) {  // graph launch: the coefficients the step record kernel wrote for this step
+        const lv_step_record *r = a.step_rec;
+        tv.k = {r->c1, r->c2, r->c_sigma};
+        seed_base = r->seed_base;
+        tv.skip = r->status != 0;
+    }
+    uint32_t raw = seed_base + D.pidx * 10007u;
     tv.sd.m = (int32_t)(raw & 0x7FFFFFFFu);
     tv.sd.p = (int32_t)(((uint32_t)tv.sd.m + 0x55555555u) & 0x7FFFFFFFu);
     tv.sd.v = (int32_t)(((uint32_t)tv.sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
@@ -708,7 +765,7 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
     if constexpr (PASS == kSingle) {
         // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
         // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
-        if (unit == tv.t_begin && threadIdx.x == 0) {
+        if (unit == tv.t_begin && threadIdx.x == 0 && !tv.skip) {
             float *sc = D.scratch;
             sc[0] = 0.0f; sc[1] = 0.0f; sc[2] = 0.0f; sc[3] = 1.0f; sc[4] = 1.0f; sc[5] = 0.0f;
         }
@@ -756,7 +813,7 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
             float ue;
-            const uint32_t act = count_elem<MODE>(a, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
+            const uint32_t act = count_elem<MODE>(a, tv.k, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
             if constexpr (BALLOT) cnt += (uint32_t)__popcll(__ballot(act));
             else cnt += act;
             if (radial) {
@@ -776,7 +833,7 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
             float ue;
             const uint32_t jj = j < 4 ? (uint32_t)j : kHalf + (uint32_t)j - 4u;  // a constant once unrolled
             const HashIn zj = {zb.m + jj, zb.p + jj, zb.v + jj};
-            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+            uint32_t act = apply_elem<MODE, PT, ST>(a, tv.k, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
                                                     mpout[j], ue);
             if constexpr (kDual) v[j] = vj;
             if constexpr (kCounting) {
@@ -820,7 +877,7 @@ __device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const
         float v = kDual ? load1<ST>(D.v, i) : 0.0f;
         if constexpr (PASS == kCount) {
             float ue;
-            cnt += count_elem<MODE>(a, flags, g, m, v, ue);
+            cnt += count_elem<MODE>(a, tv.k, flags, g, m, v, ue);
             if (radial) {
                 float pin = master ? D.mp[i] : load1<PT>(D.p, i);
                 su += (double)(ue * ue);
@@ -829,7 +886,7 @@ __device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const
         } else {
             float pin = master ? D.mp[i] : load1<PT>(D.p, i);
             float pout, mpout, ue;
-            uint32_t act = apply_elem<MODE, PT, ST>(a, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs,
+            uint32_t act = apply_elem<MODE, PT, ST>(a, tv.k, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs,
                                                     pin, g, m, v, pout, mpout, ue);
             if (!inactive) {
                 store1<PT>(D.p, i, pout);
@@ -971,6 +1028,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const int t = find_tensor<TABLE>(a, unit);
     const Desc &D = desc_of<TABLE>(a, t);
     const View tv = open_view<MODE, PASS, TABLE>(a, D, t, flags, unit);
+    if (tv.skip) return;  // block-uniform: the whole launch leaves every buffer as it was
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
@@ -1060,6 +1118,7 @@ template <int MODE, int PASS>
 __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
     __shared__ BlockSums sh;
     __shared__ uint32_t last;
+    if (a.step_rec && a.step_rec->status != 0) return;  // refused graph step: the unit launch wrote nothing
     const uint32_t ub = a.unit_base, ue = a.unit_base + a.piece_units;
     uint32_t j = blockIdx.x, cbase = 0, lo = 0, hi = 0, nc = 0;
     int t = 0;

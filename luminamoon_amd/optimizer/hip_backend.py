@@ -70,9 +70,22 @@ class LvTensor(ctypes.Structure):
     ]
 
 
+class LvStepRecord(ctypes.Structure):
+    """lv_step_record: the device-side step counter and coefficients of graph launches."""
+    _fields_ = [
+        ("step", ctypes.c_uint64),
+        ("c1", ctypes.c_float),
+        ("c2", ctypes.c_float),
+        ("c_sigma", ctypes.c_float),
+        ("seed_base", ctypes.c_uint32),
+        ("status", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
 EXPORTED_SYMBOLS = (
-    "lv_version", "lv_workspace_bytes", "lv_workspace_bytes_for", "lv_step_multi", "lv_step_multi_noalloc",
-    "lv_step_f32", "lv_last_error",
+    "lv_version", "lv_workspace_bytes", "lv_workspace_bytes_for", "lv_step_multi", "lv_step_multi_graph",
+    "lv_step_multi_noalloc", "lv_step_f32", "lv_last_error",
     # the reference's standalone C API (luminav_triton_standalone.h:37-111)
     "luminav_triton_engine_create", "luminav_triton_engine_destroy", "luminav_triton_get_platform",
     "luminav_triton_get_arch", "luminav_triton_step_f32",
@@ -109,6 +122,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
             ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
             ctypes.c_void_p,
         ]
+        L.lv_step_multi_graph.restype = ctypes.c_int
+        L.lv_step_multi_graph.argtypes = [ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         L.lv_step_multi_noalloc.restype = ctypes.c_int
         L.lv_step_multi_noalloc.argtypes = [ctypes.POINTER(LvConfig), ctypes.POINTER(LvTensor), ctypes.c_int,
                                             ctypes.c_void_p]
@@ -338,6 +354,30 @@ class HipStepper:
                 raise ValueError(f"LuminaV HIP step rejected the call ({STATUS_NAMES.get(rc, rc)}): {msg}")
             self.workspace.discard(prep.device)
             raise RuntimeError(f"LuminaV HIP step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
+
+    def graph_workspace(self, group: Dict[str, Any], prep: PreparedStep) -> torch.Tensor:
+        """A zeroed workspace of its own for lv_step_multi_graph calls over prep (graph replays
+        must not share the stepper's workspace with eager calls on other streams)."""
+        lib = load_library()
+        cfg = make_config(group)
+        need = int(lib.lv_workspace_bytes_for(ctypes.byref(cfg), prep.items, prep.n))
+        return torch.zeros(max(need, 256), dtype=torch.uint8, device=prep.device)
+
+    def launch_graph(self, group: Dict[str, Any], prep: PreparedStep, record: torch.Tensor,
+                     workspace: torch.Tensor) -> None:
+        """One lv_step_multi_graph call: the step count and coefficients come from the device step
+        record (an int64[4] tensor on prep's device), which the call advances on the stream."""
+        lib = load_library()
+        cfg = make_config(group)
+        with torch.cuda.device(prep.device):
+            stream = _current_stream_handle(prep.index)
+            rc = lib.lv_step_multi_graph(ctypes.byref(cfg), prep.items, prep.n, record.data_ptr(), workspace.data_ptr(),
+                                         workspace.numel(), stream)
+        if rc != 0:
+            msg = lib.lv_last_error().decode(errors="replace")
+            if rc in (-1, -3):
+                raise ValueError(f"LuminaV HIP graph step rejected the call ({STATUS_NAMES.get(rc, rc)}): {msg}")
+            raise RuntimeError(f"LuminaV HIP graph step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
 
     def step(
         self,

@@ -19,7 +19,7 @@ def build(verbose: bool = False) -> str:
 
     tmp = EXACT_LIB + ".tmp"
     cmd = [build_ext.hipcc(), *build_ext.HIPCC_FLAGS, "-I", os.path.join(ROOT, "luminamoon_amd", "csrc"),
-           EXACT_SRC, "-o", tmp]
+           "-I", os.path.join(ROOT, "include"), EXACT_SRC, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -15,6 +15,7 @@
 
 #include <cstdint>
 
+#include "lv_device.h"
 #include "lv_exact.h"
 
 namespace {
@@ -153,5 +154,37 @@ extern "C" int exact_check(unsigned long long *host_counts /* kCounters */, uint
         rc = -3;
     (void)hipFree(out);
     (void)hipFree(ex);
+    return rc;
+}
+
+// The graph launches' per-step coefficients computed on the device (lv::step_coeffs, the function
+// the step record kernel calls), for the host to compare with its own: out[4 * i ..] = c1, c2,
+// c_sigma (bits) and the seed base of steps[i].
+__global__ void coeff_kernel(const uint64_t *steps, int n, float b1, float b2, float eps, float tau, float lam,
+                             uint32_t seed, uint32_t *out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const lv::StepCoeffs k = lv::step_coeffs(steps[i], b1, b2, eps, tau, lam);
+    out[4 * i] = __float_as_uint(k.c1);
+    out[4 * i + 1] = __float_as_uint(k.c2);
+    out[4 * i + 2] = __float_as_uint(k.c_sigma);
+    out[4 * i + 3] = lv::step_seed_base(seed, steps[i]);
+}
+
+extern "C" int coeff_check(const uint64_t *host_steps, int n, float b1, float b2, float eps, float tau, float lam,
+                           uint32_t seed, uint32_t *host_out) {
+    uint64_t *steps = nullptr;
+    uint32_t *out = nullptr;
+    if (n <= 0) return 0;
+    if (hipMalloc(&steps, (size_t)n * sizeof(uint64_t)) != hipSuccess) return -1;
+    if (hipMalloc(&out, (size_t)n * 4 * sizeof(uint32_t)) != hipSuccess) return -1;
+    int rc = hipMemcpy(steps, host_steps, (size_t)n * sizeof(uint64_t), hipMemcpyHostToDevice) == hipSuccess ? 0 : -2;
+    if (rc == 0) {
+        coeff_kernel<<<(n + 255) / 256, 256>>>(steps, n, b1, b2, eps, tau, lam, seed, out);
+        rc = hipDeviceSynchronize() == hipSuccess ? 0 : -3;
+    }
+    if (rc == 0 && hipMemcpy(host_out, out, (size_t)n * 4 * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) rc = -4;
+    (void)hipFree(steps);
+    (void)hipFree(out);
     return rc;
 }

@@ -278,7 +278,8 @@ def _c_layout(struct, fields, tmp_path):
     return int(out[0]), [int(x) for x in out[1:]]
 
 
-@pytest.mark.parametrize("ctype,cname", [(H.LvConfig, "lv_config"), (H.LvTensor, "lv_tensor")])
+@pytest.mark.parametrize("ctype,cname", [(H.LvConfig, "lv_config"), (H.LvTensor, "lv_tensor"),
+                                          (H.LvStepRecord, "lv_step_record")])
 def test_struct_layouts_match_header(ctype, cname, tmp_path):
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")

@@ -1,0 +1,268 @@
+"""Graph-capture-safe stepping (lv_step_multi_graph): the step count and its coefficients live in
+a device record that each call advances, so a HIP graph captured around a call replays correct
+steps. Checked bit for bit against lv_step_multi (host step counts) eagerly and through captured
+graph replays, and the device coefficients against the host's (and the oracle's)."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests.parity_util import TensorSet, group_dict
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+
+
+def _lib():
+    from luminamoon_amd.optimizer import hip_backend as H
+
+    return H.load_library()
+
+
+def test_device_coefficients_equal_the_hosts(oracle_mod):
+    """lv::step_coeffs on the device (what the step record kernel runs) against the oracle's
+    bias correction and T2 sigma coefficient on the host (math.rs:27-81), bit for bit, for steps
+    1 .. 100,000, powers of two and random counts up to 2^31 - 2, over several hyper-parameter
+    sets; and the seed base against seed + step * 0x9E3779B9 mod 2^32."""
+    _need_gpu()
+    from tests.gpu_checks import build as B
+
+
+
+    if not os.path.exists(B.EXACT_LIB):
+        B.build()
+    lib = ctypes.CDLL(B.EXACT_LIB)
+    lib.coeff_check.restype = ctypes.c_int
+    lib.coeff_check.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_float] * 5 + [ctypes.c_uint32, ctypes.c_void_p]
+    L = oracle_mod.lib()
+    rng = np.random.default_rng(4)
+    steps = np.concatenate([np.arange(1, 100_001), 2 ** np.arange(0, 31), rng.integers(1, 2 ** 31 - 2, 20_000)]).astype(np.uint64)
+    out = np.zeros(4 * steps.size, dtype=np.uint32)
+    for b1, b2, eps, tau, lam, seed in ((0.9, 0.999, 1e-8, 0.8, 0.3, 1337), (0.95, 0.98, 1e-6, 1.3, 0.0, 7),
+                                        (0.0, 0.5, 3e-9, 0.25, 2.5, 0xFFFFFFFF), (0.99, 0.99999, 1e-8, 0.8, 0.3, 1)):
+        print(f"[case] coefficients b1={b1} b2={b2} eps={eps} tau={tau} lam={lam}", flush=True)
+        assert lib.coeff_check(steps.ctypes.data, steps.size, b1, b2, eps, tau, lam, seed, out.ctypes.data) == 0
+        got = out.reshape(-1, 4)
+        bc = (ctypes.c_float * 5)()
+        idx = np.r_[np.arange(0, steps.size, 97), np.arange(steps.size - 200, steps.size)]  # oracle on a sample
+        for i in idx:
+            s = int(steps[i])
+            L.lvo_bias_correction(s, b1, b2, eps, tau, bc)
+            cs = L.lvo_t2_sigma_coeff(s, b2, lam)
+            want = np.array([bc[2], bc[3], cs], dtype=np.float32).view(np.uint32)
+            assert np.array_equal(got[i, :3], want), (s, got[i, :3], want)
+        base = ((np.uint64(seed) + steps * np.uint64(0x9E3779B9)) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        assert np.array_equal(got[:, 3], base)
+
+
+CASES = [
+    ("T2", "bf16", "f32", {}),
+    (1, "f32", "f32", {"lam": 0.3}),
+    (2, "bf16", "bf16", {"state_precision": "param", "master_weights": "semi"}),
+    ("T1", "bf16", "f32", {"bound_type": "radial"}),
+    (2, "f32", "f32", {"cautious": False}),
+    ("T2", "f16", "f32", {"fused_single_pass": False}),
+]
+
+
+@pytest.mark.parametrize("buffer,pdt,sdt,extra", CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}-{i}" for i, c in enumerate(CASES)])
+def test_graph_entry_matches_lv_step_multi(buffer, pdt, sdt, extra):
+    """Eagerly: step 1 through lv_step_multi, then lv_step_multi_graph with its device record
+    (set to 1) against lv_step_multi with host step counts, bit for bit over 5 more steps, on 60
+    ragged tensors (several inline launches per class)."""
+    _need_gpu()
+    from luminamoon_amd.optimizer import hip_backend as H
+
+    L = _lib()
+    kw = dict(extra)
+    kw.setdefault("lr", 1e-3)
+    group = group_dict(buffer=buffer, **kw)
+    dual = group["buffer"] in (2, "T2")
+    master = group["master_weights"] > 0 and pdt != "f32"
+    rng = np.random.default_rng(11)
+    sizes = [int(np.exp(rng.uniform(0, np.log(100_000)))) + 1 for _ in range(60)]
+    host = TensorSet(sizes, pdt, pdt, sdt, dual, master, 3)
+    a, b = host.to("cuda"), host.to("cuda")
+    st = H.HipStepper()
+    cfg = H.make_config(group)
+    rec = torch.zeros(4, dtype=torch.int64, device="cuda")
+    ws = torch.zeros(int(L.lv_workspace_bytes(len(sizes))), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    print(f"[case] graph entry {buffer} {pdt}/{sdt} {extra}", flush=True)
+    for s in range(1, 7):
+        grads = [g.cuda() for g in host.grads(s, 8)]
+        st.step(group, a.p, grads, a.m, a.v, a.mp, a.sc, [s] * len(sizes), list(range(len(sizes))))
+        if s == 1:
+            st.step(group, b.p, grads, b.m, b.v, b.mp, b.sc, [1] * len(sizes), list(range(len(sizes))))
+            rec[0] = 1
+        else:
+            prep = st.prepare(b.p, grads, b.m, b.v, b.mp, b.sc, [0] * len(sizes), list(range(len(sizes))))
+            rc = L.lv_step_multi_graph(ctypes.byref(cfg), prep.items, prep.n, rec.data_ptr(), ws.data_ptr(), ws.numel(),
+                                       stream)
+            assert rc == 0, L.lv_last_error()
+        torch.cuda.synchronize()
+        a.assert_equal(b, f"step {s}")
+    r = rec.cpu().numpy().view(np.uint32)
+    assert int(rec[0]) == 6 and r[6] == 0  # step count, status
+
+
+def test_captured_graph_replays_match_eager():
+    """A torch.cuda.CUDAGraph (HIP graph) captured around one lv_step_multi_graph call, replayed 6
+    times with fresh gradients copied into its static grad buffers between replays, eager work and
+    host synchronisations in between; after every replay every buffer and scratch equals
+    lv_step_multi's eager step of the same count, bit for bit (T2 cautious bf16 and TD-CLM f32,
+    60 tensors)."""
+    _need_gpu()
+    from luminamoon_amd.optimizer import hip_backend as H
+
+    L = _lib()
+    for buffer, pdt in (("T2", "bf16"), (1, "f32")):
+        group = group_dict(buffer=buffer, lr=1e-3)
+        dual = group["buffer"] in (2, "T2")
+        rng = np.random.default_rng(12)
+        sizes = [int(np.exp(rng.uniform(0, np.log(70_000)))) + 1 for _ in range(60)]
+        host = TensorSet(sizes, pdt, pdt, "f32", dual, False, 5)
+        a, b = host.to("cuda"), host.to("cuda")
+        st = H.HipStepper()
+        cfg = H.make_config(group)
+        n = len(sizes)
+        static_g = [torch.zeros(k, dtype=host.gdt, device="cuda") for k in sizes]
+        rec = torch.zeros(4, dtype=torch.int64, device="cuda")
+        ws = torch.zeros(int(L.lv_workspace_bytes(n)), dtype=torch.uint8, device="cuda")
+        # step 1 eagerly on both; the record then says 1
+        g1 = [g.cuda() for g in host.grads(1, 9)]
+        for x in (a, b):
+            st.step(group, x.p, g1, x.m, x.v, x.mp, x.sc, [1] * n, list(range(n)))
+        rec[0] = 1
+        prep = st.prepare(b.p, static_g, b.m, b.v, b.mp, b.sc, [0] * n, list(range(n)))
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        print(f"[case] capture buffer={buffer} {pdt}", flush=True)
+        with torch.cuda.graph(graph):
+            rc = L.lv_step_multi_graph(ctypes.byref(cfg), prep.items, prep.n, rec.data_ptr(), ws.data_ptr(), ws.numel(),
+                                       torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, L.lv_last_error()
+        torch.cuda.synchronize()
+        assert int(rec[0]) == 1  # capture ran nothing
+        for s in range(2, 8):
+            grads = [g.cuda() for g in host.grads(s, 9)]
+            for sg, g in zip(static_g, grads):
+                sg.copy_(g)
+            scratch_work = torch.randn(1 << 16, device="cuda").sum()  # eager work between replays
+            graph.replay()
+            st.step(group, a.p, grads, a.m, a.v, a.mp, a.sc, [s] * n, list(range(n)))
+            torch.cuda.synchronize()
+            assert torch.isfinite(scratch_work)
+            a.assert_equal(b, f"buffer={buffer} replay for step {s}")
+            assert int(rec[0]) == s
+
+
+@pytest.mark.parametrize("extra", [{}, {"bound_type": "radial", "cautious": False}], ids=["cautious", "radial"])
+def test_first_step_refused_on_the_device(extra):
+    """With cautious (or the radial bound) and the fused single pass, a graph call at record step
+    0 would need the two-pass first step: the device refuses it (status 1), leaving the counter,
+    every buffer and the workspace as they were (the radial fold launch included)."""
+    _need_gpu()
+    from luminamoon_amd.optimizer import hip_backend as H
+
+    L = _lib()
+    group = group_dict(buffer="T2", lr=1e-3, **extra)
+    host = TensorSet([5000, 3], "bf16", "bf16", "f32", True, False, 2)
+    d = host.to("cuda")
+    st = H.HipStepper()
+    cfg = H.make_config(group)
+    rec = torch.zeros(4, dtype=torch.int64, device="cuda")
+    ws = torch.zeros(int(L.lv_workspace_bytes(2)), dtype=torch.uint8, device="cuda")
+    grads = [g.cuda() for g in host.grads(1, 2)]
+    prep = st.prepare(d.p, grads, d.m, d.v, d.mp, d.sc, [0, 0], [0, 1])
+    rc = L.lv_step_multi_graph(ctypes.byref(cfg), prep.items, prep.n, rec.data_ptr(), ws.data_ptr(), ws.numel(),
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    r = rec.cpu().numpy().view(np.uint32)
+    assert int(rec[0]) == 0 and r[6] == 1
+    host.assert_equal(d, "refused step")
+    assert int(torch.count_nonzero(ws)) == 0
+
+
+def _models(dtype):
+    torch.manual_seed(3)
+    a = torch.nn.Sequential(torch.nn.Linear(64, 96), torch.nn.ReLU(), torch.nn.Linear(96, 7)).to(dtype=dtype, device="cuda")
+    b = __import__("copy").deepcopy(a)
+    return a, b
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(buffer=1, bound_type="radial"), dict(buffer="T1", master_weights="full")],
+                         ids=["T2", "tdclm-radial", "t1-master"])
+def test_capturable_optimizer_graph_replays_match_eager(kw):
+    """LuminaV(capturable=True) captured with torch.cuda.graph after two eager steps, replayed for
+    steps 3..8 with new gradients copied into the static grads: after every replay every param and
+    state buffer equals a plain LuminaV's eager steps bit for bit, and state["step"] (a 0-dim
+    device tensor) equals the eager step count; state_dict() stores the counts as ints."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    a, b = _models(torch.bfloat16)
+    oa = LuminaV(a.parameters(), lr=1e-2, capturable=True, **kw)
+    ob = LuminaV(b.parameters(), lr=1e-2, **kw)
+    pa, pb = list(a.parameters()), list(b.parameters())
+    static = [torch.zeros_like(p) for p in pa]
+    for p, g in zip(pa, static):
+        p.grad = g
+
+    def grads(step):
+        gen = torch.Generator(device="cuda").manual_seed(100 + step)
+        return [torch.randn(p.shape, generator=gen, device="cuda").to(p.dtype) * 1e-2 for p in pa]
+
+    def check(step):
+        for i, (x, y) in enumerate(zip(pa, pb)):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16)), f"step {step} param {i}"
+            sa, sb = oa.state[x], ob.state[y]
+            for k in ("exp_avg", "exp_avg_sq", "master_param", "scratch"):
+                if k in sb:
+                    assert torch.equal(sa[k], sb[k]), f"step {step} param {i} {k}"
+            assert isinstance(sa["step"], torch.Tensor) and int(sa["step"]) == sb["step"] == step
+
+    for s in (1, 2):
+        for g, gs, q in zip(grads(s), static, pb):
+            gs.copy_(g)
+            q.grad = g.clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
+    graph = torch.cuda.CUDAGraph()
+    print(f"[case] capture LuminaV(capturable=True) {kw}", flush=True)
+    with torch.cuda.graph(graph):
+        oa.step()
+    torch.cuda.synchronize()
+    check(2)  # capturing ran nothing
+    for s in range(3, 9):
+        for g, gs, q in zip(grads(s), static, pb):
+            gs.copy_(g)
+            q.grad = g.clone()
+        graph.replay()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
+    sd = oa.state_dict()
+    assert all(isinstance(st["step"], int) and st["step"] == 8 for st in sd["state"].values())
+    # resume the checkpoint eagerly into a fresh capturable optimizer
+    oc = LuminaV(a.parameters(), lr=1e-2, capturable=True, **kw)
+    oc.load_state_dict(sd)
+    oa = oc
+    for g, gs, q in zip(grads(9), static, pb):
+        gs.copy_(g)
+        q.grad = g.clone()
+    oc.step()
+    ob.step()
+    torch.cuda.synchronize()
+    check(9)

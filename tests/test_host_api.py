@@ -238,3 +238,29 @@ def test_fsdp_sync_across_ranks_is_refused(monkeypatch):
     LuminaV([p], fsdp_sync=True)
     monkeypatch.setattr(torch.distributed, "is_initialized", lambda: False)
     LuminaV([p], fsdp_sync=True)
+
+
+def test_capturable_option_validation_and_guards(monkeypatch):
+    """capturable=True: a bool, not with fused buckets; a group holding state steps every
+    parameter together (a parameter with state and no grad raises); capturing a group before its
+    eager set-up step raises before anything is launched."""
+    p = nn.Parameter(torch.zeros(4))
+    assert LuminaV([p], capturable=True).param_groups[0]["capturable"] is True
+    assert LuminaV([p]).param_groups[0]["capturable"] is False
+    with pytest.raises(ValueError, match="capturable"):
+        LuminaV([p], capturable="yes")
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        with pytest.raises(ValueError, match="fuse_tensors=False"):
+            LuminaV([p], capturable=True, fuse_tensors=True)
+    q = nn.Parameter(torch.zeros(4))
+    opt = LuminaV([p, q], capturable=True)
+    opt.state[q]["step"] = 3
+    p.grad = torch.zeros(4)
+    with pytest.raises(ValueError, match="steps all of its parameters together"):
+        opt.step()
+    q.grad = torch.zeros(4)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="eager step"):
+        opt.step()
+    assert opt.state[q]["step"] == 3 and len(opt.state[p]) == 0
