@@ -238,8 +238,13 @@ __device__ __forceinline__ float rne_bf16(float v) {
 
 // f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
 
-// prng.rs:98-130
+// prng.rs:98-130. On the hardware converter's domain (sr_f16_hw in lv_exact.h: +-0 and fp16
+// normal results below 65504) the noise prng(z0) & 0x1FFF goes in bits 31..19 of its random
+// operand; when any active lane of the wave is outside that domain, the wave takes the integer
+// recipe below (the one the reference states).
 __device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!sr_f16_hw_domain(v)) == 0, 1))
+        return sr_f16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)) << 3);
     int32_t p = (int32_t)f_bits(v);
     int32_t a = p & 0x7FFFFFFF;
     int32_t ex = (a >> 23) & 0xFF;

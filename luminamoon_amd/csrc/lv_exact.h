@@ -33,6 +33,15 @@
 // The result is returned as an f32 whose high half holds the bf16 bits; its low half is NOT
 // zero, so it is only good for storing the high half.
 //
+// sr_f16_hw: fp16 stochastic rounding (prng.rs:98-130) on gfx950's v_cvt_sr_f16_f32, on its
+// domain: +-0 and 2^-14 <= |v| < 65504 (the results are fp16 normals or zeros). For such inputs the
+// reference discards 13 fraction bits and adds 13 noise bits (the low 13 of the hash); the
+// converter adds the high 13 bits of its random operand to the same 13 bits, so the noise goes in
+// bits 31..19. Outside the domain the two differ and callers take the integer recipe: below 2^-14
+// the reference widens both the discarded field and the noise to 13 + k bits where the converter
+// keeps 13 (ignoring the discarded bits below them), and at the top the reference saturates to
+// 65504 where the converter overflows to infinity. The result is the fp16 value as an f32.
+//
 // The fp16 conversions need fp16 denormals enabled, the HIP default for gfx950 code objects.
 #pragma once
 
@@ -108,6 +117,18 @@ __device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
     v2s d = __builtin_bit_cast(v2s, v);  // the low half keeps v's bits (never read)
     d = __builtin_amdgcn_cvt_sr_bf16_f32(d, v, noise_hi, true);
     return __builtin_bit_cast(float, d);
+}
+
+__device__ __forceinline__ bool sr_f16_hw_domain(float v) {
+    const float a = __builtin_fabsf(v);
+    return a < 65504.0f && (a >= 0x1p-14f || a == 0.0f);  // false for NaN
+}
+
+__device__ __forceinline__ float sr_f16_hw(float v, uint32_t noise_hi) {
+    typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+    v2h d = {(_Float16)0.0f, (_Float16)0.0f};
+    d = __builtin_amdgcn_cvt_sr_f16_f32(d, v, noise_hi, false);
+    return (float)d.x;  // exact
 }
 
 }  // namespace lv

@@ -8,7 +8,10 @@
 //   sr_bf16_hw against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
 //     with 6 noise values per input (0, 1, 0x7FFF, 0x8000, 0xFFFF and a hash of the input), 6 x 2^32;
 //   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN);
-//   pack_f16_exact on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16.
+//   pack_f16_exact on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
+//   sr_f16_hw against the reference's fp16 stochastic rounding (prng.rs:98-130, restated here) on
+//     every input of its domain (sr_f16_hw_domain) with 6 noise values per input (0, 1, 0xFFF,
+//     0x1000, 0x1FFF and a hash of the input), and the domain test against its definition, 2^32.
 // Test infrastructure: built by __graft_entry__.build() into tests/gpu_checks/libexactcheck.so
 // and run by tests/test_gpu_exact_exhaustive.py.
 #include <hip/hip_runtime.h>
@@ -65,6 +68,20 @@ __device__ uint32_t ref_sr_bf16(uint32_t p, uint32_t noise) {
     return ((p & 0x80000000u) | added) >> 16;
 }
 
+// prng.rs:98-130 with the noise given (its low 13 + k bits are used): the result's f32 bits
+__device__ uint32_t ref_sr_f16(uint32_t pu, uint32_t noise) {
+    const int32_t p = (int32_t)pu;
+    const int32_t a = p & 0x7FFFFFFF;
+    const int32_t ex = (a >> 23) & 0xFF;
+    int32_t sub = 113 - ex;
+    sub = sub > 0 ? sub : 0;
+    sub = sub < 11 ? sub : 11;
+    const uint32_t mask = (1u << (13 + sub)) - 1u;
+    const int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (noise & mask)) & ~mask);
+    const int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
+    return (uint32_t)((p & (int32_t)0x80000000u) | r);
+}
+
 __device__ uint32_t mix32(uint32_t z) {
     z ^= z >> 16;
     z *= 0x7FEB352Du;
@@ -81,7 +98,9 @@ __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) 
 // Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
 // NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
 // [4] xor_fold16 mismatches, [5] xor_fold16_hi, [6] sr_bf16_hw (input, any noise),
-// [7] sqrt_rn_normal on its domain, [8] pack_f16_exact; ex[8 * c + k] holds the first inputs of
+// [7] sqrt_rn_normal on its domain, [8] pack_f16_exact, [9] sr_f16_hw on its domain (input, any
+// noise) or a domain test that disagrees with its definition, [10] inputs in the sr_f16_hw domain
+// (not a mismatch: the size of the domain checked); ex[8 * c + k] holds the first inputs of
 // counter c.
 __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex) {
     const uint32_t i = base + blockIdx.x * blockDim.x + threadIdx.x;
@@ -99,6 +118,18 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
         if (got != ref_sr_bf16(i, noises[k])) record(&out[6], ex + 48, i);
     }
     const float x = __uint_as_float(i);
+    const uint32_t mag = i & 0x7FFFFFFFu;
+    const bool in_dom = mag == 0u || (mag >= 0x38800000u && mag < 0x477FE000u);  // 2^-14, 65504
+    if (lv::sr_f16_hw_domain(x) != in_dom) record(&out[9], ex + 72, i);
+    if (in_dom) {
+        if ((i & 0xFFFFu) == 0u) atomicAdd(&out[10], 1ull);  // sampled: one in 2^16
+        const uint32_t nf[6] = {0u, 1u, 0x0FFFu, 0x1000u, 0x1FFFu, h & 0x1FFFu};
+#pragma unroll
+        for (int k = 0; k < 6; k++) {
+            const uint32_t got = __float_as_uint(lv::sr_f16_hw(x, nf[k] << 19));
+            if (got != ref_sr_f16(i, nf[k])) record(&out[9], ex + 72, i);
+        }
+    }
     if (!(x < 0x1p-96f) || x == 0.0f) {
         const uint32_t n = __float_as_uint(lv::sqrt_rn_normal(x));
         if (n != s_ref && !(is_nan(n) && is_nan(s_ref))) record(&out[7], ex + 56, i);
@@ -133,7 +164,7 @@ __global__ void check_f16_to_f32(unsigned long long *out, uint32_t *ex) {
 
 }  // namespace
 
-constexpr int kCounters = 9;
+constexpr int kCounters = 11;
 
 extern "C" int exact_check(unsigned long long *host_counts /* kCounters */, uint32_t *host_examples /* 8 x kCounters */) {
     unsigned long long *out = nullptr;

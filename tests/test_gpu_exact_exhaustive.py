@@ -13,7 +13,10 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   against the reference's integer recipe (prng.rs:137-160): all 2^32 inputs x 6 noise values;
 * sqrt_rn_normal (no rescaling) against the IEEE square root on every input of its domain;
 * pack_f16_exact against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
-  reference's fp16 quantisation never yields an infinity).
+  reference's fp16 quantisation never yields an infinity);
+* sr_f16_hw (the hardware fp16 stochastic-rounding converter) against the reference's integer
+  recipe (prng.rs:98-130) on every input of its domain (+-0 and 2^-14 <= |x| < 65504) x 6 noise
+  values, and its domain test on all 2^32 inputs.
 """
 from __future__ import annotations
 
@@ -40,9 +43,9 @@ def _lib():
 def test_exact_helpers_on_every_input():
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
-    counts = (ctypes.c_ulonglong * 9)()
-    ex = (ctypes.c_uint32 * 72)()
-    print("[case] exact helpers, 2^32 inputs x 11 checks + 2 x 2^16", flush=True)
+    counts = (ctypes.c_ulonglong * 11)()
+    ex = (ctypes.c_uint32 * 88)()
+    print("[case] exact helpers, 2^32 inputs x 18 checks + 2 x 2^16", flush=True)
     assert _lib().exact_check(counts, ex) == 0
     assert counts[0] == 0, ("f32->f16", [hex(x) for x in ex[0:8]])
     assert counts[1] == 0, ("f16->f32", [hex(x) for x in ex[8:16]])
@@ -54,3 +57,8 @@ def test_exact_helpers_on_every_input():
     assert counts[6] == 0, ("sr_bf16_hw", [hex(x) for x in ex[48:56]])
     assert counts[7] == 0, ("sqrt_rn_normal", [hex(x) for x in ex[56:64]])
     assert counts[8] == 0, ("pack_f16_exact", [hex(x) for x in ex[64:72]])
+    assert counts[9] == 0, ("sr_f16_hw", [hex(x) for x in ex[72:80]])
+    # domain size, sampled where the low 16 bits are zero: per sign, the zero and the multiples of
+    # 2^16 in [0x38800000, 0x477FE000)
+    per_sign = 1 + len(range(0x38800000, 0x477FE000, 65536))
+    assert counts[10] == 2 * per_sign
