@@ -62,10 +62,31 @@ WORKLOADS = {
 # indexing). On gfx950 FETCH_SIZE counts each 128-byte read request as 64 bytes (probe factor
 # 2.0) and WRITE_SIZE is exact (factor 1.0); TCC_EA0_RDREQ_DRAM_32B / TCC_EA0_WRREQ_WRITE_DRAM_32B
 # give the same byte totals for this kernel.
+# Keyed by (config, bound, state, master, pdt) as given on the command line; the mean of the two
+# fused-pass dispatches of a --steps 2 --warmup 1 run.
+_PROBE = dict(probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0)
 PMC_TRAFFIC = {
-    5: dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>", fetch_kib=39500422.71875, write_kib=66010502.75,
-            probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0),
+    (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
+                                                fetch_kib=39496892.5, write_kib=66010494.1, **_PROBE),
+    (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
+                                                 fetch_kib=26325899.0, write_kib=39585731.1, **_PROBE),
+    (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
+                                                fetch_kib=3725824.05, write_kib=5614386.15, **_PROBE),
+    (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
+                                                 fetch_kib=2793107.5, write_kib=3738077.1, **_PROBE),
+    (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
+                                                    fetch_kib=2792914.0, write_kib=3738077.1, **_PROBE),
+    (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
+                                                fetch_kib=965682.6, write_kib=1451866.6, **_PROBE),
+    (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 2147483648u, true>",
+                                                fetch_kib=20725.85, write_kib=27582.75, **_PROBE),
 }
+
+# Untimed steps before the timed ones unless --warmup is given. After the inputs are generated the
+# first ~30-50 ms of steps run up to 20% slower while the GPU's clocks settle (seen in kernel
+# traces of configs 3 and 4: launch times fall from 2.6 to 2.15 ms over the first 15 cfg4
+# steps); each config's default covers at least that much step time.
+DEFAULT_WARMUP = {5: 3, 4: 25, 3: 100, 2: 100}
 
 
 def workload(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",
@@ -97,15 +118,10 @@ def workload(config: int, bound: str = "coordinate", state: str = "fp32", master
     return wl
 
 
-def is_default_variant(bound: str = "coordinate", state: str = "fp32", master: str = "none", pdt: str = "") -> bool:
-    return bound == "coordinate" and state == "fp32" and master == "none" and not pdt
-
-
 def pmc_traffic_bytes(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",
                       pdt: str = ""):
-    if not is_default_variant(bound, state, master, pdt):
-        return None  # the counter runs were taken on the default workload
-    t = PMC_TRAFFIC.get(config)
+    """HBM bytes of one fused launch from the counter runs of this exact variant, or None."""
+    t = PMC_TRAFFIC.get((config, bound, state, master, pdt))
     if t is None:
         return None
     read_factor = t["probe_bytes"] / (t["probe_fetch_kib"] * 1024.0)
@@ -319,7 +335,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default: per config, covering the GPU's clock ramp)")
     ap.add_argument("--config", type=int, default=5, choices=sorted(WORKLOADS))
     ap.add_argument("--bound", default="coordinate", choices=("coordinate", "radial"),
                     help="bound_type of the optimizer (the configs use the default, coordinate)")
@@ -334,6 +351,8 @@ def main() -> int:
     ap.add_argument("--no-reserve", action="store_true", help="skip the HBM reserve/release before allocating")
     ap.add_argument("--reserve-gb", type=float, default=200.0)
     args = ap.parse_args()
+    if args.warmup is None:
+        args.warmup = DEFAULT_WARMUP[args.config]
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (across GPUs the step "
                                    "would shard each bucket by element ranges, one range per rank)",

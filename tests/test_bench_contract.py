@@ -74,7 +74,17 @@ def test_pmc_traffic_is_the_algorithmic_bytes_plus_the_count_atomics():
     traffic = bench.pmc_traffic_bytes(5)
     blocks = bench.N5 // 1024
     assert abs(traffic - (algorithmic + 32 * blocks)) / algorithmic < 5e-4
-    assert bench.pmc_traffic_bytes(3) is None
+    # the other measured variants: within 0.5% of the algorithmic bytes (+ 32 B per count atomic)
+    for key, (bpp, unit) in {(3, "coordinate", "fp32", "none", ""): (28, 1024),
+                             (4, "coordinate", "fp32", "none", ""): (14, 1024),
+                             (4, "coordinate", "param", "none", ""): (10, 2048),
+                             (4, "coordinate", "param", "none", "f16"): (10, 2048),
+                             (5, "coordinate", "param", "none", ""): (14, 2048)}.items():
+        n = {3: bench.N3, 4: bench.N4, 5: bench.N5}[key[0]]
+        got = bench.pmc_traffic_bytes(*key)
+        want = n * bpp + 32 * (n // unit)
+        assert abs(got - want) / want < 5e-3, (key, got, want)
+    assert bench.pmc_traffic_bytes(5, state="param", master="full") is None
 
 
 def test_cpu_baseline_reports_its_fields():
