@@ -264,3 +264,19 @@ def test_capturable_option_validation_and_guards(monkeypatch):
     with pytest.raises(RuntimeError, match="eager step"):
         opt.step()
     assert opt.state[q]["step"] == 3 and len(opt.state[p]) == 0
+
+
+def test_bucket_cut_rule():
+    """Buckets take params in order while their bytes fit under the cap (a bucket may end exactly
+    at the cap); a param that would take a non-empty bucket past it opens the next one, so a param
+    larger than the cap sits alone (the reference's rule, luminav.py:763-786)."""
+    cut = LuminaV._partition_into_bounded_chunks
+    mk = lambda *ns: [(i, torch.empty(n, dtype=torch.float32)) for i, n in enumerate(ns)]  # noqa: E731
+    sizes = lambda chunks: [[int(p.numel()) for _, p in c] for c in chunks]  # noqa: E731
+    assert cut([], 100) == []
+    assert sizes(cut(mk(10, 15), 100)) == [[10, 15]]          # 100 bytes: exactly at the cap
+    assert sizes(cut(mk(10, 16), 100)) == [[10], [16]]        # 104 bytes: past it
+    assert sizes(cut(mk(50, 3, 2), 100)) == [[50], [3, 2]]    # the first param alone exceeds the cap
+    assert sizes(cut(mk(3, 50, 2), 100)) == [[3], [50], [2]]
+    assert sizes(cut(mk(5, 5, 5, 5, 5, 5), 40)) == [[5, 5], [5, 5], [5, 5]]
+    assert [i for c in cut(mk(7, 1, 30, 2, 2), 40) for i, _ in c] == [0, 1, 2, 3, 4]  # order kept
