@@ -16,7 +16,7 @@ namespace lv {
 
 
 constexpr int kThreads = 256;
-constexpr uint32_t kHalf = kThreads * 4;     // a thread owns 4 consecutive elements of each half
+constexpr uint32_t kHalf = kThreads * 4;     // unit granule: 4 elements per thread; a unit is 1 or 2 of them
 
 // Halves per work unit of a unit launch. With f32 state the step is HBM-bound and 1024-element
 // units stream best (measured in one process: T2 bf16/f32 23.2 vs 23.6 ms, T1 bf16/f32 2.17 vs
@@ -453,10 +453,12 @@ __device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i)
 // Vector-path loads and stores are non-temporal: the step streams every byte exactly once, so
 // nothing is worth keeping in L2 or the MALL, and streaming hints measurably raise HBM
 // throughput for this 4-read/3-write pattern.
-// Layout of a work unit of H 1024-element halves: thread t owns elements [4t, 4t+4) of each
-// half, so every wave-wide load or store instruction covers one contiguous span (1 KiB for
-// f32, 512 B for 16-bit types). 32-bit types use `a` (first half) and `b` (second half);
-// 16-bit types pack both halves into `a` (.xy first half, .zw second half).
+// Layout of a work unit of 1024 * H elements: thread t owns the 4 * H consecutive elements
+// [4Ht, 4Ht + 4H). With H = 1 (f32 state) every wave-wide f32 access is one 16-byte load or
+// store per lane over 1 KiB; with H = 2 (16-bit state) a 16-bit stream moves its 8 elements in
+// ONE 16-byte access per lane (1 KiB per wave instruction) and an f32 stream (a master copy, an
+// f32 grad) in two adjacent ones. 32-bit types use `a` (elements 0-3) and `b` (4-7); 16-bit
+// types pack all eight into `a` (.x = elements 0-1, ..., .w = 6-7).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -472,14 +474,16 @@ __device__ __forceinline__ Raw8 load_raw(const void *base, uint64_t h0) {
     if constexpr (DT == LV_DTYPE_F32) {
         const float *f = static_cast<const float *>(base);
         r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0));
-        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + kHalf));
+        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + 4));
         else r.b = u32x4{0, 0, 0, 0};
     } else {
         const uint16_t *h = static_cast<const uint16_t *>(base);
-        u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
-        u32x2 y = u32x2{0, 0};
-        if constexpr (H == 2) y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + kHalf));
-        r.a = u32x4{x.x, x.y, y.x, y.y};
+        if constexpr (H == 2) {
+            r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(h + h0));
+        } else {
+            const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
+            r.a = u32x4{x.x, x.y, 0, 0};
+        }
         r.b = u32x4{0, 0, 0, 0};
     }
     return r;
@@ -500,7 +504,7 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
         float *f = static_cast<float *>(base);
         __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4 *>(f + h0));
         if constexpr (H == 2)
-            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + kHalf));
+            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + 4));
     } else {
         uint32_t ws[4];
 #pragma unroll
@@ -512,8 +516,8 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
             }
         }
         uint16_t *h = static_cast<uint16_t *>(base);
-        __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
-        if constexpr (H == 2) __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + kHalf));
+        if constexpr (H == 2) __builtin_nontemporal_store(u32x4{ws[0], ws[1], ws[2], ws[3]}, reinterpret_cast<u32x4 *>(h + h0));
+        else __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
     }
 }
 
@@ -778,8 +782,7 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
     return tv;
 }
 
-// Vector loads of H 1024-element halves for one thread: elements [e, e + 4) and, with H = 2,
-// [e + kHalf, e + kHalf + 4).
+// Vector loads of one thread's 4 * H consecutive elements [e, e + 4H).
 template <int MODE, int PT, int ST, int PASS, int H>
 __device__ __forceinline__ Inflight issue_at(const Desc &D, uint32_t flags, bool radial, uint64_t e) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
@@ -836,8 +839,7 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
         for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
             float ue;
-            const uint32_t jj = j < 4 ? (uint32_t)j : kHalf + (uint32_t)j - 4u;  // a constant once unrolled
-            const HashIn zj = {zb.m + jj, zb.p + jj, zb.v + jj};
+            const HashIn zj = {zb.m + (uint32_t)j, zb.p + (uint32_t)j, zb.v + (uint32_t)j};
             uint32_t act = apply_elem<MODE, PT, ST>(a, tv.k, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
                                                     mpout[j], ue);
             if constexpr (kDual) v[j] = vj;
@@ -1051,7 +1053,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     // ballots); every other path: cnt is the lane's count.
     const bool fast = cover == 0 && tv.vec_ok;
     const bool vec = fast && ubase + kUnit <= tv.n;
-    const uint64_t e0 = ubase + (uint64_t)threadIdx.x * 4u;
+    const uint64_t e0 = ubase + (uint64_t)threadIdx.x * (4u * H);
     if (vec) {
         const Inflight f = issue_at<MODE, PT, ST, PASS, H>(D, flags, radial, e0);
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
@@ -1062,7 +1064,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         // the partial last unit of an aligned tensor
 #pragma unroll
         for (int h = 0; h < H; h++) {
-            const uint64_t e = e0 + (uint64_t)h * kHalf;
+            const uint64_t e = e0 + (uint64_t)h * 4u;
             if (e + 4u <= tv.n) {
                 const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
                 process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
