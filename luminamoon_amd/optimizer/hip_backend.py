@@ -355,13 +355,15 @@ class HipStepper:
             self.workspace.discard(prep.device)
             raise RuntimeError(f"LuminaV HIP step failed ({STATUS_NAMES.get(rc, rc)}): {msg}")
 
+    def graph_workspace_bytes(self, group: Dict[str, Any], prep: PreparedStep) -> int:
+        """Workspace bytes an lv_step_multi_graph call over prep needs with the group's options."""
+        cfg = make_config(group)
+        return int(load_library().lv_workspace_bytes_for(ctypes.byref(cfg), prep.items, prep.n))
+
     def graph_workspace(self, group: Dict[str, Any], prep: PreparedStep) -> torch.Tensor:
         """A zeroed workspace of its own for lv_step_multi_graph calls over prep (graph replays
         must not share the stepper's workspace with eager calls on other streams)."""
-        lib = load_library()
-        cfg = make_config(group)
-        need = int(lib.lv_workspace_bytes_for(ctypes.byref(cfg), prep.items, prep.n))
-        return torch.zeros(max(need, 256), dtype=torch.uint8, device=prep.device)
+        return torch.zeros(max(self.graph_workspace_bytes(group, prep), 256), dtype=torch.uint8, device=prep.device)
 
     def launch_graph(self, group: Dict[str, Any], prep: PreparedStep, record: torch.Tensor,
                      workspace: torch.Tensor) -> None:

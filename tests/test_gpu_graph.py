@@ -266,3 +266,32 @@ def test_capturable_optimizer_graph_replays_match_eager(kw):
     ob.step()
     torch.cuda.synchronize()
     check(9)
+
+
+def test_capturable_group_follows_an_option_change():
+    """Switching a capturable group to the radial bound between eager steps grows its workspace
+    (radial unit records) and the steps stay equal to a plain LuminaV's, bit for bit."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    a, b = _models(torch.float32)
+    oa = LuminaV(a.parameters(), lr=1e-2, buffer=1, capturable=True)
+    ob = LuminaV(b.parameters(), lr=1e-2, buffer=1)
+    pa, pb = list(a.parameters()), list(b.parameters())
+    for s in range(1, 6):
+        if s == 4:
+            for o in (oa, ob):
+                o.param_groups[0]["bound_type"] = "radial"
+        gen = torch.Generator(device="cuda").manual_seed(300 + s)
+        for x, y in zip(pa, pb):
+            g = torch.randn(x.shape, generator=gen, device="cuda") * 1e-2
+            x.grad = g.clone()
+            y.grad = g
+        print(f"[case] capturable option change, step {s}", flush=True)
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (x, y) in enumerate(zip(pa, pb)):
+            assert torch.equal(x, y), f"step {s} param {i}"
+            for k in ("exp_avg", "scratch"):
+                assert torch.equal(oa.state[x][k], ob.state[y][k]), f"step {s} param {i} {k}"
