@@ -24,7 +24,7 @@ from tests.parity_util import TensorSet, group_dict, oracle_config
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 96
+N_CASES = 400
 
 
 def _draw(case: int):
