@@ -295,3 +295,63 @@ def test_capturable_group_follows_an_option_change():
             assert torch.equal(x, y), f"step {s} param {i}"
             for k in ("exp_avg", "scratch"):
                 assert torch.equal(oa.state[x][k], ob.state[y][k]), f"step {s} param {i} {k}"
+
+
+def test_two_capturable_groups_in_one_graph(monkeypatch):
+    """Two capturable param groups (different lr and buffer modes) set up in the same eager
+    step() and captured in one graph: setting up the second group leaves the first one's set-up
+    valid, and every replay equals a plain LuminaV's eager steps bit for bit. Stepping a
+    non-capturable group inside the capture raises."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    a, b = _models(torch.bfloat16)
+    pa, pb = list(a.parameters()), list(b.parameters())
+    groups = lambda ps, cap: [dict(params=ps[:2], lr=1e-2, buffer="T2", capturable=cap),  # noqa: E731
+                              dict(params=ps[2:], lr=3e-3, buffer=1, capturable=cap)]
+    oa = LuminaV(groups(pa, True))
+    ob = LuminaV(groups(pb, False))
+    static = [torch.zeros_like(p) for p in pa]
+    for p, g in zip(pa, static):
+        p.grad = g
+
+    def feed(step):
+        gen = torch.Generator(device="cuda").manual_seed(500 + step)
+        for gs, q in zip(static, pb):
+            g = (torch.randn(q.shape, generator=gen, device="cuda") * 1e-2).to(q.dtype)
+            gs.copy_(g)
+            q.grad = g
+
+    def check(step):
+        for i, (x, y) in enumerate(zip(pa, pb)):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16)), f"step {step} param {i}"
+            assert torch.equal(oa.state[x]["exp_avg"], ob.state[y]["exp_avg"]), f"step {step} param {i} exp_avg"
+            assert int(oa.state[x]["step"]) == ob.state[y]["step"] == step
+
+    for s in (1, 2):
+        feed(s)
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
+    graph = torch.cuda.CUDAGraph()
+    print("[case] two capturable groups, one graph", flush=True)
+    with torch.cuda.graph(graph):
+        oa.step()
+    torch.cuda.synchronize()
+    check(2)
+    for s in range(3, 7):
+        feed(s)
+        graph.replay()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
+    oc = LuminaV([dict(params=pa[:2], capturable=True), dict(params=pa[2:], capturable=False)])
+    oc.step()  # eager set-up of the capturable group, the other steps eagerly
+    torch.cuda.synchronize()
+    # as if capturing (the guard is a host check; no graph is started for it)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="without capturable=True"):
+        oc.step()
+    monkeypatch.undo()
+    torch.cuda.synchronize()
