@@ -510,7 +510,8 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
 #pragma unroll
         for (int k = 0; k < 2 * H; k++) {
             if constexpr (DT == LV_DTYPE_BF16) {
-                ws[k] = (f_bits(in[2 * k]) >> 16) | (f_bits(in[2 * k + 1]) & 0xFFFF0000u);
+                // the high halves of both values in one v_perm_b32 (bytes 2-3 of each)
+                ws[k] = __builtin_amdgcn_perm(f_bits(in[2 * k + 1]), f_bits(in[2 * k]), 0x07060302u);
             } else {
                 ws[k] = pack_f16_exact(in[2 * k], in[2 * k + 1]);
             }
