@@ -101,8 +101,9 @@ int lv_version(void);
  * not overlap in time (stream-ordered calls on one stream are fine). After a call that returned
  * LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero it again before reusing it.
  * Layout of one call: 195 KiB of inline count slots (48 tensors x 65 slots x 64 B) and 2 KiB of
- * radial tickets and running sums; with more than 48 tensors, table count slots
- * (min(64, units) + 1 slots of 64 B per tensor, units of 1024 elements); with the radial bound,
+ * radial tickets and running sums; with more than 48 tensors in a launch class, table count
+ * slots (per tensor, one fold slot plus the smallest power of two of slots that keeps every slot
+ * at <= 64 blocks, at most 64; 64 B each); with the radial bound,
  * 32 B of chunk record per 4096 units and 20 B of unit record per unit, up to one piece of 2^22
  * units (80 MiB). No radial space is needed without the radial bound. */
 

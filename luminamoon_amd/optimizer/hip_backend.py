@@ -164,23 +164,31 @@ def make_config(group: Dict[str, Any]) -> LvConfig:
 class _Workspace:
     """Per-device workspace (cautious count slots, radial records), allocated zero-filled and
     grown to the largest call seen; every call leaves all of it zero again, so calls of any
-    layout share it."""
+    layout share it. A replaced buffer is kept, not freed: launches already queued (possibly on
+    another stream, which torch's allocator would not wait for) may still use it. Growth at least
+    doubles, so the kept buffers total less than the live one."""
 
     def __init__(self) -> None:
         self._bufs: Dict[Any, torch.Tensor] = {}
+        self._kept: List[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
         buf = self._bufs.get(device)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._kept.append(buf)
+                nbytes = max(nbytes, 2 * buf.numel())
             # torch's caching allocator returns 512-byte aligned blocks (the library needs 256)
             buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
             self._bufs[device] = buf
         return buf
 
     def discard(self, device: torch.device) -> None:
-        """Drops the device's buffer: after a failed launch its count slots may hold a partial
+        """Retires the device's buffer: after a failed launch its count slots may hold a partial
         launch's counts, so the next call starts from a fresh zero-filled one."""
-        self._bufs.pop(device, None)
+        buf = self._bufs.pop(device, None)
+        if buf is not None:
+            self._kept.append(buf)
 
 
 # lv_tensor packed little-endian: 6 pointers, numel, step, param_index, 4 x int32, index_base,
