@@ -78,8 +78,8 @@ PMC_TRAFFIC = {
                                                     fetch_kib=2792914.0, write_kib=3738077.1, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
                                                 fetch_kib=965682.6, write_kib=1451866.6, **_PROBE),
-    (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 2147483648u, true>",
-                                                fetch_kib=20725.85, write_kib=27582.75, **_PROBE),
+    (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
+                                                fetch_kib=20710.56, write_kib=27582.38, **_PROBE),
 }
 
 # Untimed steps before the timed ones unless --warmup is given. After the inputs are generated the
