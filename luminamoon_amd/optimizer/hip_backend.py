@@ -205,13 +205,15 @@ class PreparedStep:
     swap a tensor's grad (same shape/dtype/device, contiguous; checked) and set step counters;
     everything else stays as validated."""
 
-    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index", "_steps", "ws_need")
+    __slots__ = ("buf", "items", "n", "device", "numels", "gdtypes", "index", "_steps", "_gptrs", "ws_need")
 
     def __init__(self, buf: bytearray, n: int, device: torch.device, numels: List[int], gdtypes: List[Any]):
         self.buf = buf
         self.items = (LvTensor * n).from_buffer(buf) if n else None
         # the step field of every record, as one strided u64 view of the packed buffer
         self._steps = np.frombuffer(buf, dtype=np.uint64)[_STEP_OFFSET // 8::_TENSOR.size // 8] if n else None
+        # the grad pointer of every record, for re-pointing all grads at once (set_grads)
+        self._gptrs = np.frombuffer(buf, dtype=np.uint64)[_GRAD_OFFSET // 8::_TENSOR.size // 8] if n else None
         self.n = n
         self.device = device
         self.numels = numels
@@ -225,6 +227,17 @@ class PreparedStep:
                 or g.numel() != self.numels[i] or not g.is_contiguous()):
             return False
         struct.pack_into("<Q", self.buf, i * _TENSOR.size + _GRAD_OFFSET, g.data_ptr())
+        return True
+
+    def set_grads(self, grads: Sequence[torch.Tensor], ptrs: Sequence[int]) -> bool:
+        """Point every descriptor at its grad (ptrs[i] = grads[i].data_ptr()) after checking them
+        all as set_grad does; False (nothing changed) if any does not fit."""
+        idx = self.index
+        for g, dt, n in zip(grads, self.gdtypes, self.numels):
+            if (g is None or g.dtype is not dt or g.layout is not torch.strided or g.get_device() != idx
+                    or g.numel() != n or not g.is_contiguous()):  # get_device() is -1 off the GPU
+                return False
+        self._gptrs[:] = ptrs
         return True
 
     def set_step(self, i: int, step: int) -> None:

@@ -179,7 +179,8 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     """Unfused groups reuse their packed descriptors while only grads and step counters change.
     Every way the plan can go stale is driven here -- grads updated in place, new grad tensors,
     a param losing and regaining its grad, param storage replaced, load_state_dict, a changed
-    hyper-parameter -- and each step is compared bit for bit with the oracle."""
+    hyper-parameter, new grads while the old ones live on, one grad replaced -- and each step is
+    compared bit for bit with the oracle."""
     _need_gpu()
     from luminamoon_amd import LuminaV
     from tests.parity_util import TensorSet, assert_bitwise, oracle_config, seeded_tensor
@@ -199,6 +200,7 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
 
     opt._run_unfused_plan = spy
     host_steps = [0] * len(sizes)
+    kept = []
 
     def run(s, mode, expect_fast):
         grads = [seeded_tensor(n, 900 + 10 * s + i, 1e-3, torch.bfloat16) for i, n in enumerate(sizes)]
@@ -208,10 +210,12 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
         for i, p in enumerate(params):
             if not active[i]:
                 p.grad = None
-            elif mode == "inplace" and p.grad is not None:
+            elif (mode == "inplace" or (mode == "one" and i > 0)) and p.grad is not None:
                 p.grad.copy_(grads[i].cuda())
             else:
                 p.grad = grads[i].cuda()
+                if mode == "keep":  # the previous grads stay alive: new ids, no weakref death
+                    kept.append(p.grad)
         before = used["fast"]
         opt.step()
         torch.cuda.synchronize()
@@ -273,6 +277,11 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     opt.state = defaultdict(dict, {k: dict(v) for k, v in opt.state.items()})
     run(19, "new", False)
     run(20, "new", True)
+    # every grad a new tensor while the old ones stay alive (all re-pointed at once), then one
+    # grad replaced and the rest updated in place (re-pointed one by one)
+    run(21, "keep", True)
+    run(22, "keep", True)
+    run(23, "one", True)
 
 
 def test_unfused_duplicate_param_raises_like_the_native_seam():
