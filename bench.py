@@ -69,13 +69,13 @@ PMC_TRAFFIC = {
     (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
                                                 fetch_kib=39496892.5, write_kib=66010494.1, **_PROBE),
     (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=26325899.0, write_kib=39585731.1, **_PROBE),
+                                                 fetch_kib=26325903.3, write_kib=39585731.5, **_PROBE),
     (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
                                                 fetch_kib=3725824.05, write_kib=5614386.15, **_PROBE),
     (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=2793107.5, write_kib=3738077.1, **_PROBE),
+                                                 fetch_kib=2793025.2, write_kib=3738077.3, **_PROBE),
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
-                                                    fetch_kib=2792914.0, write_kib=3738077.1, **_PROBE),
+                                                    fetch_kib=2792919.3, write_kib=3738077.1, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
                                                 fetch_kib=965682.6, write_kib=1451866.6, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
