@@ -915,7 +915,7 @@ struct LuminaVTritonEngine {
 
 extern "C" {
 
-int lv_version(void) { return 300; }
+int lv_version(void) { return 400; }
 
 size_t lv_workspace_bytes(int n_tensors) {
     // any call with n_tensors tensors: every tensor with kSlots count slots in a table launch, and

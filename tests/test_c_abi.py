@@ -50,7 +50,7 @@ def _chunk_bytes(units):
 
 
 def test_version_and_workspace(lib):
-    assert lib.lv_version() >= 300
+    assert lib.lv_version() >= 400  # 0.4: lv_step_multi_graph and the standalone engine API
     ws = lib.lv_workspace_bytes(1)
     assert ws % 256 == 0
     # the launches of a call reuse per-launch regions, so the size does not grow up to 48 tensors
