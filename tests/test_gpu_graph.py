@@ -355,3 +355,70 @@ def test_two_capturable_groups_in_one_graph(monkeypatch):
         oc.step()
     monkeypatch.undo()
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_capturable_random_options(case):
+    """Seeded random option draws (mode, param dtype, state precision, master weights, cautious,
+    stochastic rounding, coordinate or radial bound, weight decay, fused pass, lr, seed; 1-60
+    ragged tensors) through LuminaV(capturable=True): two eager steps, a captured graph, four
+    replays with new gradients; every buffer, the scratch and the step count equal a plain
+    LuminaV's eager steps bit for bit after each step."""
+    _need_gpu()
+    import warnings
+
+    from luminamoon_amd import LuminaV
+
+    rng = np.random.default_rng(7000 + case)
+    pick = lambda xs: xs[int(rng.integers(len(xs)))]  # noqa: E731
+    dt = pick([torch.float32, torch.bfloat16, torch.float16])
+    kw = dict(buffer=pick([1, 2, "T1", "T2"]), cautious=bool(rng.random() < 0.7),
+              stochastic_rounding=bool(rng.random() < 0.7), bound_type=pick(["coordinate", "radial"]),
+              weight_decay=float(pick([0.0, 0.01, 0.08])), lr=float(10 ** rng.uniform(-4, -2)),
+              state_precision=pick(["fp32", "param"]), fused_single_pass=bool(rng.random() < 0.8),
+              master_weights=pick(["none", "semi", "full"]) if dt != torch.float32 else "none",
+              seed=int(rng.integers(0, 2**31)))
+    nten = int(pick([1, 3, 7, 60]))
+    torch.manual_seed(case)
+    shapes = [(int(rng.integers(1, 3000)),) for _ in range(nten)]
+    pa = [torch.nn.Parameter((torch.randn(s, device="cuda") * 0.02).to(dt)) for s in shapes]
+    pb = [torch.nn.Parameter(p.detach().clone()) for p in pa]
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        oa = LuminaV(pa, capturable=True, **kw)
+        ob = LuminaV(pb, **kw)
+    static = [torch.zeros_like(p) for p in pa]
+    for p, g in zip(pa, static):
+        p.grad = g
+    print(f"[case] capturable random {case}: {dt} {nten} tensors {kw}", flush=True)
+
+    def feed(s):
+        gen = torch.Generator(device="cuda").manual_seed(case * 100 + s)
+        for gs, q in zip(static, pb):
+            g = (torch.randn(q.shape, generator=gen, device="cuda") * 1e-3).to(q.dtype)
+            gs.copy_(g)
+            q.grad = g
+
+    def check(s):
+        for i, (x, y) in enumerate(zip(pa, pb)):
+            assert torch.equal(x.detach().view(torch.uint8), y.detach().view(torch.uint8)), f"step {s} p[{i}]"
+            for k in ("exp_avg", "exp_avg_sq", "master_param", "scratch"):
+                if k in ob.state[y]:
+                    assert torch.equal(oa.state[x][k].view(torch.uint8), ob.state[y][k].view(torch.uint8)), f"step {s} {k}[{i}]"
+            assert int(oa.state[x]["step"]) == ob.state[y]["step"] == s
+
+    for s in (1, 2):
+        feed(s)
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        oa.step()
+    for s in range(3, 7):
+        feed(s)
+        graph.replay()
+        ob.step()
+        torch.cuda.synchronize()
+        check(s)
