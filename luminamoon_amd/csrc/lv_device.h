@@ -238,13 +238,16 @@ __device__ __forceinline__ float rne_bf16(float v) {
 
 // f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
 
-// prng.rs:98-130. On the hardware converter's domain (sr_f16_hw in lv_exact.h: +-0 and fp16
-// normal results below 65504) the noise prng(z0) & 0x1FFF goes in bits 31..19 of its random
-// operand; when any active lane of the wave is outside that domain, the wave takes the integer
-// recipe below (the one the reference states).
+// prng.rs:98-130. Returns an f32 register whose LOW half holds the fp16 bits (the high half is
+// not defined: store the low half, do not compute with it). On the hardware converter's domain
+// (sr_f16_hw in lv_exact.h: +-0 and fp16 normal results below 65504) the noise prng(z0) & 0x1FFF
+// goes in bits 31..19 of its random operand; when any active lane of the wave is outside that
+// domain, the wave takes the integer recipe below (the one the reference states).
 __device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!sr_f16_hw_domain(v)) == 0, 1))
-        return sr_f16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)) << 3);
+    // the converter's result, replaced below in the rare waves that need the recipe (computing it
+    // first lets both paths leave the result in one register)
+    const float hw = sr_f16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)) << 3);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!sr_f16_hw_domain(v)) == 0, 1)) return hw;
     int32_t p = (int32_t)f_bits(v);
     int32_t a = p & 0x7FFFFFFF;
     int32_t ex = (a >> 23) & 0xFF;
@@ -255,20 +258,23 @@ __device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
     int32_t noise = prng(z0) & mask;
     int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
     int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
-    // The reference converts sign | r to fp16 and back (prng.rs:129). That is the identity here,
-    // because sign | r is already an fp16 value. r is one of:
+    // The reference converts sign | r to fp16 and back (prng.rs:129). sign | r is already an fp16
+    // value, so that round trip is the identity and its fp16 bits come from one exact conversion
+    // (pack_f16_exact). r is one of:
     // - 0, or 65504;
     // - the sign bit alone (-0.0), when a NaN's magnitude plus the noise wraps past 2^31;
     // - a value with its (13 + sub) low bits clear. For ex >= 113 that leaves 10 fraction bits
     //   below 65504 (an fp16 normal). For 103 <= ex <= 112 it leaves a multiple of 2^-24 below
     //   2^-13 (fp16 subnormals and the lowest normal binade).
-    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
+    return bits_f(pack_f16_exact(bits_f((uint32_t)((p & (int32_t)0x80000000u) | r)), 0.0f));
 }
 
-__device__ __forceinline__ float rne_fp16(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
+// prng.rs:29-67: fp16 bits in the low half (high half zero), like sr_fp16.
+__device__ __forceinline__ float rne_fp16(float v) { return bits_f(f32_to_f16_rne(v)); }
 
 // prng.rs:180-195; dtype is a compile-time constant at every call site. z0 is the element's
-// hash input for the buffer's seed (offset + seed + kPrngAdd).
+// hash input for the buffer's seed (offset + seed + kPrngAdd). The result is only stored:
+// bf16 results hold the bf16 bits in the high half, fp16 results the fp16 bits in the low half.
 template <int DT>
 __device__ __forceinline__ float quantize(float v, uint32_t z0, bool sr) {
     if constexpr (DT == LV_DTYPE_BF16) {
@@ -285,6 +291,25 @@ __device__ __forceinline__ float quantize(float v, uint32_t z0, bool sr) {
 // in it, one compare per element and a scalar branch replace the general sequence. The general
 // sequence still runs, for the whole wave, whenever any lane needs it, so results are unchanged.
 __device__ __forceinline__ bool wave_all(bool c) { return __builtin_amdgcn_ballot_w64(!c) == 0; }
+
+// How an element's cautious mask bit is counted: not at all (SINGLE pass), into the lane's own
+// count, or into the wave's count (every lane of the wave present; cnt is the same in every lane).
+enum : int { kTallyNone = 0, kTallyLane = 1, kTallyWave = 2 };
+
+// Adds the mask bit where it is computed. For the wave count the empty asm holds the ballot's
+// popcount in an SGPR at this point: otherwise the compiler sinks every element's ballot past the
+// wave-uniform branches that follow and carries each lane mask across them through a VGPR (a
+// v_cndmask and a v_cmp per element).
+template <int TALLY>
+__device__ __forceinline__ void tally(uint32_t &cnt, bool active) {
+    if constexpr (TALLY == kTallyWave) {
+        uint32_t c = (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(active));
+        asm volatile("" : "+s"(c));
+        cnt += c;
+    } else if constexpr (TALLY == kTallyLane) {
+        cnt += active ? 1u : 0u;
+    }
+}
 
 // math.rs:4-11. |g| < 1e38 is false for NaN and +-inf, so one compare also covers is_finite;
 // on that path g is not NaN and med3 is exactly the clamp. |g| <= 1e18 (false for NaN) leaves g
@@ -308,13 +333,32 @@ __device__ __forceinline__ float sqrt_cr(float x) {
     return sqrt_rn(x);
 }
 
-// math.rs:83-118 -- [13/6] Pade tanh, Horner with fma.
-__device__ __forceinline__ float tanh_pade(float x_in) {
+// Three constants of tanh_pade: the clamp bound and the leading coefficients of its numerator and
+// denominator. An fma or median instruction takes at most one literal or SGPR operand on gfx950,
+// so each of these needs a VGPR; the vector path passes copies made once per unit (in_vgpr), which
+// the compiler would otherwise re-create with a v_mov at every call.
+struct PadeK {
+    float hi, p0, q0;
+};
+constexpr PadeK kPade = {7.9988117f, -2.7607684e-16f, 1.1982584e-6f};
+
+// A wave-uniform value copied to a VGPR once. A VOP3 instruction reads at most one SGPR on gfx950,
+// so an fma with two uniform operands needs one of them in a VGPR; the asm copy cannot be
+// re-created, where the compiler would otherwise re-create it (a v_mov) for every element.
+__device__ __forceinline__ float in_vgpr(float x) {
+    float r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
+    return r;
+}
+
+// math.rs:83-118 -- [13/6] Pade tanh, Horner with fma. c holds kPade's values.
+__device__ __forceinline__ float tanh_pade(float x_in, const PadeK &c = kPade) {
     if (__builtin_isnan(x_in)) return bits_f(0x7FC00000u);  // Rust f32::NAN
-    float x = rclamp(x_in, -7.9988117f, 7.9988117f);
+    // x_in is not NaN here, so the median of three is exactly the clamp
+    float x = __builtin_amdgcn_fmed3f(x_in, -7.9988117f, c.hi);
     float x2 = x * x;
-    float p = __builtin_fmaf(-2.7607684e-16f, x2, 2.000188e-13f);
-    float q = __builtin_fmaf(1.1982584e-6f, x2, 1.1853471e-4f);
+    float p = __builtin_fmaf(c.p0, x2, 2.000188e-13f);
+    float q = __builtin_fmaf(c.q0, x2, 1.1853471e-4f);
     p = __builtin_fmaf(p, x2, -8.604672e-11f);
     q = __builtin_fmaf(q, x2, 2.2684346e-3f);
     p = __builtin_fmaf(p, x2, 5.122297e-8f);
@@ -327,25 +371,25 @@ __device__ __forceinline__ float tanh_pade(float x_in) {
 
 // math.rs:162-186
 template <bool TRI>
-__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio) {
+__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio, const PadeK &c = kPade) {
     if constexpr (TRI) {
         float b = ratio * (fabsf(p_init) + 1.0e-2f);
         float bb = b * (b + fabsf(step));
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
         float b = ratio * sqrt_cr(__builtin_fmaf(p_init, p_init, 1.0e-4f));
-        return b * tanh_pade(step / b);
+        return b * tanh_pade(step / b, c);
     }
 }
 
 template <bool TRI>
-__device__ __forceinline__ float fp16_safety_bound(float step, float p_init) {
+__device__ __forceinline__ float fp16_safety_bound(float step, float p_init, const PadeK &c = kPade) {
     float b = __builtin_fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);
     if constexpr (TRI) {
         float bb = b * (b + fabsf(step));
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
-        return b * tanh_pade(step / b);
+        return b * tanh_pade(step / b, c);
     }
 }
 
@@ -385,11 +429,19 @@ __device__ __forceinline__ float u64_to_f32_rn(uint64_t x) {
     return ldexpf((float)(uint32_t)mant, sh);
 }
 
+// Uniform constants an element's update reads from VGPRs: a.eps and the tanh constants (kPade).
+// The vector path copies them to VGPRs once per unit (lane_consts); the per-element path uses
+// them as they are.
+struct LaneK {
+    float eps;
+    PadeK pade;
+};
+
 // u, m_new, v_new for one element.
 // CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
 template <int MODE>
-__device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, bool clamp_v, float g, float m, float v,
-                                           float &m_new, float &v_new) {
+__device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, const LaneK &lk, bool clamp_v, float g,
+                                           float m, float v, float &m_new, float &v_new) {
     m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
     if constexpr (MODE == LV_BUFFER_DUAL) {
         float clm = __builtin_fmaf(a.b1, m_new, a.omb1 * g);
@@ -397,13 +449,13 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, b
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
         float sigma = __builtin_fmaf(sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), k.c1, k.c2);
-        return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f));
+        return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f), lk.pade);
     } else if constexpr (MODE == LV_BUFFER_T2) {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
         float diff = clamp_defect(g - m);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
-        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), lk.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
         float env = __builtin_fmaf(k.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
@@ -411,7 +463,7 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, b
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
         float diff = clamp_defect(g - m);
-        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), a.eps);
+        float env0 = __builtin_fmaf(a.b1sq, fabsf(m), lk.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
         v_new = 0.0f;
@@ -439,7 +491,7 @@ __device__ __forceinline__ void store1(void *base, uint64_t i, float x) {
     } else if constexpr (DT == LV_DTYPE_BF16) {
         static_cast<uint16_t *>(base)[i] = (uint16_t)(f_bits(x) >> 16);
     } else {
-        static_cast<uint16_t *>(base)[i] = (uint16_t)pack_f16_exact(x, x);  // x is an f16 value
+        static_cast<uint16_t *>(base)[i] = (uint16_t)f_bits(x);  // fp16 bits in the low half
     }
 }
 
@@ -495,9 +547,9 @@ __device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t 
     return load_raw<LV_DTYPE_BF16, H>(base, h0);  // 16-bit types share the raw layout
 }
 
-// Stores 4 * H values in the same layout; 16-bit values are already exact in the target
-// type (quantised), so bf16 is a truncation of the high half (worker.rs:55-63) and f16 an exact
-// conversion (pack_f16_exact).
+// Stores 4 * H values in the same layout; 16-bit values are already quantised: a bf16 value is
+// the high half of its register (worker.rs:55-63), an fp16 value the low half (sr_fp16,
+// rne_fp16).
 template <int DT, int H>
 __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
     if constexpr (DT == LV_DTYPE_F32) {
@@ -513,7 +565,8 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
                 // the high halves of both values in one v_perm_b32 (bytes 2-3 of each)
                 ws[k] = __builtin_amdgcn_perm(f_bits(in[2 * k + 1]), f_bits(in[2 * k]), 0x07060302u);
             } else {
-                ws[k] = pack_f16_exact(in[2 * k], in[2 * k + 1]);
+                // the low halves (bytes 0-1 of each)
+                ws[k] = __builtin_amdgcn_perm(f_bits(in[2 * k + 1]), f_bits(in[2 * k]), 0x05040100u);
             }
         }
         uint16_t *h = static_cast<uint16_t *>(base);
@@ -575,19 +628,20 @@ __device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
 }
 
 // Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
-// Returns the cautious mask bit; u_eff is the (masked) direction whose square feeds the radial
-// norm (dual.rs:176-180).
-template <int MODE, int PT, int ST>
-__device__ __forceinline__ uint32_t apply_elem(const Args &a, const StepCoeffs &k, uint32_t flags, const HashIn &z,
-                                               float cs, float bs, float p_init, float g_raw, float &m_io,
-                                               float &v_io, float &p_out, float &mp_out, float &u_eff) {
+// Counts the cautious mask bit into cnt (TALLY); u_eff is the (masked) direction whose square
+// feeds the radial norm (dual.rs:176-180).
+template <int MODE, int PT, int ST, int TALLY>
+__device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags, const HashIn &z,
+                                           float cs, float bs, float p_init, float g_raw, float &m_io,
+                                           float &v_io, float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     const bool sr = flags & kFSR;
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, k, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
     bool active = (u * g) > 0.0f;
+    tally<TALLY>(cnt, active);
     float m_mask = active ? 1.0f : 0.0f;
     m_io = quantize<ST>(m_new, z.m, sr);
     if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
@@ -595,8 +649,8 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, const StepCoeffs &
     float delta = (flags & kFCautious) ? u_eff * cs : u;
     float step = a.lr * delta;
     if (flags & kFRadial) step *= bs;
-    else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio);
-    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init);
+    else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio, lk.pade);
+    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init, lk.pade);
     float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
     float p_upd = p_dec - step;
     if (flags & kFMaster) {
@@ -605,19 +659,18 @@ __device__ __forceinline__ uint32_t apply_elem(const Args &a, const StepCoeffs &
     } else {
         p_out = quantize<PT>(p_upd, z.p, sr);
     }
-    return active ? 1u : 0u;
 }
 
 // Counting path for one element (dual.rs:279-303, dual.rs:720-746, tdclm.rs:232-248).
-template <int MODE>
-__device__ __forceinline__ uint32_t count_elem(const Args &a, const StepCoeffs &k, uint32_t flags, float g_raw, float m, float v,
-                                               float &u_eff) {
+template <int MODE, int TALLY>
+__device__ __forceinline__ void count_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags, float g_raw,
+                                           float m, float v, float &u_eff, uint32_t &cnt) {
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, k, flags & kFClampV, g, m, v, m_new, v_new);
+    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m, v, m_new, v_new);
     bool active = (u * g) > 0.0f;
+    tally<TALLY>(cnt, active);
     u_eff = (flags & kFCautious) ? u * (active ? 1.0f : 0.0f) : u;
-    return active ? 1u : 0u;
 }
 
 // ------------------------------------------------------------------ scratch finalisation
@@ -799,6 +852,20 @@ __device__ __forceinline__ Inflight issue_at(const Desc &D, uint32_t flags, bool
     return f;
 }
 
+// The LaneK of the vector path: VGPR copies of the constants that mode reads with another uniform
+// operand. eps is read by T1, T2 and TD-CLM, the tanh constants by CLM and TD-CLM (tanh_pade).
+// The two-buffer modes with 16-bit state (T2, CLM) keep them as they are: there the extra VGPRs
+// would cost some of their kernels a wave of occupancy.
+template <int MODE, int H>
+__device__ __forceinline__ LaneK lane_consts(const Args &a) {
+    LaneK lk{a.eps, kPade};
+    if constexpr (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_TDCLM || (MODE == LV_BUFFER_T2 && H == 1))
+        lk.eps = in_vgpr(a.eps);
+    if constexpr (MODE == LV_BUFFER_TDCLM || (MODE == LV_BUFFER_DUAL && H == 1))
+        lk.pade = PadeK{in_vgpr(kPade.hi), in_vgpr(kPade.p0), in_vgpr(kPade.q0)};
+    return lk;
+}
+
 // Update (or count) the 4 * H elements loaded by issue_at(e0) and store them. BALLOT: every lane
 // of the wave is here, and cnt accumulates the wave's count (the same in every lane) from ballots;
 // otherwise cnt accumulates the lane's own count.
@@ -807,8 +874,10 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
                                            const Inflight &cur, uint64_t e0, uint32_t &cnt, double &su, double &sp) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    constexpr int kTally = !kCounting ? kTallyNone : (BALLOT ? kTallyWave : kTallyLane);
     const int gdt = (int)((flags >> 8) & 3u);
     const bool master = flags & kFMaster;
+    const LaneK lk = lane_consts<MODE, H>(a);
     float g[8], m[8], v[8];
     decode_raw_dyn<H>(gdt, cur.g, g);
     decode_raw<ST, H>(cur.m, m);
@@ -822,9 +891,7 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
             float ue;
-            const uint32_t act = count_elem<MODE>(a, tv.k, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue);
-            if constexpr (BALLOT) cnt += (uint32_t)__popcll(__ballot(act));
-            else cnt += act;
+            count_elem<MODE, kTally>(a, tv.k, lk, flags, g[j], m[j], kDual ? v[j] : 0.0f, ue, cnt);
             if (radial) {
                 su += (double)(ue * ue);
                 sp += (double)(pin[j] * pin[j]);
@@ -841,16 +908,12 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
             float vj = kDual ? v[j] : 0.0f;
             float ue;
             const HashIn zj = {zb.m + (uint32_t)j, zb.p + (uint32_t)j, zb.v + (uint32_t)j};
-            uint32_t act = apply_elem<MODE, PT, ST>(a, tv.k, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
-                                                    mpout[j], ue);
+            apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+                                             mpout[j], ue, cnt);
             if constexpr (kDual) v[j] = vj;
-            if constexpr (kCounting) {
-                if constexpr (BALLOT) cnt += (uint32_t)__popcll(__ballot(act));
-                else cnt += act;
-                if (radial) {
-                    su += (double)(ue * ue);
-                    sp += (double)(pin[j] * pin[j]);
-                }
+            if (kCounting && radial) {
+                su += (double)(ue * ue);
+                sp += (double)(pin[j] * pin[j]);
             }
         }
         store_raw<PT, H>(D.p, e0, pout);
@@ -885,7 +948,7 @@ __device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const
         float v = kDual ? load1<ST>(D.v, i) : 0.0f;
         if constexpr (PASS == kCount) {
             float ue;
-            cnt += count_elem<MODE>(a, tv.k, flags, g, m, v, ue);
+            count_elem<MODE, kTallyLane>(a, tv.k, LaneK{a.eps, kPade}, flags, g, m, v, ue, cnt);
             if (radial) {
                 float pin = master ? D.mp[i] : load1<PT>(D.p, i);
                 su += (double)(ue * ue);
@@ -894,20 +957,18 @@ __device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const
         } else {
             float pin = master ? D.mp[i] : load1<PT>(D.p, i);
             float pout, mpout, ue;
-            uint32_t act = apply_elem<MODE, PT, ST>(a, tv.k, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs,
-                                                    pin, g, m, v, pout, mpout, ue);
+            apply_elem<MODE, PT, ST, kCounting ? kTallyLane : kTallyNone>(
+                a, tv.k, LaneK{a.eps, kPade}, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs, pin, g, m, v,
+                pout, mpout, ue, cnt);
             if (!inactive) {
                 store1<PT>(D.p, i, pout);
                 if (master) D.mp[i] = mpout;
                 store1<ST>(D.m, i, m);
                 if constexpr (kDual) store1<ST>(D.v, i, v);
             }
-            if constexpr (kCounting) {
-                cnt += act;
-                if (radial) {
-                    su += (double)(ue * ue);
-                    sp += (double)(pin * pin);
-                }
+            if (kCounting && radial) {
+                su += (double)(ue * ue);
+                sp += (double)(pin * pin);
             }
         }
     }

@@ -40,7 +40,9 @@
 // bits 31..19. Outside the domain the two differ and callers take the integer recipe: below 2^-14
 // the reference widens both the discarded field and the noise to 13 + k bits where the converter
 // keeps 13 (ignoring the discarded bits below them), and at the top the reference saturates to
-// 65504 where the converter overflows to infinity. The result is the fp16 value as an f32.
+// 65504 where the converter overflows to infinity. The result is an f32 register whose LOW half
+// holds the fp16 bits; its high half keeps v's high bits (store the low half, do not compute
+// with it), which spares clearing the converter's destination.
 //
 // The fp16 conversions need fp16 denormals enabled, the HIP default for gfx950 code objects.
 #pragma once
@@ -121,14 +123,15 @@ __device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
 
 __device__ __forceinline__ bool sr_f16_hw_domain(float v) {
     const float a = __builtin_fabsf(v);
-    return a < 65504.0f && (a >= 0x1p-14f || a == 0.0f);  // false for NaN
+    // false for NaN; & and | (not && and ||) keep the three compares free of branches
+    return (a < 65504.0f) & ((a >= 0x1p-14f) | (a == 0.0f));
 }
 
 __device__ __forceinline__ float sr_f16_hw(float v, uint32_t noise_hi) {
     typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-    v2h d = {(_Float16)0.0f, (_Float16)0.0f};
+    v2h d = __builtin_bit_cast(v2h, v);  // the high half keeps v's bits (never read)
     d = __builtin_amdgcn_cvt_sr_f16_f32(d, v, noise_hi, false);
-    return (float)d.x;  // exact
+    return __builtin_bit_cast(float, d);
 }
 
 }  // namespace lv

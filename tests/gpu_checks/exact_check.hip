@@ -126,8 +126,9 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
         const uint32_t nf[6] = {0u, 1u, 0x0FFFu, 0x1000u, 0x1FFFu, h & 0x1FFFu};
 #pragma unroll
         for (int k = 0; k < 6; k++) {
-            const uint32_t got = __float_as_uint(lv::sr_f16_hw(x, nf[k] << 19));
-            if (got != ref_sr_f16(i, nf[k])) record(&out[9], ex + 72, i);
+            // the fp16 bits are the low half of the result
+            const uint32_t got = __float_as_uint(lv::sr_f16_hw(x, nf[k] << 19)) & 0xFFFFu;
+            if (got != ref_f32_to_f16(ref_sr_f16(i, nf[k]))) record(&out[9], ex + 72, i);
         }
     }
     if (!(x < 0x1p-96f) || x == 0.0f) {
