@@ -505,12 +505,17 @@ __device__ __forceinline__ float load1_dyn(int dt, const void *base, uint64_t i)
 // Vector-path loads and stores are non-temporal: the step streams every byte exactly once, so
 // nothing is worth keeping in L2 or the MALL, and streaming hints measurably raise HBM
 // throughput for this 4-read/3-write pattern.
-// Layout of a work unit of 1024 * H elements: thread t owns the 4 * H consecutive elements
-// [4Ht, 4Ht + 4H). With H = 1 (f32 state) every wave-wide f32 access is one 16-byte load or
-// store per lane over 1 KiB; with H = 2 (16-bit state) a 16-bit stream moves its 8 elements in
-// ONE 16-byte access per lane (1 KiB per wave instruction) and an f32 stream (a master copy, an
-// f32 grad) in two adjacent ones. 32-bit types use `a` (elements 0-3) and `b` (4-7); 16-bit
-// types pack all eight into `a` (.x = elements 0-1, ..., .w = 6-7).
+// Layout of a work unit of 1024 * H elements. With H = 1 (f32 state) thread t owns [4t, 4t + 4):
+// every wave-wide f32 access is one 16-byte load or store per lane over 1 KiB. With H = 2
+// (16-bit state) thread t owns two groups of 4, at 4t and at 4t + HS (lane_split):
+// - HS = 4, when every stream is 16-bit: the 8 consecutive elements [8t, 8t + 8), so a 16-bit
+//   stream moves them in ONE 16-byte access per lane (1 KiB per wave instruction);
+// - HS = 1024, when an f32 stream (a master copy, f32 grads) comes with the 16-bit ones: each
+//   group is contiguous across the wave, so the f32 stream moves 1 KiB per wave instruction
+//   (two adjacent 16-byte accesses per lane would stride 32 B and cost ~6% of the semi-master
+//   bf16-state step) and a 16-bit stream 512 B.
+// 32-bit types use `a` (the first group) and `b` (the second); 16-bit types pack all eight into
+// `a` (.x = elements 0-1, ..., .w = 6-7).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -519,44 +524,50 @@ struct Raw8 {
     u32x4 a, b;
 };
 
-// H (1 or 2) is the number of 1024-element halves in the unit: a thread moves 4 * H elements.
-template <int DT, int H>
+// H (1 or 2) is the number of 1024-element halves in the unit: a thread moves 4 * H elements, in
+// groups of 4 at h0 and (H = 2) h0 + HS.
+template <int DT, int H, uint32_t HS = 4>
 __device__ __forceinline__ Raw8 load_raw(const void *base, uint64_t h0) {
     Raw8 r;
     if constexpr (DT == LV_DTYPE_F32) {
         const float *f = static_cast<const float *>(base);
         r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0));
-        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + 4));
+        if constexpr (H == 2) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(f + h0 + HS));
         else r.b = u32x4{0, 0, 0, 0};
     } else {
         const uint16_t *h = static_cast<const uint16_t *>(base);
-        if constexpr (H == 2) {
+        if constexpr (H == 2 && HS == 4) {
             r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(h + h0));
         } else {
             const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0));
-            r.a = u32x4{x.x, x.y, 0, 0};
+            if constexpr (H == 2) {
+                const u32x2 y = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(h + h0 + HS));
+                r.a = u32x4{x.x, x.y, y.x, y.y};
+            } else {
+                r.a = u32x4{x.x, x.y, 0, 0};
+            }
         }
         r.b = u32x4{0, 0, 0, 0};
     }
     return r;
 }
 
-template <int H>
+template <int H, uint32_t HS = 4>
 __device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t h0) {
-    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32, H>(base, h0);
-    return load_raw<LV_DTYPE_BF16, H>(base, h0);  // 16-bit types share the raw layout
+    if (dt == LV_DTYPE_F32) return load_raw<LV_DTYPE_F32, H, HS>(base, h0);
+    return load_raw<LV_DTYPE_BF16, H, HS>(base, h0);  // 16-bit types share the raw layout
 }
 
 // Stores 4 * H values in the same layout; 16-bit values are already quantised: a bf16 value is
 // the high half of its register (worker.rs:55-63), an fp16 value the low half (sr_fp16,
 // rne_fp16).
-template <int DT, int H>
+template <int DT, int H, uint32_t HS = 4>
 __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
     if constexpr (DT == LV_DTYPE_F32) {
         float *f = static_cast<float *>(base);
         __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4 *>(f + h0));
         if constexpr (H == 2)
-            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + 4));
+            __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4 *>(f + h0 + HS));
     } else {
         uint32_t ws[4];
 #pragma unroll
@@ -570,8 +581,12 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
             }
         }
         uint16_t *h = static_cast<uint16_t *>(base);
-        if constexpr (H == 2) __builtin_nontemporal_store(u32x4{ws[0], ws[1], ws[2], ws[3]}, reinterpret_cast<u32x4 *>(h + h0));
-        else __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
+        if constexpr (H == 2 && HS == 4) {
+            __builtin_nontemporal_store(u32x4{ws[0], ws[1], ws[2], ws[3]}, reinterpret_cast<u32x4 *>(h + h0));
+        } else {
+            __builtin_nontemporal_store(u32x2{ws[0], ws[1]}, reinterpret_cast<u32x2 *>(h + h0));
+            if constexpr (H == 2) __builtin_nontemporal_store(u32x2{ws[2], ws[3]}, reinterpret_cast<u32x2 *>(h + h0 + HS));
+        }
     }
 }
 
@@ -836,18 +851,18 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
     return tv;
 }
 
-// Vector loads of one thread's 4 * H consecutive elements [e, e + 4H).
-template <int MODE, int PT, int ST, int PASS, int H>
+// Vector loads of one thread's 4 * H elements: [e, e + 4) and (H = 2) [e + HS, e + HS + 4).
+template <int MODE, int PT, int ST, int PASS, int H, uint32_t HS = 4>
 __device__ __forceinline__ Inflight issue_at(const Desc &D, uint32_t flags, bool radial, uint64_t e) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     const int gdt = (int)((flags >> 8) & 3u);
     Inflight f;
-    f.g = load_raw_dyn<H>(gdt, D.g, e);
-    f.m = load_raw<ST, H>(D.m, e);
-    if constexpr (kDual) f.v = load_raw<ST, H>(D.v, e);
+    f.g = load_raw_dyn<H, HS>(gdt, D.g, e);
+    f.m = load_raw<ST, H, HS>(D.m, e);
+    if constexpr (kDual) f.v = load_raw<ST, H, HS>(D.v, e);
     if (PASS != kCount || radial) {  // the count pass reads p only for the radial norm
-        if (flags & kFMaster) f.p = load_raw<LV_DTYPE_F32, H>(D.mp, e);
-        else f.p = load_raw<PT, H>(D.p, e);
+        if (flags & kFMaster) f.p = load_raw<LV_DTYPE_F32, H, HS>(D.mp, e);
+        else f.p = load_raw<PT, H, HS>(D.p, e);
     }
     return f;
 }
@@ -869,7 +884,7 @@ __device__ __forceinline__ LaneK lane_consts(const Args &a) {
 // Update (or count) the 4 * H elements loaded by issue_at(e0) and store them. BALLOT: every lane
 // of the wave is here, and cnt accumulates the wave's count (the same in every lane) from ballots;
 // otherwise cnt accumulates the lane's own count.
-template <int MODE, int PT, int ST, int PASS, int H, bool BALLOT>
+template <int MODE, int PT, int ST, int PASS, int H, bool BALLOT, uint32_t HS = 4>
 __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
                                            const Inflight &cur, uint64_t e0, uint32_t &cnt, double &su, double &sp) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
@@ -907,7 +922,8 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
         for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
             float ue;
-            const HashIn zj = {zb.m + (uint32_t)j, zb.p + (uint32_t)j, zb.v + (uint32_t)j};
+            const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);  // element offset from e0
+            const HashIn zj = {zb.m + off, zb.p + off, zb.v + off};
             apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
                                              mpout[j], ue, cnt);
             if constexpr (kDual) v[j] = vj;
@@ -916,10 +932,10 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
                 sp += (double)(pin[j] * pin[j]);
             }
         }
-        store_raw<PT, H>(D.p, e0, pout);
-        if (master) store_raw<LV_DTYPE_F32, H>(D.mp, e0, mpout);
-        store_raw<ST, H>(D.m, e0, m);
-        if constexpr (kDual) store_raw<ST, H>(D.v, e0, v);
+        store_raw<PT, H, HS>(D.p, e0, pout);
+        if (master) store_raw<LV_DTYPE_F32, H, HS>(D.mp, e0, mpout);
+        store_raw<ST, H, HS>(D.m, e0, m);
+        if constexpr (kDual) store_raw<ST, H, HS>(D.v, e0, v);
     }
 }
 
@@ -1063,6 +1079,14 @@ __device__ __forceinline__ void report_count(const Args &a, const Desc &D, const
     finalize_scratch<MODE, PASS>(a, false, D, (prev >> kFoldBits) + slot_count, 0.0f, 0.0f);
 }
 
+// Offset in elements of a thread's second group of 4 in a 2048-element unit (the layout above
+// load_raw): 4, so that the thread's 8 elements are consecutive, unless the launch may move an
+// f32 stream beside its 16-bit ones (a master copy, f32 grads, or a flag word known only at run
+// time), then 1024.
+constexpr uint32_t lane_split(int H, uint32_t FL) {
+    return (H == 2 && ((FL & kFDynamic) || (FL & kFMaster) || ((FL >> 8) & 3u) == LV_DTYPE_F32)) ? kHalf : 4u;
+}
+
 // Unit launch: each block updates exactly one work unit (1024 or 2048 elements, unit_halves) and
 // exits.
 // The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
@@ -1101,6 +1125,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
+    constexpr uint32_t HS = lane_split(H, FL);
     constexpr uint64_t kUnit = (uint64_t)kHalf * H;
     const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit;
     int cover = 0;
@@ -1115,18 +1140,18 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     // ballots); every other path: cnt is the lane's count.
     const bool fast = cover == 0 && tv.vec_ok;
     const bool vec = fast && ubase + kUnit <= tv.n;
-    const uint64_t e0 = ubase + (uint64_t)threadIdx.x * (4u * H);
+    const uint64_t e0 = ubase + (uint64_t)threadIdx.x * (HS == 4 ? 4u * H : 4u);  // the first group
     if (vec) {
-        const Inflight f = issue_at<MODE, PT, ST, PASS, H>(D, flags, radial, e0);
+        const Inflight f = issue_at<MODE, PT, ST, PASS, H, HS>(D, flags, radial, e0);
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
-        process_at<MODE, PT, ST, PASS, H, true>(a, D, tv, flags, radial, f, e0, cnt, su, sp);
+        process_at<MODE, PT, ST, PASS, H, true, HS>(a, D, tv, flags, radial, f, e0, cnt, su, sp);
     } else if (fast) {
-        // the partial last unit of an aligned tensor
+        // the partial last unit of an aligned tensor: the same groups of 4
 #pragma unroll
         for (int h = 0; h < H; h++) {
-            const uint64_t e = e0 + (uint64_t)h * 4u;
+            const uint64_t e = e0 + (uint64_t)h * HS;
             if (e + 4u <= tv.n) {
                 const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
                 process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
