@@ -67,19 +67,19 @@ WORKLOADS = {
 _PROBE = dict(probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0)
 PMC_TRAFFIC = {
     (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
-                                                fetch_kib=39496892.5, write_kib=66010494.1, **_PROBE),
+                                                fetch_kib=39496781.6562, write_kib=66010493.8125, **_PROBE),
     (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=26325903.3, write_kib=39585731.5, **_PROBE),
+                                                 fetch_kib=26325301.8438, write_kib=39585733.4375, **_PROBE),
     (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
-                                                fetch_kib=3725824.05, write_kib=5614386.15, **_PROBE),
+                                                fetch_kib=3725898.4688, write_kib=5614386.375, **_PROBE),
     (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=2793025.2, write_kib=3738077.3, **_PROBE),
+                                                 fetch_kib=2793077.3125, write_kib=3738077.3438, **_PROBE),
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
-                                                    fetch_kib=2792919.3, write_kib=3738077.1, **_PROBE),
+                                                    fetch_kib=2792931.6562, write_kib=3738077.0938, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
-                                                fetch_kib=965682.6, write_kib=1451866.6, **_PROBE),
+                                                fetch_kib=965740.1562, write_kib=1451871.1562, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
-                                                fetch_kib=20710.56, write_kib=27582.38, **_PROBE),
+                                                fetch_kib=20713.4375, write_kib=27582.2812, **_PROBE),
 }
 
 # Untimed steps before the timed ones unless --warmup is given. After the inputs are generated the
