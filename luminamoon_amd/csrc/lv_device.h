@@ -377,7 +377,8 @@ __device__ __forceinline__ float coordinate_bound(float step, float p_init, floa
         float bb = b * (b + fabsf(step));
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
-        float b = ratio * sqrt_cr(__builtin_fmaf(p_init, p_init, 1.0e-4f));
+        // p^2 + 1e-4 is at least 1e-4 (or NaN or +inf), where the root needs no rescaling
+        float b = ratio * sqrt_rn_normal(__builtin_fmaf(p_init, p_init, 1.0e-4f));
         return b * tanh_pade(step / b, c);
     }
 }

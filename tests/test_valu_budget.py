@@ -53,9 +53,9 @@ KERNELS = {
     "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 91.0,
                                        {"v_div_fixup_f32": 3, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 1,
                                         "v_cvt_sr_f16_f32": 1}),
-    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 122.0,
+    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 120.0,
                      {"v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
-    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 93.5,
+    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 91.5,
                                {"v_div_fixup_f32": 3, "v_sqrt_f32": 1, "v_mul_lo_u32": 0}),
 }
 
