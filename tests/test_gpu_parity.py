@@ -76,6 +76,10 @@ CASES = [
     ("T1", "bf16", "bf16", "f32", {"fused_single_pass": False}),
     (2, "f32", "f32", "f32", {"fused_single_pass": False, "weight_decay": 0.0}),
     ("T2", "f32", "f32", "f32", {"stochastic_rounding": False, "lr": 1e-2}),
+    # 16-bit state with an f32 stream beside it: the split lane layout of 2048-element units
+    ("T2", "bf16", "bf16", "bf16", {"state_precision": "param", "master_weights": "semi"}),
+    ("T1", "bf16", "f32", "bf16", {"state_precision": "param"}),
+    (2, "f16", "f16", "f16", {"state_precision": "param", "master_weights": "semi"}),
 ]
 
 
