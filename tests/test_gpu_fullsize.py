@@ -8,6 +8,8 @@
   - bitwise equality with the oracle on slices that straddle 2^31 and 2^32 (the int32
     offset wraps twice) and on the tail, re-run on the host with index_base = slice start and the
     GPU's pre-step scratch.
+* T1 with bf16 params, grads and m and an fp32 master past 2^32 elements: the split lane layout
+  of 2048-element units, the same exact-count and slice checks.
 * shards: a tensor stepped as slices with index_base equals the whole tensor stepped at once.
 """
 from __future__ import annotations
@@ -120,4 +122,70 @@ def test_cfg5_full_bucket_count_and_wrap_slices(oracle_mod):
         assert_bitwise(hm, m[a:b], f"m[{a}:{b}]")
         assert_bitwise(hv, v[a:b], f"v[{a}:{b}]")
     del p, g, m, v
+    torch.cuda.empty_cache()
+
+
+def test_bf16_state_master_past_2_32_split_lanes(oracle_mod):
+    """T1 with bf16 params, grads and m and an fp32 master (semi): 2048-element units whose
+    threads own two groups of 4 elements 1024 apart (an f32 stream beside 16-bit ones), over
+    2^32 + 2^21 + 4101 elements (a 5-element last unit). The cautious count is exact at steps 1
+    and 2 (sign(u) = sign(g), as m starts at 0 and then holds a rounding of (1 - b1) g); slices
+    across 2^31, 2^32 and the tail equal the oracle bit for bit at step 2."""
+    _need_gpu(min_free_gb=60)
+    from luminamoon_amd.optimizer.hip_backend import HipStepper
+
+    O = oracle_mod
+    L = O.lib()
+    n = (1 << 32) + (1 << 21) + 4101
+    print(f"[fullsize] T1 bf16 state + semi master n={n}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    p = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    g = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    chunk = 1 << 27
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        z = torch.randn(e - s, device="cuda", generator=gen)
+        p[s:e].copy_(z.mul_(0.02))
+        z = torch.randn(e - s, device="cuda", generator=gen)
+        z[::20] = 0.0
+        g[s:e].copy_(z.mul_(1e-3))
+        del z
+    mp = torch.empty(n, dtype=torch.float32, device="cuda")
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        mp[s:e].copy_(p[s:e])
+    m = torch.zeros(n, dtype=torch.bfloat16, device="cuda")
+    sc = torch.tensor([0, 0, 0, 1, 1, 0.0], device="cuda")
+    count = int((g != 0).sum().item())
+    group = group_dict(buffer="T1", lr=1e-3, master_weights="semi", state_precision="param")
+    cfg = oracle_config(O, group)
+    st = HipStepper()
+    two32 = 1 << 32
+    slices = [(0, 1 << 21), ((1 << 31) - (1 << 20), (1 << 31) + (1 << 20)),
+              (two32 - (1 << 20) - 3, two32 + (1 << 20)), (n - (1 << 21) - 7, n)]
+
+    st.step(group, [p], [g], [m], [None], [mp], [sc], [1], [0])
+    torch.cuda.synchronize()
+    want1 = L.lvo_cautious_scale(L.lvo_u64_to_f32(count), L.lvo_u64_to_f32(n), 0.5)
+    got1 = sc.cpu()
+    assert got1[3].item() == want1 and got1[4].item() == 1.0 and got1[0].item() == 0.0
+
+    before = [(p[a:b].cpu(), g[a:b].cpu(), m[a:b].cpu(), mp[a:b].cpu()) for a, b in slices]
+    sc_before = got1.clone()
+    st.step(group, [p], [g], [m], [None], [mp], [sc], [2], [0])
+    torch.cuda.synchronize()
+    s_exp = (ctypes.c_float * 6)(*[float(x) for x in sc_before])
+    s_exp[0] = L.lvo_u64_to_f32(count)
+    L.lvo_update_post_step_ema(s_exp, L.lvo_u64_to_f32(n), ctypes.byref(cfg), 1)
+    got2 = sc.cpu()
+    assert list(got2.numpy().view(np.uint32)) == list(np.array(list(s_exp), dtype=np.float32).view(np.uint32))
+
+    for (a, b), (hp, hg, hm, hmp) in zip(slices, before):
+        hs = sc_before.clone()
+        O.step(cfg, [hp], [hg], [hm], [None], [hmp], [hs], [2], [0], threads=8, index_bases=[a])
+        print(f"[fullsize] slice [{a}, {b})", flush=True)
+        assert_bitwise(hp, p[a:b], f"p[{a}:{b}]")
+        assert_bitwise(hm, m[a:b], f"m[{a}:{b}]")
+        assert_bitwise(hmp, mp[a:b], f"master[{a}:{b}]")
+    del p, g, m, mp
     torch.cuda.empty_cache()
