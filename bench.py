@@ -291,7 +291,7 @@ def _cpu_baseline_timed(O, np, torch, workload: dict, threads: int, target_s: fl
 
 
 def cpu_threads() -> dict:
-    """Threads for the CPU baseline: os.cpu_count() (BASELINE.md's rule), lowered to what this
+    """Threads for the CPU baseline: os.cpu_count() (the baseline's stated rule), lowered to what this
     process may actually use -- its CPU affinity, the cgroup CPU quota, and the host share the GPU
     box grants one GPU (OMP_NUM_THREADS, which the box sets) -- each stated in the result, with
     the host's logical CPUs and physical cores reported separately."""
