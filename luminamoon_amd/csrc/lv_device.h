@@ -643,24 +643,15 @@ __device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
     return {off + (uint32_t)sd.m + kPrngAdd, off + (uint32_t)sd.p + kPrngAdd, off + (uint32_t)sd.v + kPrngAdd};
 }
 
-// Apply path for one element: dual.rs:150-228 and the matching blocks of dual.rs / tdclm.rs.
-// Counts the cautious mask bit into cnt (TALLY); u_eff is the (masked) direction whose square
-// feeds the radial norm (dual.rs:176-180).
-template <int MODE, int PT, int ST, int TALLY>
-__device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags, const HashIn &z,
-                                           float cs, float bs, float p_init, float g_raw, float &m_io,
-                                           float &v_io, float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
+// The param's update from the masked direction u (dual.rs:150-228 and the matching blocks of
+// dual.rs / tdclm.rs): the cautious scale cs, the radial scale bs or the coordinate bound, the
+// fp16 safety bound, weight decay. u_eff is the masked direction whose square feeds the radial
+// norm (dual.rs:176-180).
+template <int MODE, int PT>
+__device__ __forceinline__ float param_update(const Args &a, const LaneK &lk, uint32_t flags, float cs, float bs,
+                                              float p_init, float u, bool active, float &u_eff) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
-    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
-    const bool sr = flags & kFSR;
-    float g = sanitize(g_raw);
-    float m_new, v_new;
-    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
-    bool active = (u * g) > 0.0f;
-    tally<TALLY>(cnt, active);
     float m_mask = active ? 1.0f : 0.0f;
-    m_io = quantize<ST>(m_new, z.m, sr);
-    if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
     u_eff = (flags & kFCautious) ? u * m_mask : u;
     float delta = (flags & kFCautious) ? u_eff * cs : u;
     float step = a.lr * delta;
@@ -668,12 +659,100 @@ __device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, c
     else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio, lk.pade);
     if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init, lk.pade);
     float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
-    float p_upd = p_dec - step;
+    return p_dec - step;
+}
+
+// Apply path for one element. Counts the cautious mask bit into cnt (TALLY). m and v are
+// quantised as soon as they are known: the hashes of their stochastic rounding then overlap the
+// param's bound (each wave-uniform guard limits how far the compiler moves code). With master
+// weights p is rounded to nearest from the master (the master keeps the f32 value).
+template <int MODE, int PT, int ST, int TALLY>
+__device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags, const HashIn &z,
+                                           float cs, float bs, float p_init, float g_raw, float &m_io,
+                                           float &v_io, float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    const bool sr = flags & kFSR;
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    bool active = (u * g) > 0.0f;
+    tally<TALLY>(cnt, active);
+    m_io = quantize<ST>(m_new, z.m, sr);
+    if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
+    float p_upd = param_update<MODE, PT>(a, lk, flags, cs, bs, p_init, u, active, u_eff);
     if (flags & kFMaster) {
         mp_out = p_upd;
         p_out = quantize<PT>(p_upd, z.p, false);
     } else {
         p_out = quantize<PT>(p_upd, z.p, sr);
+    }
+}
+
+// apply_elem without the quantisation: m_io and v_io receive m' and v', p_out the updated param
+// (and mp_out too, with master weights), all in f32, for quantize_lane.
+template <int MODE, int PT, int TALLY>
+__device__ __forceinline__ void update_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags,
+                                            float cs, float bs, float p_init, float g_raw, float &m_io, float &v_io,
+                                            float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
+    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    float g = sanitize(g_raw);
+    float m_new, v_new;
+    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    bool active = (u * g) > 0.0f;
+    tally<TALLY>(cnt, active);
+    m_io = m_new;
+    if constexpr (kDual) v_io = v_new;
+    p_out = param_update<MODE, PT>(a, lk, flags, cs, bs, p_init, u, active, u_eff);
+    if (flags & kFMaster) mp_out = p_out;
+}
+
+// The vector path's quantisation of a thread's N = 4H updated values of m, v (kDual) and p: the
+// values quantize<> gives element by element (element j's hash input is its stream's base plus
+// j's offset from the thread's first element: j, or HS + j - 4 in the second group of 4). The
+// bf16 stochastic roundings share ONE overflow test: the converter overflows where the reference
+// saturates, so when any of the lane's values to round has |x| above the largest finite bf16 in
+// any lane of the wave, all of them are saturated first (the identity for the others). A maximum
+// of the magnitudes ignores NaNs, as the per-value test `|x| > max` does (false for NaN).
+template <int ST, int PT, bool kDual, int N, uint32_t HS>
+__device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, float m[8], float v[8], float p[8]) {
+    const bool sr = flags & kFSR;
+    const bool psr = sr && !(flags & kFMaster);
+    constexpr bool kBfMV = ST == LV_DTYPE_BF16;  // m (and v) rounded stochastically to bf16 when sr
+    constexpr bool kBfP = PT == LV_DTYPE_BF16;   // p rounded stochastically to bf16 when psr
+    const bool mv_sr = kBfMV && sr, p_sr = kBfP && psr;
+    if (mv_sr || p_sr) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; j++) {
+            if (mv_sr) {
+                mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
+                if constexpr (kDual) mx = __builtin_fmaxf(mx, __builtin_fabsf(v[j]));
+            }
+            if (p_sr) mx = __builtin_fmaxf(mx, __builtin_fabsf(p[j]));
+        }
+        if (__builtin_expect(!wave_all(!(mx > __uint_as_float(kBf16MaxBits))), 0)) {
+#pragma unroll
+            for (int j = 0; j < N; j++) {
+                if (mv_sr) {
+                    m[j] = bf16_saturate(m[j]);
+                    if constexpr (kDual) v[j] = bf16_saturate(v[j]);
+                }
+                if (p_sr) p[j] = bf16_saturate(p[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);
+        if (mv_sr) {
+            m[j] = sr_bf16_cvt(m[j], xor_fold16_hi((uint32_t)prng_mixed(zb.m + off)));
+            if constexpr (kDual) v[j] = sr_bf16_cvt(v[j], xor_fold16_hi((uint32_t)prng_mixed(zb.v + off)));
+        } else {
+            m[j] = quantize<ST>(m[j], zb.m + off, sr);
+            if constexpr (kDual) v[j] = quantize<ST>(v[j], zb.v + off, sr);
+        }
+        if (p_sr) p[j] = sr_bf16_cvt(p[j], xor_fold16_hi((uint32_t)prng_mixed(zb.p + off)));
+        else p[j] = quantize<PT>(p[j], zb.p + off, psr);
     }
 }
 
@@ -923,16 +1002,26 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
         for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
             float ue;
-            const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);  // element offset from e0
-            const HashIn zj = {zb.m + off, zb.p + off, zb.v + off};
-            apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
-                                             mpout[j], ue, cnt);
+            if constexpr (PT == LV_DTYPE_F16) {
+                // fp16 params: the lane's values are quantised together below (2% faster on the
+                // fp16-container cfg4 step than element by element)
+                update_elem<MODE, PT, kTally>(a, tv.k, lk, flags, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j], mpout[j],
+                                              ue, cnt);
+            } else {
+                // quantised element by element: each hash then overlaps the next element's arithmetic
+                // (quantising the lane's bf16 values together after all of them measured 4% slower)
+                const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);  // element offset from e0
+                const HashIn zj = {zb.m + off, zb.p + off, zb.v + off};
+                apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+                                                 mpout[j], ue, cnt);
+            }
             if constexpr (kDual) v[j] = vj;
             if (kCounting && radial) {
                 su += (double)(ue * ue);
                 sp += (double)(pin[j] * pin[j]);
             }
         }
+        if constexpr (PT == LV_DTYPE_F16) quantize_lane<ST, PT, kDual, 4 * H, HS>(flags, zb, m, v, pout);
         store_raw<PT, H, HS>(D.p, e0, pout);
         if (master) store_raw<LV_DTYPE_F32, H, HS>(D.mp, e0, mpout);
         store_raw<ST, H, HS>(D.m, e0, m);

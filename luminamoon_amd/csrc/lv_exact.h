@@ -111,14 +111,25 @@ __device__ __forceinline__ uint32_t pack_f16_exact(float lo, float hi) {
 // Largest finite bf16 as an f32.
 constexpr uint32_t kBf16MaxBits = 0x7F7F0000u;
 
-__device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
+// +-largest finite bf16 for a magnitude above it (inf included), v itself otherwise (NaN included).
+__device__ __forceinline__ float bf16_saturate(float v) {
     const bool big = __builtin_fabsf(v) > __uint_as_float(kBf16MaxBits);  // false for NaN
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(big) != 0, 0))
-        v = big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
+    return big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
+}
+
+// The converter alone: sr_bf16_hw for |v| <= largest finite bf16 and for NaN.
+__device__ __forceinline__ float sr_bf16_cvt(float v, uint32_t noise_hi) {
     typedef short v2s __attribute__((ext_vector_type(2)));
     v2s d = __builtin_bit_cast(v2s, v);  // the low half keeps v's bits (never read)
     d = __builtin_amdgcn_cvt_sr_bf16_f32(d, v, noise_hi, true);
     return __builtin_bit_cast(float, d);
+}
+
+__device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
+    const bool big = __builtin_fabsf(v) > __uint_as_float(kBf16MaxBits);  // false for NaN
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(big) != 0, 0))
+        v = big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
+    return sr_bf16_cvt(v, noise_hi);
 }
 
 __device__ __forceinline__ bool sr_f16_hw_domain(float v) {

@@ -50,7 +50,7 @@ KERNELS = {
                             {"v_div_fixup_f32": 2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 1}),
     "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 71.0,
                              {"v_div_fixup_f32": 2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 2}),
-    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 91.0,
+    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 90.5,
                                        {"v_div_fixup_f32": 3, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 1,
                                         "v_cvt_sr_f16_f32": 1}),
     "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 120.0,
@@ -70,7 +70,7 @@ CATEGORIES = [
     ("byte permute (16-bit pack)", r"v_perm_b32"),
     ("bitwise / shift", r"v_(xor|and|or|ashr|lshr|lshl|bfe|bfi|alignbit|bitop3)"),
     ("integer add", r"v_(add|sub)_u32|v_(add|sub)_co|v_addc"),
-    ("f32 fma / mul / add / min / max", r"v_(fma|fmac|fmaak|fmamk|mul|add|sub|subrev|min|max|med3)_f32"),
+    ("f32 fma / mul / add / min / max", r"v_(fma|fmac|fmaak|fmamk|mul|add|sub|subrev|min|max|min3|max3|med3)_f32"),
 ]
 
 
