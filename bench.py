@@ -75,7 +75,7 @@ PMC_TRAFFIC = {
     (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
                                                  fetch_kib=2793077.3125, write_kib=3738077.3438, **_PROBE),
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
-                                                    fetch_kib=2792931.6562, write_kib=3738077.0938, **_PROBE),
+                                                    fetch_kib=2792924.5312, write_kib=3738077.0938, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
                                                 fetch_kib=965740.1562, write_kib=1451871.1562, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
