@@ -94,6 +94,7 @@ CASES = [
     ("T1", "bf16", "bf16", "bf16", {"state_precision": "param"}),
     ("T2", "f16", "f16", "f32", {}),
     (2, "f16", "f16", "f16", {"state_precision": "param"}),
+    ("T1", "f16", "f16", "f16", {"state_precision": "param"}),
     ("T2", "bf16", "bf16", "f32", {"cautious": False, "stochastic_rounding": False}),
 ]
 
