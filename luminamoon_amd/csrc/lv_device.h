@@ -883,11 +883,27 @@ struct View {
     bool skip;                // graph launch whose step record refused the step: change nothing
 };
 
-template <int MODE, int PASS, bool TABLE>
-__device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, uint32_t flags, uint32_t unit) {
+// What a block needs to address its unit: the tensor's first unit, size and alignment. Everything
+// else a block reads before its arithmetic (open_step) waits until its stream loads are in flight:
+// each dependent scalar load before the first vector load delays every block's loads by a
+// scalar-cache round trip, and a block lives only a few microseconds.
+template <int MODE>
+__device__ __forceinline__ View open_view(const Desc &D, uint32_t flags) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     View tv;
     tv.t_begin = D.unit_begin;
+    tv.n = D.n;
+    uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
+    if (kDual) al |= (uintptr_t)D.v;
+    if (flags & kFMaster) al |= (uintptr_t)D.mp;
+    tv.vec_ok = (al & 15u) == 0;
+    return tv;
+}
+
+// The rest of the view: the tensor's unit end and count slots, this step's coefficients and seeds
+// (the kernel arguments, or the step record of a graph launch) and the scales in the scratch.
+template <int MODE, int PASS, bool TABLE>
+__device__ __forceinline__ void open_step(const Args &a, const Desc &D, int t, uint32_t unit, View &tv) {
     if constexpr (TABLE) {
         tv.t_end = a.dtab[t].unit_end;
         tv.slot_base = a.dtab[t].slot_base;
@@ -895,11 +911,6 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
         tv.t_end = (t + 1 < a.ndesc) ? a.d[t + 1].unit_begin : a.total_units;
         tv.slot_base = (uint32_t)t * kSlotWords;
     }
-    tv.n = D.n;
-    uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
-    if (kDual) al |= (uintptr_t)D.v;
-    if (flags & kFMaster) al |= (uintptr_t)D.mp;
-    tv.vec_ok = (al & 15u) == 0;
     tv.ibase = D.ibase;
     uint32_t seed_base = a.seed_base;
     tv.k = {a.c1, a.c2, a.c_sigma};
@@ -917,8 +928,10 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
     tv.cs = 1.0f;
     tv.bs = 1.0f;
     if constexpr (PASS == kFused || PASS == kApply) {
-        tv.cs = D.scratch[3];
-        tv.bs = D.scratch[4];
+        // Read after the stream loads, these come back through the vector memory path; the
+        // values are block-uniform and stay in scalar registers.
+        tv.cs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, D.scratch[3])));
+        tv.bs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, D.scratch[4])));
     }
     if constexpr (PASS == kSingle) {
         // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
@@ -928,7 +941,6 @@ __device__ __forceinline__ View open_view(const Args &a, const Desc &D, int t, u
             sc[0] = 0.0f; sc[1] = 0.0f; sc[2] = 0.0f; sc[3] = 1.0f; sc[4] = 1.0f; sc[5] = 0.0f;
         }
     }
-    return tv;
 }
 
 // Vector loads of one thread's 4 * H elements: [e, e + 4) and (H = 2) [e + HS, e + HS + 4).
@@ -1210,8 +1222,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const uint32_t unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
     const int t = find_tensor<TABLE>(a, unit);
     const Desc &D = desc_of<TABLE>(a, t);
-    const View tv = open_view<MODE, PASS, TABLE>(a, D, t, flags, unit);
-    if (tv.skip) return;  // block-uniform: the whole launch leaves every buffer as it was
+    View tv = open_view<MODE>(D, flags);
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
@@ -1220,12 +1231,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit;
     int cover = 0;
     uint32_t first = 0;
-    if (D.nskip) {
-        cover = inactive_cover(D, ubase, ubase + kUnit < tv.n ? ubase + kUnit : tv.n, first);
-        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
-        // its elements still enter the radial norms.
-        if (!kCounting && cover == 2) return;
-    }
+    if (D.nskip) cover = inactive_cover(D, ubase, ubase + kUnit < tv.n ? ubase + kUnit : tv.n, first);
     // Vector path over a whole unit: cnt ends as the wave's count (the same in every lane, from
     // ballots); every other path: cnt is the lane's count.
     const bool fast = cover == 0 && tv.vec_ok;
@@ -1233,26 +1239,37 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const uint64_t e0 = ubase + (uint64_t)threadIdx.x * (HS == 4 ? 4u * H : 4u);  // the first group
     if (vec) {
         const Inflight f = issue_at<MODE, PT, ST, PASS, H, HS>(D, flags, radial, e0);
+        open_step<MODE, PASS, TABLE>(a, D, t, unit, tv);
+        // A graph step refused by its step record changes nothing (block-uniform; the loads above
+        // only read).
+        if (tv.skip) return;
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
         process_at<MODE, PT, ST, PASS, H, true, HS>(a, D, tv, flags, radial, f, e0, cnt, su, sp);
-    } else if (fast) {
-        // the partial last unit of an aligned tensor: the same groups of 4
+    } else {
+        open_step<MODE, PASS, TABLE>(a, D, t, unit, tv);
+        if (tv.skip) return;  // block-uniform: the whole launch leaves every buffer as it was
+        // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
+        // its elements still enter the radial norms.
+        if (!kCounting && cover == 2) return;
+        if (fast) {
+            // the partial last unit of an aligned tensor: the same groups of 4
 #pragma unroll
-        for (int h = 0; h < H; h++) {
-            const uint64_t e = e0 + (uint64_t)h * HS;
-            if (e + 4u <= tv.n) {
-                const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
-                process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
-            } else if (e < tv.n) {
-                scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
+            for (int h = 0; h < H; h++) {
+                const uint64_t e = e0 + (uint64_t)h * HS;
+                if (e + 4u <= tv.n) {
+                    const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
+                    process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
+                } else if (e < tv.n) {
+                    scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
+                }
             }
+        } else if (cover != 2 || radial) {
+            const uint64_t eb = ubase + (uint64_t)threadIdx.x * (4u * H);
+            const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
+            scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
         }
-    } else if (cover != 2 || radial) {
-        const uint64_t eb = ubase + (uint64_t)threadIdx.x * (4u * H);
-        const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
-        scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
     }
     if constexpr (kCounting) {
         if (radial) {
