@@ -183,6 +183,47 @@ def copy_probe(torch, n_floats: int = 1 << 30, reps: int = 5) -> float:
     return 8.0 * n_floats / (ms / 1e3) / 1e9
 
 
+def stream_floor(torch, p, g, m, v, reps: int) -> dict:
+    """The stream floor of the step (--stream-floor): libstream_probe.so's bare kernel reads and
+    writes the step's own buffers (p and the state read and written, g read; same element sizes,
+    1024-element blocks, 4 consecutive elements per thread, non-temporal accesses) with no
+    arithmetic, lookup or count, `reps` launches back to back between HIP events on the current
+    stream. Its bandwidth is what the hardware gives that read/write mix on these very pages. It
+    overwrites the buffers, so it runs after every read of the optimizer's state."""
+    import ctypes
+
+    from luminamoon_amd import build_ext
+
+    lib = ctypes.CDLL(build_ext.PROBE_OUT)
+    fn = lib.lv_stream_probe
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    pb, sb, ns, n = p.element_size(), m.element_size(), 1 if v is None else 2, p.numel()
+    assert g.element_size() == pb and g.numel() == n and m.numel() == n and (v is None or v.numel() == n)
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        rc = fn(pb, sb, ns, p.data_ptr(), g.data_ptr(), m.data_ptr(), None if v is None else v.data_ptr(), n,
+                stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lv_stream_probe returned {rc}")
+
+    for _ in range(3):
+        launch()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        launch()
+    b.record(stream)
+    b.synchronize()
+    ms = a.elapsed_time(b) / reps
+    bpp = 3 * pb + 2 * sb * ns
+    gbs = n * bpp / (ms / 1e3) / 1e9
+    return {"gb_per_s": gbs, "frac": gbs / HBM_PEAK_GBS, "ms": ms, "bytes_per_param": bpp, "reps": reps,
+            "kernel": f"stream_probe_kernel<{pb}, {sb}, {ns}>"}
+
+
 def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
     """The reference's CPU path restated in C (oracle/): its AVX-512 chunk kernels
     (luminav-simd/src/avx512/*.rs, 16 lanes) when this host has AVX-512, else its scalar core,
@@ -350,6 +391,9 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-reserve", action="store_true", help="skip the HBM reserve/release before allocating")
     ap.add_argument("--reserve-gb", type=float, default=200.0)
+    ap.add_argument("--stream-floor", action="store_true",
+                    help="after the timed steps, time a bare kernel that streams the step's own buffers "
+                         "(one-tensor configs without master weights)")
     args = ap.parse_args()
     if args.warmup is None:
         args.warmup = DEFAULT_WARMUP[args.config]
@@ -435,6 +479,17 @@ def main() -> int:
             log(f"non-finite scratch {sc}")
             return 1
     log(f"scratch of the last tensor after {args.warmup + args.steps} steps: {sc}")
+    floor = None
+    if args.stream_floor:
+        if len(params) != 1 or args.master != "none":
+            log("--stream-floor: one-tensor configs without master weights only; skipped")
+        else:
+            st = opt.state[params[0]]
+            floor = stream_floor(torch, params[0].data, params[0].grad, st["exp_avg"], st.get("exp_avg_sq"),
+                                 reps=args.steps)
+            log(f"stream floor ({floor['kernel']}, {floor['bytes_per_param']} B/param, {floor['reps']} launches): "
+                f"{floor['ms']:.4f} ms, {floor['gb_per_s']:.0f} GB/s ({100 * floor['frac']:.1f}% of peak); "
+                f"the step: {ms_avg:.4f} ms, {achieved:.0f} GB/s ({100 * achieved / HBM_PEAK_GBS:.1f}%)")
     del opt, params, p
     torch.cuda.empty_cache()
     copy_gbs = copy_probe(torch)
@@ -492,6 +547,8 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if floor is not None:
+        out["stream_floor"] = floor
     print(json.dumps(out), flush=True)
     return 0
 

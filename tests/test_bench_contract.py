@@ -125,3 +125,29 @@ def test_cpu_baseline_draws_student_t_grads_for_cfg5():
     assert wl["grad"] == "student_t3"
     out = bench.cpu_baseline(wl, threads=2, target_s=0.3)
     assert out["grads"] == "student_t3" and out["value"] > 0
+
+
+def _probe_lib():
+    import ctypes
+
+    from luminamoon_amd import build_ext
+
+    if not os.path.exists(build_ext.PROBE_OUT):
+        pytest.skip("libstream_probe.so is not built")
+    fn = ctypes.CDLL(build_ext.PROBE_OUT).lv_stream_probe
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    return fn
+
+
+def test_stream_probe_rejects_invalid_arguments_before_any_launch():
+    """Every invalid call returns 1 from the argument checks (the fake addresses are never used)."""
+    fn = _probe_lib()
+    a = 1 << 20  # 16-byte aligned stand-ins
+    ok = dict(pb=2, sb=4, ns=2, p=a, g=a, m=a, v=a, n=4096)
+    bad = [dict(pb=3), dict(sb=8), dict(ns=3), dict(ns=0), dict(p=None), dict(g=None), dict(m=None),
+           dict(v=None), dict(n=0), dict(n=4098), dict(p=a + 8), dict(v=a + 4), dict(n=(1 << 24) * 1024)]
+    for change in bad:
+        c = {**ok, **change}
+        assert fn(c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"], None) == 1, change
