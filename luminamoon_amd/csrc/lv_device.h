@@ -218,11 +218,11 @@ __device__ __forceinline__ int32_t prng(uint32_t z0) {
     return z ^ (z >> 16);
 }
 
-// prng.rs:137-160 on the hardware converter (sr_bf16_hw in lv_exact.h): the noise
-// prng(z0) & 0xFFFF goes in the high half of the converter's random operand. Returns an f32
-// whose HIGH half holds the bf16 bits (the low half is not zero: store it, do not compute with it).
+// prng.rs:137-160 (sr_bf16_checked in lv_exact.h) with the noise prng(z0) & 0xFFFF. Returns an
+// f32 whose HIGH half holds the bf16 bits (the low half is not zero: store it, do not compute
+// with it).
 __device__ __forceinline__ float sr_bf16(float v, uint32_t z0) {
-    return sr_bf16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)));
+    return sr_bf16_checked(v, xor_fold16((uint32_t)prng_mixed(z0)));
 }
 
 // prng.rs:162-178
@@ -709,10 +709,10 @@ __device__ __forceinline__ void update_elem(const Args &a, const StepCoeffs &k, 
 // The vector path's quantisation of a thread's N = 4H updated values of m, v (kDual) and p: the
 // values quantize<> gives element by element (element j's hash input is its stream's base plus
 // j's offset from the thread's first element: j, or HS + j - 4 in the second group of 4). The
-// bf16 stochastic roundings share ONE overflow test: the converter overflows where the reference
-// saturates, so when any of the lane's values to round has |x| above the largest finite bf16 in
-// any lane of the wave, all of them are saturated first (the identity for the others). A maximum
-// of the magnitudes ignores NaNs, as the per-value test `|x| > max` does (false for NaN).
+// bf16 stochastic roundings (one integer add each, sr_bf16_add) share ONE test: when any of the
+// lane's values to round is NaN or has |x| above the largest finite bf16 in any lane of the wave,
+// all of them go through sr_bf16_prep first (the identity for the others). The maximum of the
+// magnitudes is NaN-propagating (v_maximum3_f32), so the test `!(max <= largest)` sees NaNs.
 template <int ST, int PT, bool kDual, int N, uint32_t HS>
 __device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, float m[8], float v[8], float p[8]) {
     const bool sr = flags & kFSR;
@@ -725,19 +725,19 @@ __device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, 
 #pragma unroll
         for (int j = 0; j < N; j++) {
             if (mv_sr) {
-                mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
-                if constexpr (kDual) mx = __builtin_fmaxf(mx, __builtin_fabsf(v[j]));
+                mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(m[j]));
+                if constexpr (kDual) mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(v[j]));
             }
-            if (p_sr) mx = __builtin_fmaxf(mx, __builtin_fabsf(p[j]));
+            if (p_sr) mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(p[j]));
         }
-        if (__builtin_expect(!wave_all(!(mx > __uint_as_float(kBf16MaxBits))), 0)) {
+        if (__builtin_expect(!wave_all(mx <= __uint_as_float(kBf16MaxBits)), 0)) {
 #pragma unroll
             for (int j = 0; j < N; j++) {
                 if (mv_sr) {
-                    m[j] = bf16_saturate(m[j]);
-                    if constexpr (kDual) v[j] = bf16_saturate(v[j]);
+                    m[j] = sr_bf16_prep(m[j]);
+                    if constexpr (kDual) v[j] = sr_bf16_prep(v[j]);
                 }
-                if (p_sr) p[j] = bf16_saturate(p[j]);
+                if (p_sr) p[j] = sr_bf16_prep(p[j]);
             }
         }
     }
@@ -745,13 +745,13 @@ __device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, 
     for (int j = 0; j < N; j++) {
         const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);
         if (mv_sr) {
-            m[j] = sr_bf16_cvt(m[j], xor_fold16_hi((uint32_t)prng_mixed(zb.m + off)));
-            if constexpr (kDual) v[j] = sr_bf16_cvt(v[j], xor_fold16_hi((uint32_t)prng_mixed(zb.v + off)));
+            m[j] = sr_bf16_add(m[j], xor_fold16((uint32_t)prng_mixed(zb.m + off)));
+            if constexpr (kDual) v[j] = sr_bf16_add(v[j], xor_fold16((uint32_t)prng_mixed(zb.v + off)));
         } else {
             m[j] = quantize<ST>(m[j], zb.m + off, sr);
             if constexpr (kDual) v[j] = quantize<ST>(v[j], zb.v + off, sr);
         }
-        if (p_sr) p[j] = sr_bf16_cvt(p[j], xor_fold16_hi((uint32_t)prng_mixed(zb.p + off)));
+        if (p_sr) p[j] = sr_bf16_add(p[j], xor_fold16((uint32_t)prng_mixed(zb.p + off)));
         else p[j] = quantize<PT>(p[j], zb.p + off, psr);
     }
 }

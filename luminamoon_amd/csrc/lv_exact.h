@@ -21,17 +21,18 @@
 // step (prng.rs:25) that bf16 stochastic rounding uses as noise, in one SDWA instruction.
 // xor_fold16_hi(z) is the same 16 bits placed in the high half (low half zero).
 //
-// sr_bf16_hw: bf16 stochastic rounding (prng.rs:137-160) on gfx950's v_cvt_sr_bf16_f32. The
-// converter adds the high 16 bits of its random operand to the 16 bits it truncates (its top
-// random bit lines up with the first truncated bit), so the reference's 16-bit noise goes in the
-// high half. It then equals the reference's integer recipe on every input -- zeros, denormals and
-// NaNs included (a NaN becomes its quietened upper half, as in the reference) -- except that it
-// overflows to +-inf where the reference saturates to the largest finite bf16 (0x7F7F). A
-// magnitude above that largest value (inf included, NaN excluded) always rounds to 0x7F7F in the
-// reference, so such inputs are replaced by +-0x7F7F0000 first, which converts to itself for any
-// noise; the replacement only runs when a lane of the wave needs it (one compare per element).
-// The result is returned as an f32 whose high half holds the bf16 bits; its low half is NOT
-// zero, so it is only good for storing the high half.
+// sr_bf16_checked: bf16 stochastic rounding (prng.rs:137-160) as one integer add. For
+// |v| <= the largest finite bf16 (0x7F7F0000; NaN excluded) the reference's recipe -- 16 noise
+// bits added to |v|'s bits, the low half dropped, the sign put back -- is the high half of
+// bits(v) + noise: the sum never carries into the sign bit and never passes 0x7F7FFFFF, so the
+// reference's saturation never applies. The other inputs are first replaced by values whose sum
+// with any noise has the reference's high half (sr_bf16_prep): a magnitude above the largest
+// finite bf16 (inf included), which the reference always rounds to +-0x7F7F, by +-0x7F7F0000;
+// a NaN by its quietened upper half (bits | 0x00400000, prng.rs:141-143) with a zero low half.
+// The replacement runs only when a lane of the wave needs it (one compare per value). The
+// result is an f32 whose HIGH half holds the bf16 bits; its low half is NOT zero, so it is only
+// good for storing the high half. (gfx950's v_cvt_sr_bf16_f32 gives the same bits on its
+// domain but takes about 3.4 times an integer add's issue time.)
 //
 // sr_f16_hw: fp16 stochastic rounding (prng.rs:98-130) on gfx950's v_cvt_sr_f16_f32, on its
 // domain: +-0 and 2^-14 <= |v| < 65504 (the results are fp16 normals or zeros). For such inputs the
@@ -117,19 +118,27 @@ __device__ __forceinline__ float bf16_saturate(float v) {
     return big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
 }
 
-// The converter alone: sr_bf16_hw for |v| <= largest finite bf16 and for NaN.
-__device__ __forceinline__ float sr_bf16_cvt(float v, uint32_t noise_hi) {
-    typedef short v2s __attribute__((ext_vector_type(2)));
-    v2s d = __builtin_bit_cast(v2s, v);  // the low half keeps v's bits (never read)
-    d = __builtin_amdgcn_cvt_sr_bf16_f32(d, v, noise_hi, true);
-    return __builtin_bit_cast(float, d);
+// True where sr_bf16_add needs sr_bf16_prep first: |v| above the largest finite bf16, or NaN.
+__device__ __forceinline__ bool sr_bf16_odd(float v) {
+    return !(__builtin_fabsf(v) <= __uint_as_float(kBf16MaxBits));
 }
 
-__device__ __forceinline__ float sr_bf16_hw(float v, uint32_t noise_hi) {
-    const bool big = __builtin_fabsf(v) > __uint_as_float(kBf16MaxBits);  // false for NaN
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(big) != 0, 0))
-        v = big ? __uint_as_float((__float_as_uint(v) & 0x80000000u) | kBf16MaxBits) : v;
-    return sr_bf16_cvt(v, noise_hi);
+// v itself where |v| <= the largest finite bf16; otherwise the value whose sum with any 16-bit
+// noise has the reference's rounding of v in its high half.
+__device__ __forceinline__ float sr_bf16_prep(float v) {
+    const uint32_t quiet = (__float_as_uint(v) | 0x00400000u) & 0xFFFF0000u;
+    return v != v ? __uint_as_float(quiet) : bf16_saturate(v);
+}
+
+// The add alone: the reference's rounding of v (high half) for |v| <= the largest finite bf16
+// and for sr_bf16_prep's values; `noise` is the 16-bit noise in the low half.
+__device__ __forceinline__ float sr_bf16_add(float v, uint32_t noise) {
+    return __uint_as_float(__float_as_uint(v) + noise);
+}
+
+__device__ __forceinline__ float sr_bf16_checked(float v, uint32_t noise) {
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(sr_bf16_odd(v)) != 0, 0)) v = sr_bf16_prep(v);
+    return sr_bf16_add(v, noise);
 }
 
 __device__ __forceinline__ bool sr_f16_hw_domain(float v) {

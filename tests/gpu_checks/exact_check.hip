@@ -5,7 +5,7 @@
 //   sqrt_rn against the compiler's correctly rounded square root (IEEE, as Rust's f32::sqrt), 2^32;
 //   xor_fold16 against (z ^ (z >> 16)) & 0xFFFF with the arithmetic shift of prng.rs:25, 2^32;
 //   xor_fold16_hi against the same 16 bits in the high half, 2^32;
-//   sr_bf16_hw against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
+//   sr_bf16_checked against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
 //     with 6 noise values per input (0, 1, 0x7FFF, 0x8000, 0xFFFF and a hash of the input), 6 x 2^32;
 //   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN);
 //   pack_f16_exact on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
@@ -97,7 +97,7 @@ __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) 
 
 // Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
 // NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
-// [4] xor_fold16 mismatches, [5] xor_fold16_hi, [6] sr_bf16_hw (input, any noise),
+// [4] xor_fold16 mismatches, [5] xor_fold16_hi, [6] sr_bf16_checked (input, any noise),
 // [7] sqrt_rn_normal on its domain, [8] pack_f16_exact, [9] sr_f16_hw on its domain (input, any
 // noise) or a domain test that disagrees with its definition, [10] inputs in the sr_f16_hw domain
 // (not a mismatch: the size of the domain checked); ex[8 * c + k] holds the first inputs of
@@ -114,7 +114,7 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     const uint32_t noises[6] = {0u, 1u, 0x7FFFu, 0x8000u, 0xFFFFu, h & 0xFFFFu};
 #pragma unroll
     for (int k = 0; k < 6; k++) {
-        const uint32_t got = __float_as_uint(lv::sr_bf16_hw(__uint_as_float(i), noises[k] << 16)) >> 16;
+        const uint32_t got = __float_as_uint(lv::sr_bf16_checked(__uint_as_float(i), noises[k])) >> 16;
         if (got != ref_sr_bf16(i, noises[k])) record(&out[6], ex + 48, i);
     }
     const float x = __uint_as_float(i);

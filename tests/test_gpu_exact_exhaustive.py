@@ -9,8 +9,9 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   f32::sqrt): all 2^32 inputs bit for bit, NaN for NaN;
 * xor_fold16 against (z ^ (z >> 16)) & 0xFFFF, and xor_fold16_hi against the same bits in the
   high half: all 2^32 inputs;
-* sr_bf16_hw (the hardware stochastic-rounding converter with the reference's saturation)
-  against the reference's integer recipe (prng.rs:137-160): all 2^32 inputs x 6 noise values;
+* sr_bf16_checked (one integer add, with the out-of-range and NaN inputs replaced first when a
+  lane of the wave has one) against the reference's integer recipe (prng.rs:137-160): all 2^32
+  inputs x 6 noise values;
 * sqrt_rn_normal (no rescaling) against the IEEE square root on every input of its domain;
 * pack_f16_exact against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
   reference's fp16 quantisation never yields an infinity);
@@ -54,7 +55,7 @@ def test_exact_helpers_on_every_input():
     assert counts[3] == 0, ("sqrt_rn", [hex(x) for x in ex[24:32]])
     assert counts[4] == 0, ("xor_fold16", [hex(x) for x in ex[32:40]])
     assert counts[5] == 0, ("xor_fold16_hi", [hex(x) for x in ex[40:48]])
-    assert counts[6] == 0, ("sr_bf16_hw", [hex(x) for x in ex[48:56]])
+    assert counts[6] == 0, ("sr_bf16_checked", [hex(x) for x in ex[48:56]])
     assert counts[7] == 0, ("sqrt_rn_normal", [hex(x) for x in ex[56:64]])
     assert counts[8] == 0, ("pack_f16_exact", [hex(x) for x in ex[64:72]])
     assert counts[9] == 0, ("sr_f16_hw", [hex(x) for x in ex[72:80]])
