@@ -238,16 +238,17 @@ __device__ __forceinline__ float rne_bf16(float v) {
 
 // f32_to_f16_rne (prng.rs:29-67) and f16_to_f32 (prng.rs:69-96) are in lv_exact.h.
 
-// prng.rs:98-130. Returns an f32 register whose LOW half holds the fp16 bits (the high half is
-// not defined: store the low half, do not compute with it). On the hardware converter's domain
-// (sr_f16_hw in lv_exact.h: +-0 and fp16 normal results below 65504) the noise prng(z0) & 0x1FFF
-// goes in bits 31..19 of its random operand; when any active lane of the wave is outside that
-// domain, the wave takes the integer recipe below (the one the reference states).
-__device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
-    // the converter's result, replaced below in the rare waves that need the recipe (computing it
+// prng.rs:98-130 as an f32 whose round-toward-zero fp16 conversion (pack_f16_rtz) is the
+// reference's result. On sr_f16_domain (lv_exact.h: +-0 and fp16 normal results below 65504)
+// that is v's bits plus the 13 noise bits prng(z0) & 0x1FFF (sr_f16_add); when any active lane of
+// the wave is outside the domain, the wave takes the integer recipe below (the one the reference
+// states), whose result is itself an fp16 value.
+__device__ __forceinline__ float sr_fp16_val(float v, uint32_t z0) {
+    const uint32_t z = (uint32_t)prng_mixed(z0);
+    // the domain's result, replaced below in the rare waves that need the recipe (computing it
     // first lets both paths leave the result in one register)
-    const float hw = sr_f16_hw(v, xor_fold16_hi((uint32_t)prng_mixed(z0)) << 3);
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!sr_f16_hw_domain(v)) == 0, 1)) return hw;
+    const float fast = sr_f16_add(v, xor_fold16(z) & 0x1FFFu);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!sr_f16_domain(v)) == 0, 1)) return fast;
     int32_t p = (int32_t)f_bits(v);
     int32_t a = p & 0x7FFFFFFF;
     int32_t ex = (a >> 23) & 0xFF;
@@ -255,22 +256,27 @@ __device__ __forceinline__ float sr_fp16(float v, uint32_t z0) {
     sub = sub > 0 ? sub : 0;
     sub = sub < 11 ? sub : 11;
     int32_t mask = (int32_t)((1u << (13 + sub)) - 1u);
-    int32_t noise = prng(z0) & mask;
+    int32_t noise = ((int32_t)z ^ ((int32_t)z >> 16)) & mask;  // prng(z0)
     int32_t added = ex < 103 ? 0 : (int32_t)(((uint32_t)a + (uint32_t)noise) & (uint32_t)(~mask));
     int32_t r = added > 0x477FE000 ? 0x477FE000 : added;
     // The reference converts sign | r to fp16 and back (prng.rs:129). sign | r is already an fp16
-    // value, so that round trip is the identity and its fp16 bits come from one exact conversion
-    // (pack_f16_exact). r is one of:
+    // value, so that round trip is the identity and pack_f16_rtz converts it exactly. r is one of:
     // - 0, or 65504;
     // - the sign bit alone (-0.0), when a NaN's magnitude plus the noise wraps past 2^31;
     // - a value with its (13 + sub) low bits clear. For ex >= 113 that leaves 10 fraction bits
     //   below 65504 (an fp16 normal). For 103 <= ex <= 112 it leaves a multiple of 2^-24 below
     //   2^-13 (fp16 subnormals and the lowest normal binade).
-    return bits_f(pack_f16_exact(bits_f((uint32_t)((p & (int32_t)0x80000000u) | r)), 0.0f));
+    return bits_f((uint32_t)((p & (int32_t)0x80000000u) | r));
 }
+
+// The same with the fp16 bits in the low half (high half zero), for element-wise stores.
+__device__ __forceinline__ float sr_fp16(float v, uint32_t z0) { return bits_f(pack_f16_rtz(sr_fp16_val(v, z0), 0.0f)); }
 
 // prng.rs:29-67: fp16 bits in the low half (high half zero), like sr_fp16.
 __device__ __forceinline__ float rne_fp16(float v) { return bits_f(f32_to_f16_rne(v)); }
+
+// The same as an fp16 value in an f32 (exact for pack_f16_rtz), like sr_fp16_val.
+__device__ __forceinline__ float rne_fp16_val(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
 
 // prng.rs:180-195; dtype is a compile-time constant at every call site. z0 is the element's
 // hash input for the buffer's seed (offset + seed + kPrngAdd). The result is only stored:
@@ -560,8 +566,8 @@ __device__ __forceinline__ Raw8 load_raw_dyn(int dt, const void *base, uint64_t 
 }
 
 // Stores 4 * H values in the same layout; 16-bit values are already quantised: a bf16 value is
-// the high half of its register (worker.rs:55-63), an fp16 value the low half (sr_fp16,
-// rne_fp16).
+// the high half of its register (worker.rs:55-63); an fp16 value is an f32 whose round-toward-zero
+// conversion is the fp16 result (sr_fp16_val, rne_fp16_val: quantize_lane).
 template <int DT, int H, uint32_t HS = 4>
 __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float in[8]) {
     if constexpr (DT == LV_DTYPE_F32) {
@@ -577,8 +583,8 @@ __device__ __forceinline__ void store_raw(void *base, uint64_t h0, const float i
                 // the high halves of both values in one v_perm_b32 (bytes 2-3 of each)
                 ws[k] = __builtin_amdgcn_perm(f_bits(in[2 * k + 1]), f_bits(in[2 * k]), 0x07060302u);
             } else {
-                // the low halves (bytes 0-1 of each)
-                ws[k] = __builtin_amdgcn_perm(f_bits(in[2 * k + 1]), f_bits(in[2 * k]), 0x05040100u);
+                // fp16 values (or sr_fp16_val's sums) converted and packed in one instruction
+                ws[k] = pack_f16_rtz(in[2 * k], in[2 * k + 1]);
             }
         }
         uint16_t *h = static_cast<uint16_t *>(base);
@@ -752,6 +758,7 @@ __device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, 
             if constexpr (kDual) v[j] = quantize<ST>(v[j], zb.v + off, sr);
         }
         if (p_sr) p[j] = sr_bf16_add(p[j], xor_fold16((uint32_t)prng_mixed(zb.p + off)));
+        else if constexpr (PT == LV_DTYPE_F16) p[j] = psr ? sr_fp16_val(p[j], zb.p + off) : rne_fp16_val(p[j]);
         else p[j] = quantize<PT>(p[j], zb.p + off, psr);
     }
 }

@@ -19,7 +19,6 @@
 //
 // xor_fold16(z) = (z ^ (z >> 16)) & 0xFFFF, the low half of the reference PRNG's last mixing
 // step (prng.rs:25) that bf16 stochastic rounding uses as noise, in one SDWA instruction.
-// xor_fold16_hi(z) is the same 16 bits placed in the high half (low half zero).
 //
 // sr_bf16_checked: bf16 stochastic rounding (prng.rs:137-160) as one integer add. For
 // |v| <= the largest finite bf16 (0x7F7F0000; NaN excluded) the reference's recipe -- 16 noise
@@ -34,16 +33,15 @@
 // good for storing the high half. (gfx950's v_cvt_sr_bf16_f32 gives the same bits on its
 // domain but takes about 3.4 times an integer add's issue time.)
 //
-// sr_f16_hw: fp16 stochastic rounding (prng.rs:98-130) on gfx950's v_cvt_sr_f16_f32, on its
-// domain: +-0 and 2^-14 <= |v| < 65504 (the results are fp16 normals or zeros). For such inputs the
-// reference discards 13 fraction bits and adds 13 noise bits (the low 13 of the hash); the
-// converter adds the high 13 bits of its random operand to the same 13 bits, so the noise goes in
-// bits 31..19. Outside the domain the two differ and callers take the integer recipe: below 2^-14
-// the reference widens both the discarded field and the noise to 13 + k bits where the converter
-// keeps 13 (ignoring the discarded bits below them), and at the top the reference saturates to
-// 65504 where the converter overflows to infinity. The result is an f32 register whose LOW half
-// holds the fp16 bits; its high half keeps v's high bits (store the low half, do not compute
-// with it), which spares clearing the converter's destination.
+// sr_f16_add: fp16 stochastic rounding (prng.rs:98-130) on its common domain, +-0 and
+// 2^-14 <= |v| < 65504 (sr_f16_domain). There the reference adds 13 noise bits (the low 13 of the
+// hash) to |v|'s bits and clears those 13 bits: an fp16 normal or zero, at most 65504. That is the
+// round-toward-zero fp16 conversion of bits(v) + noise (v_cvt_pkrtz_f16_f32, pack_f16_rtz): the
+// sum never carries into the sign bit, stays below 0x47800000 (RTZ gives at most 65504), and for
+// +-0 is an f32 far below the smallest fp16 subnormal, which converts to +-0. Outside the domain
+// callers take the integer recipe: below 2^-14 the reference widens both the cleared field and
+// the noise to 13 + k bits. (gfx950's v_cvt_sr_f16_f32 gives the same bits on the domain but takes
+// about 3.4 times an integer add's issue time, plus a shift to place its noise.)
 //
 // The fp16 conversions need fp16 denormals enabled, the HIP default for gfx950 code objects.
 #pragma once
@@ -93,19 +91,12 @@ __device__ __forceinline__ uint32_t xor_fold16(uint32_t z) {
     return r;
 }
 
-__device__ __forceinline__ uint32_t xor_fold16_hi(uint32_t z) {
-    uint32_t r;
-    asm("v_xor_b32_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
-        : "=v"(r)
-        : "v"(z));
-    return r;
-}
-
-// Two f32 values that are already f16 values (every result of the reference's fp16 quantisation:
-// finite f16 values, +-65504, signed zeros, subnormals, or the canonical quiet NaN +-0x7FC00000)
-// packed as f16 bits, low half first, with one v_cvt_pkrtz_f16_f32: for such values rounding
-// toward zero is exact, and the canonical NaN becomes the reference's +-0x7E00.
-__device__ __forceinline__ uint32_t pack_f16_exact(float lo, float hi) {
+// Two f32 values packed as fp16 bits, low half first, with one v_cvt_pkrtz_f16_f32 (round toward
+// zero). For values that are already fp16 values (every result of the reference's fp16
+// quantisation: finite fp16 values, +-65504, signed zeros, subnormals, or the canonical quiet NaN
+// +-0x7FC00000) it is exact, and the canonical NaN becomes the reference's +-0x7E00; for
+// sr_f16_add's sums it is the truncation that completes the stochastic rounding.
+__device__ __forceinline__ uint32_t pack_f16_rtz(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
@@ -141,17 +132,16 @@ __device__ __forceinline__ float sr_bf16_checked(float v, uint32_t noise) {
     return sr_bf16_add(v, noise);
 }
 
-__device__ __forceinline__ bool sr_f16_hw_domain(float v) {
+__device__ __forceinline__ bool sr_f16_domain(float v) {
     const float a = __builtin_fabsf(v);
     // false for NaN; & and | (not && and ||) keep the three compares free of branches
     return (a < 65504.0f) & ((a >= 0x1p-14f) | (a == 0.0f));
 }
 
-__device__ __forceinline__ float sr_f16_hw(float v, uint32_t noise_hi) {
-    typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-    v2h d = __builtin_bit_cast(v2h, v);  // the high half keeps v's bits (never read)
-    d = __builtin_amdgcn_cvt_sr_f16_f32(d, v, noise_hi, false);
-    return __builtin_bit_cast(float, d);
+// bits(v) + noise, noise in [0, 0x1FFF]: the reference's rounding of v after pack_f16_rtz, for v
+// in sr_f16_domain.
+__device__ __forceinline__ float sr_f16_add(float v, uint32_t noise) {
+    return __uint_as_float(__float_as_uint(v) + noise);
 }
 
 }  // namespace lv

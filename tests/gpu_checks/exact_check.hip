@@ -4,13 +4,15 @@
 //   f16 -> f32 against prng.rs:69-96 (restated here), 2^16;
 //   sqrt_rn against the compiler's correctly rounded square root (IEEE, as Rust's f32::sqrt), 2^32;
 //   xor_fold16 against (z ^ (z >> 16)) & 0xFFFF with the arithmetic shift of prng.rs:25, 2^32;
-//   xor_fold16_hi against the same 16 bits in the high half, 2^32;
+//   sr_fp16_val (the library's whole fp16 stochastic rounding: the domain's integer add, the wave's
+//     switch to the integer recipe, pack_f16_rtz) against prng.rs:98-130 with prng.rs:21-26's noise,
+//     2 hash inputs per input, 2 x 2^32;
 //   sr_bf16_checked against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
 //     with 6 noise values per input (0, 1, 0x7FFF, 0x8000, 0xFFFF and a hash of the input), 6 x 2^32;
 //   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN);
-//   pack_f16_exact on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
-//   sr_f16_hw against the reference's fp16 stochastic rounding (prng.rs:98-130, restated here) on
-//     every input of its domain (sr_f16_hw_domain) with 6 noise values per input (0, 1, 0xFFF,
+//   pack_f16_rtz on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
+//   sr_f16_add + pack_f16_rtz against the reference's fp16 stochastic rounding (prng.rs:98-130,
+//     restated here) on every input of its domain (sr_f16_domain) with 6 noise values per input (0, 1, 0xFFF,
 //     0x1000, 0x1FFF and a hash of the input), and the domain test against its definition, 2^32.
 // Test infrastructure: built by __graft_entry__.build() into tests/gpu_checks/libexactcheck.so
 // and run by tests/test_gpu_exact_exhaustive.py.
@@ -82,6 +84,14 @@ __device__ uint32_t ref_sr_f16(uint32_t pu, uint32_t noise) {
     return (uint32_t)((p & (int32_t)0x80000000u) | r);
 }
 
+// prng.rs:21-26: wrapping i32 arithmetic, arithmetic right shifts; z0 = idx + seed - 1640531527.
+__device__ uint32_t ref_prng(uint32_t z0) {
+    int32_t z = (int32_t)z0;
+    z = (int32_t)((uint32_t)(z ^ (z >> 16)) * (uint32_t)-2048173461);
+    z = (int32_t)((uint32_t)(z ^ (z >> 13)) * (uint32_t)-1028477387);
+    return (uint32_t)(z ^ (z >> 16));
+}
+
 __device__ uint32_t mix32(uint32_t z) {
     z ^= z >> 16;
     z *= 0x7FEB352Du;
@@ -97,9 +107,10 @@ __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) 
 
 // Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
 // NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
-// [4] xor_fold16 mismatches, [5] xor_fold16_hi, [6] sr_bf16_checked (input, any noise),
-// [7] sqrt_rn_normal on its domain, [8] pack_f16_exact, [9] sr_f16_hw on its domain (input, any
-// noise) or a domain test that disagrees with its definition, [10] inputs in the sr_f16_hw domain
+// [4] xor_fold16 mismatches, [5] sr_fp16_val (input, either hash input), [6] sr_bf16_checked
+// (input, any noise), [7] sqrt_rn_normal on its domain, [8] pack_f16_rtz, [9] sr_f16_add on its
+// domain (input, any noise) or a domain test that disagrees with its definition, [10] inputs in
+// the sr_f16_domain
 // (not a mismatch: the size of the domain checked); ex[8 * c + k] holds the first inputs of
 // counter c.
 __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex) {
@@ -109,7 +120,12 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     const uint32_t s_ref = __float_as_uint(__builtin_sqrtf(__uint_as_float(i)));
     if (s != s_ref && !(is_nan(s) && is_nan(s_ref))) record(&out[3], ex + 24, i);
     if (lv::xor_fold16(i) != ((i ^ (uint32_t)((int32_t)i >> 16)) & 0xFFFFu)) record(&out[4], ex + 32, i);
-    if (lv::xor_fold16_hi(i) != (((i ^ (i >> 16)) & 0xFFFFu) << 16)) record(&out[5], ex + 40, i);
+    const uint32_t zs[2] = {i * 0x9E3779B9u, mix32(i ^ 0x5bd1e995u)};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const uint32_t got = lv::pack_f16_rtz(lv::sr_fp16_val(__uint_as_float(i), zs[k]), 0.0f);
+        if (got != ref_f32_to_f16(ref_sr_f16(i, ref_prng(zs[k])))) record(&out[5], ex + 40, i);
+    }
     const uint32_t h = mix32(i);
     const uint32_t noises[6] = {0u, 1u, 0x7FFFu, 0x8000u, 0xFFFFu, h & 0xFFFFu};
 #pragma unroll
@@ -120,14 +136,13 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     const float x = __uint_as_float(i);
     const uint32_t mag = i & 0x7FFFFFFFu;
     const bool in_dom = mag == 0u || (mag >= 0x38800000u && mag < 0x477FE000u);  // 2^-14, 65504
-    if (lv::sr_f16_hw_domain(x) != in_dom) record(&out[9], ex + 72, i);
+    if (lv::sr_f16_domain(x) != in_dom) record(&out[9], ex + 72, i);
     if (in_dom) {
         if ((i & 0xFFFFu) == 0u) atomicAdd(&out[10], 1ull);  // sampled: one in 2^16
         const uint32_t nf[6] = {0u, 1u, 0x0FFFu, 0x1000u, 0x1FFFu, h & 0x1FFFu};
 #pragma unroll
         for (int k = 0; k < 6; k++) {
-            // the fp16 bits are the low half of the result
-            const uint32_t got = __float_as_uint(lv::sr_f16_hw(x, nf[k] << 19)) & 0xFFFFu;
+            const uint32_t got = lv::pack_f16_rtz(lv::sr_f16_add(x, nf[k]), 0.0f);
             if (got != ref_f32_to_f16(ref_sr_f16(i, nf[k]))) record(&out[9], ex + 72, i);
         }
     }
@@ -137,7 +152,7 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     }
 }
 
-// pack_f16_exact: every finite f16 value h (as f32), and the canonical quiet NaNs, against the
+// pack_f16_rtz: every finite f16 value h (as f32), and the canonical quiet NaNs, against the
 // reference's f32 -> f16 RNE; the packed word holds the value in both halves. The infinities are
 // not in the domain: the reference's fp16 quantisation saturates them to +-65504 (prng.rs:29-67,
 // prng.rs:98-130), so no quantised value is infinite.
@@ -148,7 +163,7 @@ __global__ void check_pack_f16(unsigned long long *out, uint32_t *ex) {
     if (is_nan(xb)) xb = (xb & 0x80000000u) | 0x7FC00000u;  // quantisation yields canonical NaNs only
     const float x = __uint_as_float(xb);
     const uint32_t want = ref_f32_to_f16(xb);
-    if (lv::pack_f16_exact(x, x) != (want | (want << 16))) record(&out[8], ex + 64, h);
+    if (lv::pack_f16_rtz(x, x) != (want | (want << 16))) record(&out[8], ex + 64, h);
 }
 
 __global__ void check_f16_to_f32(unsigned long long *out, uint32_t *ex) {

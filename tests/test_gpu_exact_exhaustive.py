@@ -7,17 +7,19 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   (the hardware returns them quietened, same sign);
 * sqrt_rn against the IEEE square root (the compiler's correctly rounded one, as Rust's
   f32::sqrt): all 2^32 inputs bit for bit, NaN for NaN;
-* xor_fold16 against (z ^ (z >> 16)) & 0xFFFF, and xor_fold16_hi against the same bits in the
-  high half: all 2^32 inputs;
+* xor_fold16 against (z ^ (z >> 16)) & 0xFFFF: all 2^32 inputs;
+* sr_fp16_val, the library's whole fp16 stochastic rounding (the domain's integer add, the wave's
+  switch to the integer recipe outside it, then pack_f16_rtz), against prng.rs:98-130 with the
+  noise of prng.rs:21-26: all 2^32 inputs x 2 hash inputs;
 * sr_bf16_checked (one integer add, with the out-of-range and NaN inputs replaced first when a
   lane of the wave has one) against the reference's integer recipe (prng.rs:137-160): all 2^32
   inputs x 6 noise values;
 * sqrt_rn_normal (no rescaling) against the IEEE square root on every input of its domain;
-* pack_f16_exact against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
+* pack_f16_rtz against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
   reference's fp16 quantisation never yields an infinity);
-* sr_f16_hw (the hardware fp16 stochastic-rounding converter) against the reference's integer
-  recipe (prng.rs:98-130) on every input of its domain (+-0 and 2^-14 <= |x| < 65504) x 6 noise
-  values, and its domain test on all 2^32 inputs.
+* sr_f16_add + pack_f16_rtz (the integer add and round-toward-zero pack) against the reference's
+  integer recipe (prng.rs:98-130) on every input of its domain (+-0 and 2^-14 <= |x| < 65504) x 6
+  noise values, and its domain test on all 2^32 inputs.
 """
 from __future__ import annotations
 
@@ -54,11 +56,11 @@ def test_exact_helpers_on_every_input():
     assert counts[2] <= 2 * 511
     assert counts[3] == 0, ("sqrt_rn", [hex(x) for x in ex[24:32]])
     assert counts[4] == 0, ("xor_fold16", [hex(x) for x in ex[32:40]])
-    assert counts[5] == 0, ("xor_fold16_hi", [hex(x) for x in ex[40:48]])
+    assert counts[5] == 0, ("sr_fp16_val", [hex(x) for x in ex[40:48]])
     assert counts[6] == 0, ("sr_bf16_checked", [hex(x) for x in ex[48:56]])
     assert counts[7] == 0, ("sqrt_rn_normal", [hex(x) for x in ex[56:64]])
-    assert counts[8] == 0, ("pack_f16_exact", [hex(x) for x in ex[64:72]])
-    assert counts[9] == 0, ("sr_f16_hw", [hex(x) for x in ex[72:80]])
+    assert counts[8] == 0, ("pack_f16_rtz", [hex(x) for x in ex[64:72]])
+    assert counts[9] == 0, ("sr_f16_add", [hex(x) for x in ex[72:80]])
     # domain size, sampled where the low 16 bits are zero: per sign, the zero and the multiples of
     # 2^16 in [0x38800000, 0x477FE000)
     per_sign = 1 + len(range(0x38800000, 0x477FE000, 65536))

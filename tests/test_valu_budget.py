@@ -34,10 +34,10 @@ SRC = os.path.join(HERE, "gpu_checks", "valu_budget.hip")
 # multiple of 0.5, plus 0.5. The anchors are the per-element counts of the instructions the
 # reference's arithmetic needs on the path: an IEEE division ends in one v_div_fixup_f32, a
 # correctly rounded root has one v_sqrt_f32, a hashed (stochastically rounded) stream two
-# v_mul_lo_u32, and an fp16 stochastic rounding one v_cvt_sr_f16_f32. A walk that skipped real
-# work (a branch the code never takes) would miss one of them. bf16 stochastic rounding is one
-# integer add on the path (v_cvt_sr_bf16_f32 takes about 3.4 times its issue time), so that converter
-# is anchored at zero.
+# v_mul_lo_u32, and a stored fp16 value half a v_cvt_pkrtz_f16_f32 (two per pack). A walk that
+# skipped real work (a branch the code never takes) would miss one of them. Stochastic rounding to
+# bf16 or fp16 is one integer add on the path (the v_cvt_sr_bf16_f32 / v_cvt_sr_f16_f32 converters
+# take about 3.4 times its issue time), so the converters are anchored at zero.
 #   T2: clm / env, the coordinate bound's quotient; sqrt(v). T1: the same without v.
 #   CLM: clm / sigma, the bound's step / b, two tanh quotients; sqrt(v), sqrt(p^2 + 1e-4).
 #   TD-CLM: clm / env, step / b, one tanh quotient; sqrt(p^2 + 1e-4).
@@ -54,7 +54,7 @@ KERNELS = {
                              {"v_div_fixup_f32": 2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0}),
     "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 90.5,
                                        {"v_div_fixup_f32": 3, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0,
-                                        "v_cvt_sr_f16_f32": 1}),
+                                        "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
     "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 120.0,
                      {"v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
     "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 91.5,
