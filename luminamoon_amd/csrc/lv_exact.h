@@ -31,7 +31,7 @@
 // The replacement runs only when a lane of the wave needs it (one compare per value). The
 // result is an f32 whose HIGH half holds the bf16 bits; its low half is NOT zero, so it is only
 // good for storing the high half. (gfx950's v_cvt_sr_bf16_f32 gives the same bits on its
-// domain but takes about 3.4 times an integer add's issue time.)
+// domain but takes about 3 times an integer add's issue time.)
 //
 // sr_f16_add: fp16 stochastic rounding (prng.rs:98-130) on its common domain, +-0 and
 // 2^-14 <= |v| < 65504 (sr_f16_domain). There the reference adds 13 noise bits (the low 13 of the
@@ -41,7 +41,7 @@
 // +-0 is an f32 far below the smallest fp16 subnormal, which converts to +-0. Outside the domain
 // callers take the integer recipe: below 2^-14 the reference widens both the cleared field and
 // the noise to 13 + k bits. (gfx950's v_cvt_sr_f16_f32 gives the same bits on the domain but takes
-// about 3.4 times an integer add's issue time, plus a shift to place its noise.)
+// about 3 times an integer add's issue time, plus a shift to place its noise.)
 //
 // The fp16 conversions need fp16 denormals enabled, the HIP default for gfx950 code objects.
 #pragma once

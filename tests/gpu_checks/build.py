@@ -1,4 +1,5 @@
-"""Builds the GPU check libraries of the tests (hipcc, gfx950, the library's own flags)."""
+"""Builds the GPU check libraries of the tests (hipcc, gfx950, the library's own flags): the exact
+helpers' exhaustive check and the VALU issue-rate probe."""
 from __future__ import annotations
 
 import os
@@ -12,21 +13,29 @@ if ROOT not in sys.path:
 
 EXACT_SRC = os.path.join(HERE, "exact_check.hip")
 EXACT_LIB = os.path.join(HERE, "libexactcheck.so")
+RATE_SRC = os.path.join(HERE, "issue_rate.hip")
+RATE_LIB = os.path.join(HERE, "libissuerate.so")
 
 
-def build(verbose: bool = False) -> str:
+def _build_one(src: str, lib: str, verbose: bool) -> None:
     from luminamoon_amd import build_ext
 
-    tmp = EXACT_LIB + ".tmp"
+    tmp = lib + ".tmp"
     cmd = [build_ext.hipcc(), *build_ext.HIPCC_FLAGS, "-I", os.path.join(ROOT, "luminamoon_amd", "csrc"),
-           "-I", os.path.join(ROOT, "include"), EXACT_SRC, "-o", tmp]
+           "-I", os.path.join(ROOT, "include"), src, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {EXACT_SRC}")
-    os.replace(tmp, EXACT_LIB)
+        raise RuntimeError(f"hipcc failed building {src}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    """Builds libexactcheck.so and libissuerate.so; returns the first's path."""
+    _build_one(EXACT_SRC, EXACT_LIB, verbose)
+    _build_one(RATE_SRC, RATE_LIB, verbose)
     return EXACT_LIB
 
 
