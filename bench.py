@@ -67,19 +67,19 @@ WORKLOADS = {
 _PROBE = dict(probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0)
 PMC_TRAFFIC = {
     (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
-                                                fetch_kib=39496781.6562, write_kib=66010493.8125, **_PROBE),
+                                                fetch_kib=39495825.9688, write_kib=66010492.8750, **_PROBE),
     (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=26325301.8438, write_kib=39585733.4375, **_PROBE),
+                                                 fetch_kib=26325554.6875, write_kib=39585737.2500, **_PROBE),
     (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
-                                                fetch_kib=3725898.4688, write_kib=5614386.375, **_PROBE),
+                                                fetch_kib=3726628.2812, write_kib=5614386.1875, **_PROBE),
     (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=2793077.3125, write_kib=3738077.3438, **_PROBE),
+                                                 fetch_kib=2793086.3750, write_kib=3738077.0938, **_PROBE),
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
-                                                    fetch_kib=2792924.5312, write_kib=3738077.0938, **_PROBE),
+                                                    fetch_kib=2792961.7812, write_kib=3738077.0938, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
-                                                fetch_kib=965740.1562, write_kib=1451871.1562, **_PROBE),
+                                                fetch_kib=965684.1562, write_kib=1451873.4062, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
-                                                fetch_kib=20713.4375, write_kib=27582.2812, **_PROBE),
+                                                fetch_kib=20713.6250, write_kib=27582.4219, **_PROBE),
 }
 
 # Untimed steps before the timed ones unless --warmup is given. After the inputs are generated the
