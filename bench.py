@@ -4,7 +4,9 @@ Default workload = configs[4] of BASELINE.json, the headline: buffer="T2", cauti
 params and grads with fp32 m/v, one contiguous 6,738,415,616-element bucket (Llama-7B shape),
 grads 1e-3 * Student-t(df=3). Inputs are generated on the GPU and stay resident in HBM; a step is
 one drop-in `LuminaV.step()`: at steady state one fused unit-kernel launch over the bucket, whose
-last block folds the mask count into the scratch. The HIP events bracket the step.
+last block folds the mask count into the scratch. The timed steps run back to back between two
+HIP events on the launch stream (their average is the roofline's launch time); ms_per_step is
+the wall clock over the same steps.
 
 Prints ONE JSON line with params/s (whole job), ms per step, achieved HBM GB/s against the
 8 TB/s peak (`roofline`), and the CPU oracle timed on a bounded sample on this host
@@ -87,6 +89,11 @@ PMC_TRAFFIC = {
 # traces of configs 3 and 4: launch times fall from 2.6 to 2.15 ms over the first 15 cfg4
 # steps); each config's default covers at least that much step time.
 DEFAULT_WARMUP = {5: 3, 4: 25, 3: 100, 2: 100}
+
+# Timed steps unless --steps is given: about half a second of step time or more, so the two
+# synchronizations and the events that bracket the timed region stay below 0.1% of it (cfg2's
+# step is ~20 us: 20 steps read 28 us per step, 2,000 read the loop's 20.7).
+DEFAULT_STEPS = {5: 20, 4: 200, 3: 1000, 2: 20000}
 
 
 def workload(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",
@@ -375,7 +382,7 @@ def cpu_threads() -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: per config)")
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps first (default: per config, covering the GPU's clock ramp)")
     ap.add_argument("--config", type=int, default=5, choices=sorted(WORKLOADS))
@@ -397,6 +404,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.warmup is None:
         args.warmup = DEFAULT_WARMUP[args.config]
+    if args.steps is None:
+        args.steps = DEFAULT_STEPS[args.config]
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (across GPUs the step "
                                    "would shard each bucket by element ranges, one range per rank)",
@@ -456,29 +465,41 @@ def main() -> int:
         opt.step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # The timed steps run back to back between ONE pair of HIP events on the launch stream: per-step
+    # event records would add host time to every step (about 6 us per step, a quarter of cfg2's).
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
+    t_start.record(stream)
+    for _ in range(args.steps):
         opt.step()
-        ends[i].record(stream)
+    t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    per_step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    ms_avg = sum(per_step_ms) / len(per_step_ms)
+    ms_avg = t_start.elapsed_time(t_end) / args.steps
     ms_wall = wall * 1e3 / args.steps
     params_per_s = n / (ms_wall / 1e3)
     bytes_launch = n * wl["bytes_per_param"]
     achieved = bytes_launch / (ms_avg / 1e3) / 1e9
-    log(f"per-step event ms: min {min(per_step_ms):.3f} avg {ms_avg:.3f} max {max(per_step_ms):.3f}; wall {ms_wall:.3f}")
+    # the per-step spread, from a short untimed pass with events around each step
+    spread = []
+    for _ in range(min(args.steps, 10)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        opt.step()
+        b.record(stream)
+        spread.append((a, b))
+    torch.cuda.synchronize()
+    per_step_ms = [a.elapsed_time(b) for a, b in spread]
+    log(f"timed steps: {ms_avg:.4f} ms per step on the stream (HIP events), wall {ms_wall:.4f}; "
+        f"untimed per-step check: min {min(per_step_ms):.4f} max {max(per_step_ms):.4f} ms")
     for q in params:
         sc = opt.state[q]["scratch"].tolist()
         if not all(math.isfinite(x) for x in sc):
             log(f"non-finite scratch {sc}")
             return 1
-    log(f"scratch of the last tensor after {args.warmup + args.steps} steps: {sc}")
+    log(f"scratch of the last tensor after {args.warmup + args.steps + len(spread)} steps: {sc}")
     floor = None
     if args.stream_floor:
         if len(params) != 1 or args.master != "none":

@@ -344,7 +344,11 @@ static void call_needs(const lv_config *cfg, const lv_tensor *T, int count, uint
 // and the new table is uploaded on the caller's stream. A slot is leased to one call from
 // acquisition until its launches are enqueued and its event recorded; a call on another stream
 // that reuses a slot first waits for the slot's earlier readers, so the event always covers
-// every reader.
+// every reader. A call on the null stream that reuses the slot the previous null-stream call
+// left (the steady step of a many-tensor group) records no event: the slot is marked `pending`,
+// and whoever next needs the event records it on the null stream first, which covers every
+// reader enqueued there (the null stream cannot be destroyed, so that record is always valid).
+// That spares one hipEventRecord of host time per step.
 constexpr int kRingSlots = 4;
 
 struct TableSlot {
@@ -354,7 +358,8 @@ struct TableSlot {
     size_t len = 0;   // descriptors of the table last uploaded (0: none)
     hipEvent_t ev = nullptr;
     hipStream_t last = nullptr;
-    bool used = false;  // ev has been recorded
+    bool used = false;     // ev has been recorded
+    bool pending = false;  // readers enqueued on the null stream (last) after ev was recorded
     bool busy = false;
     uint64_t stamp = 0;
 };
@@ -372,6 +377,13 @@ struct TableLease {
     TableSlot *s = nullptr;
     bool uploaded = false;
 };
+
+// Records a leased slot's deferred event on the null stream (see above); false on failure.
+static bool record_pending(TableSlot &s) {
+    if (hipEventRecord(s.ev, nullptr) != hipSuccess) return false;
+    s.pending = false;
+    return true;
+}
 
 static int acquire_table(const TDesc *want, size_t n, hipStream_t stream, TableLease &lease) {
     int dev = 0;
@@ -393,7 +405,8 @@ static int acquire_table(const TDesc *want, size_t n, hipStream_t stream, TableL
             lk.unlock();
             lease.s = &s;
             lease.uploaded = false;
-            if (s.used && s.last != stream && hipStreamWaitEvent(stream, s.ev, 0) != hipSuccess) {
+            if (s.used && s.last != stream &&
+                ((s.pending && !record_pending(s)) || hipStreamWaitEvent(stream, s.ev, 0) != hipSuccess)) {
                 lk.lock();
                 s.busy = false;
                 return fail(LV_STATUS_EXECUTION_FAILED, "descriptor table wait failed");
@@ -423,7 +436,7 @@ static int acquire_table(const TDesc *want, size_t n, hipStream_t stream, TableL
     };
     if (!s.ev && hipEventCreateWithFlags(&s.ev, hipEventDisableTiming) != hipSuccess)
         return give_back(fail(LV_STATUS_EXECUTION_FAILED, "event creation failed"));
-    if (s.used && hipEventSynchronize(s.ev) != hipSuccess)
+    if (s.used && ((s.pending && !record_pending(s)) || hipEventSynchronize(s.ev) != hipSuccess))
         return give_back(fail(LV_STATUS_EXECUTION_FAILED, "descriptor table event wait failed"));
     s.len = 0;
     if (s.cap < n) {
@@ -457,10 +470,19 @@ static int acquire_table(const TDesc *want, size_t n, hipStream_t stream, TableL
 static int release_table(TableLease &lease, hipStream_t stream) {
     if (!lease.s) return LV_STATUS_SUCCESS;
     TableSlot &s = *lease.s;
+    if (stream == nullptr && !lease.uploaded && s.used && s.last == nullptr) {
+        // a reuse on the null stream after null-stream readers: defer the record
+        std::lock_guard<std::mutex> g(g_ring_mu);
+        s.pending = true;
+        s.busy = false;
+        lease.s = nullptr;
+        return LV_STATUS_SUCCESS;
+    }
     const bool ok = hipEventRecord(s.ev, stream) == hipSuccess;
     std::lock_guard<std::mutex> g(g_ring_mu);
     if (ok) {
         s.used = true;
+        s.pending = false;
         s.last = stream;
     } else {
         s.len = 0;  // nothing certain covers this slot's readers: never reuse its bytes

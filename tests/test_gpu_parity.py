@@ -251,6 +251,63 @@ def test_table_launches_from_two_host_threads(oracle_mod):
         host.assert_equal(dev, f"thread {k}")
 
 
+
+def test_table_reuse_on_the_null_stream_then_other_streams_and_evictions(oracle_mod):
+    """A table launch that reuses its descriptor-table slot on the null stream after null-stream
+    readers records no event (the slot is marked pending). One 100-tensor set keeps its grads in
+    fixed buffers, so every step reuses the same table: steps 1-3 on the null stream (an upload,
+    then two deferred reuses), step 4 on a side stream (the reuse records the pending event and
+    waits for it), step 5 on the null stream again, then five other sets on the null stream,
+    which rewrite every slot of the device's ring (the pending one included), and step 6 of the
+    first set (a fresh upload). Every set ends bit for bit equal to the oracle."""
+    import numpy as np
+
+    _need_gpu()
+    O = oracle_mod
+    group = group_dict(buffer="T2", lr=1e-3)
+    cfg = oracle_config(O, group)
+    rng = np.random.default_rng(11)
+
+    def make(seed):
+        sizes = [int(np.exp(rng.uniform(0, np.log(5000)))) + 1 for _ in range(100)]
+        host = TensorSet(sizes, "bf16", "bf16", "f32", True, False, seed)
+        return host, host.to("cuda"), _stepper()
+
+    host, dev, st = make(60)
+    gbufs = [g.cuda() for g in host.grads(1, 70)]  # fixed addresses: the table stays the same
+    side = torch.cuda.Stream()
+
+    def step(s, stream=None):
+        gs = host.grads(s, 70 + s)
+        ctx = torch.cuda.stream(stream) if stream is not None else torch.cuda.stream(torch.cuda.default_stream())
+        with ctx:
+            for buf, g in zip(gbufs, gs):
+                buf.copy_(g, non_blocking=False)
+            dev.hip_step(st, group, gbufs, s)
+        host.oracle_step(O, cfg, gs, s)
+
+    print("[case] table reuse: null stream x3, side stream, null stream", flush=True)
+    for s in (1, 2, 3):
+        step(s)
+    torch.cuda.default_stream().synchronize()
+    step(4, side)
+    side.synchronize()
+    step(5)
+    torch.cuda.synchronize()
+    host.assert_equal(dev, "after the stream changes")
+    print("[case] table reuse: five other sets rewrite the ring", flush=True)
+    others = [make(80 + k) for k in range(5)]
+    for k, (h2, d2, st2) in enumerate(others):
+        for s in (1, 2):
+            gs = h2.grads(s, 90 + 10 * k + s)
+            d2.hip_step(st2, group, [g.cuda() for g in gs], s)
+            h2.oracle_step(O, cfg, gs, s)
+    step(6)
+    torch.cuda.synchronize()
+    host.assert_equal(dev, "after the evictions")
+    for k, (h2, d2, _) in enumerate(others):
+        h2.assert_equal(d2, f"other set {k}")
+
 def _table_case(oracle_mod, count, buffer, pdt, sdt, extra):
     """`count` ragged tensors (plus three larger ones) stepped three times, bitwise against the
     oracle, with the whole workspace checked zero after every step."""
