@@ -154,6 +154,56 @@ def test_corrupted_state_propagates_like_the_scalar_core(oracle_mod, buffer, pdt
         assert any(bool(torch.isnan(t.float()).any()) for t in host.p), "a NaN param stays NaN"
 
 
+
+# fp16 param values at both ends of the fp16 range: subnormals, the lowest normal binade, the
+# largest finite value and zeros. A param that a step leaves below 2^-14 or that a step pushes to
+# 65504 or past it is outside the integer add's domain, so its wave takes the reference's integer
+# recipe (prng.rs:98-130: the widened field for subnormals, the saturation at 65504).
+F16_ENDS = [6e-8, -1.2e-7, 3.1e-6, -4.5e-5, 6.1e-5, -9.2e-5, 1.2e-4, 65504.0, -65504.0, 65000.0,
+            -64990.0, 0.0, -0.0, 2.0e-5]
+
+
+@pytest.mark.parametrize("buffer,sdt,extra", [
+    ("T2", "f32", {}),
+    ("T2", "f32", {"weight_decay": 0.0}),
+    ("T1", "f16", {"state_precision": "param"}),
+    (2, "f16", {"state_precision": "param", "weight_decay": 0.0}),
+], ids=["T2", "T2-no-wd", "T1-param", "CLM-param-no-wd"])
+def test_fp16_params_at_the_ends_of_the_fp16_range(oracle_mod, buffer, sdt, extra):
+    """fp16 params from F16_ENDS fill the first 1,500 elements of the first tensor (whole units,
+    so mixed waves run the recipe for in-domain lanes too) and every element of the second (the
+    per-element path of a partial unit); three steps, bit for bit against the oracle."""
+    O = oracle_mod
+    _need_gpu()
+    kw = dict(extra)
+    kw.setdefault("lr", 1e-3)
+    group = group_dict(buffer=buffer, **kw)
+    dual = group["buffer"] in (2, "T2")
+    host = TensorSet(SIZES, "f16", "f16", sdt, dual, False, seed=47, m_scale=1e-3)
+    vals = torch.tensor(F16_ENDS, dtype=torch.float32)
+    host.p[0][:1500] = vals.repeat(1500 // len(F16_ENDS) + 1)[:1500].to(torch.float16)
+    host.p[1][:] = vals.repeat(SIZES[1] // len(F16_ENDS) + 1)[:SIZES[1]].to(torch.float16)
+    dev = host.to("cuda")
+    cfg = oracle_config(O, group)
+    from luminamoon_amd.optimizer.hip_backend import HipStepper
+
+    st = HipStepper()
+    label = f"fp16 range ends buffer={buffer} state={sdt} {extra}"
+    print(f"[case] {label}", flush=True)
+    for s in range(1, 4):
+        grads = host.grads(s, 53)
+        host.oracle_step(O, cfg, grads, s)
+        dev.hip_step(st, group, [g.cuda() for g in grads], s)
+        torch.cuda.synchronize()
+        for i in range(len(SIZES)):
+            assert _assert_same(host.p[i], dev.p[i], f"{label} step {s} p[{i}]") == 0
+            assert _assert_same(host.m[i], dev.m[i], f"{label} step {s} m[{i}]") == 0
+            if dual:
+                assert _assert_same(host.v[i], dev.v[i], f"{label} step {s} v[{i}]") == 0
+            assert _assert_same(host.sc[i], dev.sc[i], f"{label} step {s} scratch[{i}]") == 0
+    subnormal = [int(((bits(t.cpu()) & 0x7C00) == 0).sum()) - int(((bits(t.cpu()) & 0x7FFF) == 0).sum()) for t in host.p]
+    assert sum(subnormal) > 0, "some params stay fp16 subnormals (the recipe's widened field ran)"
+
 def test_radial_with_special_gradients(oracle_mod):
     """Radial bound: the squared norms see only sanitised gradients, so the sums stay finite and
     the f64 sums match the oracle's f64 mode bit for bit."""
