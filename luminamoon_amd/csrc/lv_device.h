@@ -919,6 +919,13 @@ __device__ __forceinline__ void open_step(const Args &a, const Desc &D, int t, u
         tv.slot_base = (uint32_t)t * kSlotWords;
     }
     tv.ibase = D.ibase;
+    // The scales are loaded before the step record is read, so that a graph launch waits for both
+    // loads at once rather than for one after the other.
+    float cs = 1.0f, bs = 1.0f;
+    if constexpr (PASS == kFused || PASS == kApply) {
+        cs = D.scratch[3];
+        bs = D.scratch[4];
+    }
     uint32_t seed_base = a.seed_base;
     tv.k = {a.c1, a.c2, a.c_sigma};
     tv.skip = false;
@@ -932,18 +939,15 @@ __device__ __forceinline__ void open_step(const Args &a, const Desc &D, int t, u
     tv.sd.m = (int32_t)(raw & 0x7FFFFFFFu);
     tv.sd.p = (int32_t)(((uint32_t)tv.sd.m + 0x55555555u) & 0x7FFFFFFFu);
     tv.sd.v = (int32_t)(((uint32_t)tv.sd.m + 0x2A6D365Bu) & 0x7FFFFFFFu);
-    tv.cs = 1.0f;
-    tv.bs = 1.0f;
-    if constexpr ((PASS == kFused || PASS == kApply) && TABLE) {
-        // a vector load here (the descriptor is in device memory), waited for only where used
-        tv.cs = D.scratch[3];
-        tv.bs = D.scratch[4];
-    } else if constexpr (PASS == kFused || PASS == kApply) {
-        // Read after the stream loads, these come back through the vector memory path; the
+    if constexpr ((PASS == kFused || PASS == kApply) && !TABLE) {
+        // Read after the stream loads, the scales come back through the vector memory path; the
         // values are block-uniform and stay in scalar registers.
-        tv.cs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, D.scratch[3])));
-        tv.bs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, D.scratch[4])));
+        cs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs)));
+        bs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, bs)));
     }
+    // (table launches read the descriptor from device memory: a vector load, waited for where used)
+    tv.cs = cs;
+    tv.bs = bs;
     if constexpr (PASS == kSingle) {
         // reset_accumulators (state.rs:105-111) with the host-side forcing of slots 3/4
         // that the reference applies when cautious/radial are off (luminav.py:1748-1751).
@@ -1258,6 +1262,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     if (vec) {
         const Inflight f = issue_at<MODE, PT, ST, PASS, H, HS>(D, flags, radial, e0);
         if constexpr (!TABLE) {
+            __builtin_amdgcn_sched_barrier(0);  // every stream load is issued before the step's reads
             open_step<MODE, PASS, TABLE>(a, D, t, unit, tv);
             // A graph step refused by its step record changes nothing (block-uniform; the loads
             // above only read).
