@@ -151,3 +151,12 @@ def test_stream_probe_rejects_invalid_arguments_before_any_launch():
     for change in bad:
         c = {**ok, **change}
         assert fn(c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"], None) == 1, change
+
+
+def test_every_config_has_default_steps_and_warmup():
+    """Each workload times about half a second of steps or more by default (cfg2's ~20 us step
+    needs thousands for the bracketing synchronizations to vanish) and warms up first."""
+    step_ms = {5: 23.1, 4: 2.13, 3: 0.57, 2: 0.021}
+    for c in bench.WORKLOADS:
+        assert bench.DEFAULT_STEPS[c] > 0 and bench.DEFAULT_WARMUP[c] > 0
+        assert bench.DEFAULT_STEPS[c] * step_ms[c] >= 400.0, c
