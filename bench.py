@@ -190,24 +190,83 @@ def copy_probe(torch, n_floats: int = 1 << 30, reps: int = 5) -> float:
     return 8.0 * n_floats / (ms / 1e3) / 1e9
 
 
+PROBE_SRC = os.path.join(ROOT, "stream_probe.hip")
+PROBE_LIB = os.path.join(ROOT, "_build", "libstream_probe.so")
+
+
+def build_stream_probe() -> str:
+    """Compiles stream_probe.hip (the bare streaming kernel of --stream-floor) into
+    _build/libstream_probe.so with the optimizer library's flags, when it is missing or older than
+    its source. It is a measurement tool of this script, not part of the optimizer library."""
+    import subprocess
+
+    from luminamoon_amd import build_ext
+
+    if os.path.exists(PROBE_LIB) and os.path.getmtime(PROBE_LIB) >= os.path.getmtime(PROBE_SRC):
+        return PROBE_LIB
+    os.makedirs(os.path.dirname(PROBE_LIB), exist_ok=True)
+    tmp = PROBE_LIB + f".tmp{os.getpid()}"
+    res = subprocess.run([build_ext.hipcc(), *build_ext.HIPCC_FLAGS, PROBE_SRC, "-o", tmp], capture_output=True,
+                         text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building stream_probe.hip")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
+def stream_probe_fn():
+    """lv_stream_probe(param_bytes, state_bytes, nstate, p, g, m, v, n, stream) -> 0 or 1."""
+    import ctypes
+
+    fn = ctypes.CDLL(build_stream_probe()).lv_stream_probe
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    return fn
+
+
+def check_stream_probe(torch, fn, pb: int, sb: int, ns: int) -> None:
+    """The probe writes exactly what it states on a few sizes of this element-size combination,
+    so the bandwidth it reports is that of real reads and writes of whole buffers: p ^= g word by
+    word, m ^= the group's first gradient word, v ^= the group's first old m word (groups of 4
+    elements), and nothing past n elements."""
+    import numpy as np
+
+    pad = 64
+    for i, n in enumerate((4, 1024, 3 * 1024 + 520, 40_000)):
+        rng = np.random.default_rng(100 * pb + 10 * sb + ns + i)
+        host = {k: rng.integers(0, 256, size=(n + pad) * w, dtype=np.uint8)
+                for k, w in (("p", pb), ("g", pb), ("m", sb), ("v", sb))}
+        dev = {k: torch.from_numpy(x.copy()).cuda() for k, x in host.items()}
+        rc = fn(pb, sb, ns, dev["p"].data_ptr(), dev["g"].data_ptr(), dev["m"].data_ptr(),
+                dev["v"].data_ptr() if ns == 2 else None, n, torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lv_stream_probe returned {rc} on its check")
+        torch.cuda.synchronize()
+        w = {k: x.view(np.uint32) for k, x in host.items()}
+        groups = n // 4
+        exp = {k: x.copy() for k, x in w.items()}
+        exp["p"][:groups * pb] ^= w["g"][:groups * pb]
+        exp["m"][:groups * sb] ^= np.repeat(w["g"][0:groups * pb:pb], sb)
+        if ns == 2:
+            exp["v"][:groups * sb] ^= np.repeat(w["m"][0:groups * sb:sb], sb)
+        for k in ("p", "g", "m", "v"):
+            if not np.array_equal(dev[k].cpu().numpy().view(np.uint32), exp[k]):
+                raise RuntimeError(f"stream probe check failed: {k} (pb={pb} sb={sb} ns={ns} n={n})")
+
+
 def stream_floor(torch, p, g, m, v, reps: int) -> dict:
-    """The stream floor of the step (--stream-floor): libstream_probe.so's bare kernel reads and
+    """The stream floor of the step (--stream-floor): the bare kernel of stream_probe.hip reads and
     writes the step's own buffers (p and the state read and written, g read; same element sizes,
     1024-element blocks, 4 consecutive elements per thread, non-temporal accesses) with no
     arithmetic, lookup or count, `reps` launches back to back between HIP events on the current
     stream. Its bandwidth is what the hardware gives that read/write mix on these very pages. It
     overwrites the buffers, so it runs after every read of the optimizer's state."""
-    import ctypes
-
-    from luminamoon_amd import build_ext
-
-    lib = ctypes.CDLL(build_ext.PROBE_OUT)
-    fn = lib.lv_stream_probe
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    fn = stream_probe_fn()
     pb, sb, ns, n = p.element_size(), m.element_size(), 1 if v is None else 2, p.numel()
     assert g.element_size() == pb and g.numel() == n and m.numel() == n and (v is None or v.numel() == n)
+    check_stream_probe(torch, fn, pb, sb, ns)
     stream = torch.cuda.current_stream()
 
     def launch():
@@ -229,6 +288,59 @@ def stream_floor(torch, p, g, m, v, reps: int) -> dict:
     gbs = n * bpp / (ms / 1e3) / 1e9
     return {"gb_per_s": gbs, "frac": gbs / HBM_PEAK_GBS, "ms": ms, "bytes_per_param": bpp, "reps": reps,
             "kernel": f"stream_probe_kernel<{pb}, {sb}, {ns}>"}
+
+
+def offset_ab(torch, n: int, offset: int, steps: int, rounds: int = 5) -> dict:
+    """--offset-ab K: the unaligned-view path against the aligned one on the same buffers. One set
+    of T2 buffers (bf16 p/g, fp32 m/v, cautious, n elements plus slack) is stepped through the C
+    ABI as the view [0, n) and as the view [K, K + n) of every buffer (each view its own scratch),
+    `rounds` times `steps` steps each, alternating; each batch is timed between HIP events on the
+    stream. The views share their physical pages, so placement cancels out. Returns both median
+    batch times per step and their ratio."""
+    from luminamoon_amd.optimizer.hip_backend import HipStepper
+    from luminamoon_amd.optimizer.luminav import LuminaV
+
+    group = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.08, tau=0.8, lam=0.3, cautious=True,
+                 cautious_clamp_min=0.5, buffer="T2", stochastic_rounding=True, bound=True, bound_type="coordinate",
+                 bound_ratio=0.05, master_weights="none", execution="auto", fused_single_pass=True,
+                 fuse_tensors=False, bucket_cap_mb=500.0, prewarm_jit=True, ema_decay="auto", fsdp_sync=False,
+                 seed=1337, version=None, spec=None)
+    LuminaV._validate_and_normalize_group(group)
+    slack = 16
+    p, g = fill_inputs(torch, n + slack, torch.bfloat16, "student_t3", seed=77)
+    m = torch.zeros(n + slack, dtype=torch.float32, device="cuda")
+    v = torch.zeros(n + slack, dtype=torch.float32, device="cuda")
+    views = {k: (p[k:k + n], g[k:k + n], m[k:k + n], v[k:k + n],
+                 torch.tensor([0, 0, 0, 1, 1, 0.0], device="cuda")) for k in (0, offset)}
+    st = HipStepper()
+    preps = {k: st.prepare([x[0]], [x[1]], [x[2]], [x[3]], [None], [x[4]], [1], [0]) for k, x in views.items()}
+    count = {k: 0 for k in views}
+    stream = torch.cuda.current_stream()
+
+    def run(k: int, reps: int) -> None:
+        for _ in range(reps):
+            count[k] += 1
+            preps[k].set_steps([count[k]])
+            st.launch(group, preps[k])
+
+    for k in views:  # step 1 (two-pass) and a warm-up
+        run(k, 5)
+    times = {k: [] for k in views}
+    for _ in range(rounds):
+        for k in views:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            run(k, steps)
+            b.record(stream)
+            b.synchronize()
+            times[k].append(a.elapsed_time(b) / steps)
+    med = {k: sorted(t)[len(t) // 2] for k, t in times.items()}
+    bytes_step = 22.0 * n
+    return {"n": n, "offset_elements": offset, "steps_per_batch": steps, "rounds": rounds,
+            "aligned_ms": med[0], "offset_ms": med[offset], "offset_over_aligned": med[offset] / med[0],
+            "aligned_frac": bytes_step / (med[0] / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "offset_frac": bytes_step / (med[offset] / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "batches_ms": {str(k): t for k, t in times.items()}}
 
 
 def cpu_baseline(workload: dict, threads: int, target_s: float = 15.0) -> dict:
@@ -401,6 +513,10 @@ def main() -> int:
     ap.add_argument("--stream-floor", action="store_true",
                     help="after the timed steps, time a bare kernel that streams the step's own buffers "
                          "(one-tensor configs without master weights)")
+    ap.add_argument("--offset-ab", type=int, default=None, metavar="K",
+                    help="instead of a config: a T2 bf16/fp32-state tensor stepped as a view K elements into "
+                         "its buffers against the aligned view of the same buffers (prints its own JSON line)")
+    ap.add_argument("--elems", type=int, default=1 << 27, help="elements of the --offset-ab tensor")
     args = ap.parse_args()
     if args.warmup is None:
         args.warmup = DEFAULT_WARMUP[args.config]
@@ -421,6 +537,16 @@ def main() -> int:
     if not torch.cuda.is_available():
         log("no GPU visible")
         return 1
+    if args.offset_ab is not None:
+        if not 0 < args.offset_ab < 16:
+            print(json.dumps({"error": "--offset-ab takes an element offset from 1 to 15"}), flush=True)
+            return 2
+        res = offset_ab(torch, args.elems, args.offset_ab, steps=args.steps if args.steps else 20)
+        log(f"offset A/B: aligned {res['aligned_ms']:.4f} ms, +{args.offset_ab} elements {res['offset_ms']:.4f} ms "
+            f"per step (ratio {res['offset_over_aligned']:.4f})")
+        print(json.dumps({"metric": "unaligned view / aligned view step time, same buffers", "offset_ab": res}),
+              flush=True)
+        return 0
     try:
         wl = workload(args.config, args.bound, args.state, args.master, args.pdt)
     except ValueError as e:

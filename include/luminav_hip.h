@@ -97,9 +97,12 @@ int lv_version(void);
 /* Workspace. lv_step_multi needs caller-owned device memory, 256-byte aligned, ZERO-FILLED before
  * its first use; every call leaves all of it zero again (the kernels re-zero the cautious count
  * slots and tickets they use, and the radial fold zeroes every record it reads), so one workspace
- * serves every later call, whatever its tensors or options. Calls that share a workspace must
- * not overlap in time (stream-ordered calls on one stream are fine). After a call that returned
- * LV_STATUS_EXECUTION_FAILED (a launch failed part-way), zero it again before reusing it.
+ * serves every later call, whatever its tensors or options. Calls that share a workspace are
+ * ordered by the library: a call on another stream than the workspace's previous call first
+ * waits for that call (an event the library records after it; after a call on the NULL stream the
+ * event is recorded only when another stream needs it). One host thread at a time may call with a
+ * given workspace. After a call that returned LV_STATUS_EXECUTION_FAILED (a launch failed
+ * part-way), zero it again before reusing it.
  * Layout of one call: 195 KiB of inline count slots (48 tensors x 65 slots x 64 B) and 2 KiB of
  * radial tickets and running sums; with more than 48 tensors in a launch class, table count
  * slots (per tensor, one fold slot plus the smallest power of two of slots that keeps every slot
@@ -187,7 +190,8 @@ int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int co
  * The one deliberate difference: device pointers and a stream instead of the engine and host
  * buffers (luminav_triton_step_f32 below takes those). The step runs like lv_step_multi's (the
  * reference CPU core's pass selection). Uses an internal per-device workspace allocated on first
- * use: calls on one device share it, so calls on different streams must not overlap in time.
+ * use: calls on one device share it, and a call on another stream than the previous one waits for
+ * it (as lv_step_multi's workspace ordering).
  */
 int lv_step_f32(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
                 float *master_param, float *scratch, size_t num_elements, float lr, float beta1,

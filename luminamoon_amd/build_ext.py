@@ -2,8 +2,7 @@
 
 Five objects compiled in parallel and linked into one shared library: the host side and C ABI
 (csrc/luminav_hip.hip) and the kernels of each buffer mode (csrc/lv_kernels.hip with
--DLV_MODE=1..4). Alongside, libstream_probe.so (csrc/stream_probe.hip): the bare streaming kernel
-that bench.py --stream-floor times on a step's buffers; not part of the optimizer library.
+-DLV_MODE=1..4).
 
 Flags that the bitwise-parity contract depends on:
   -ffp-contract=off                          no fused multiply-add except the explicit fmaf calls
@@ -26,8 +25,6 @@ KERNEL_SRC = os.path.join(CSRC, "lv_kernels.hip")
 SRC = HOST_SRC
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libluminav_hip.so")
-PROBE_SRC = os.path.join(CSRC, "stream_probe.hip")
-PROBE_OUT = os.path.join(OUT_DIR, "libstream_probe.so")
 ARCH = os.environ.get("LUMINAV_OFFLOAD_ARCH", "gfx950")
 MODES = (1, 2, 3, 4)  # LV_BUFFER_TDCLM, _DUAL, _T1, _T2
 
@@ -63,11 +60,9 @@ def build(verbose: bool = False) -> str:
     for m in MODES:
         jobs.append(([hipcc(), *COMPILE_FLAGS, *inc, f"-DLV_MODE={m}", "-c", KERNEL_SRC,
                       "-o", os.path.join(OUT_DIR, f"kernels_{m}.o")], f"{KERNEL_SRC} (mode {m})"))
-    jobs.append(([hipcc(), *HIPCC_FLAGS, PROBE_SRC, "-o", PROBE_OUT + ".tmp"], PROBE_SRC))
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
         for f in [ex.submit(_run, cmd, what, verbose) for cmd, what in jobs]:
             f.result()
-    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     tmp = OUT + ".tmp"
     objs = [os.path.join(OUT_DIR, "host.o")] + [os.path.join(OUT_DIR, f"kernels_{m}.o") for m in MODES]
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], OUT, verbose)

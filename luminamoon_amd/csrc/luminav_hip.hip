@@ -493,6 +493,70 @@ static int release_table(TableLease &lease, hipStream_t stream) {
     return ok ? LV_STATUS_SUCCESS : fail(LV_STATUS_EXECUTION_FAILED, "descriptor table event record failed");
 }
 
+// ------------------------------------------------------------------ workspace ordering
+
+// Calls that share a workspace share its count slots and radial records, so each must start after
+// the previous one has finished. Calls on one stream are ordered by the stream; a call on another
+// stream first waits for an event that follows the previous call. The library keeps one such
+// record per workspace address (a handful per process; kept until it ends). A call on a non-null
+// stream records its event right after its launches. A call on the null stream records none: the
+// next call from another stream records it on the null stream first, which covers everything
+// enqueued there (the null stream cannot be destroyed, so that late record is always valid), so
+// the steady step on the null stream pays no event. The reference gives every parameter scratch
+// of its own for the same reason (changelogs/LUMINAV_ALGORITHM_CHANGELOG.md:281-283).
+struct WsOrder {
+    const void *ws = nullptr;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool called = false;   // a call has used the workspace
+    bool recorded = false;  // ev follows the last call (else: the last call was on the null stream)
+};
+
+static std::mutex g_order_mu;
+static std::vector<WsOrder *> g_orders;
+
+// Makes `stream` wait for the previous call on workspace `ws` when that call ran on another
+// stream. Returns the workspace's record (locked by the caller's sequencing: one host thread per
+// workspace at a time, as the header requires).
+static int order_before(const void *ws, hipStream_t stream, WsOrder *&out) {
+    WsOrder *o = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_order_mu);
+        for (WsOrder *x : g_orders)
+            if (x->ws == ws) o = x;
+        if (!o) {
+            o = new (std::nothrow) WsOrder();
+            if (!o) return fail(LV_STATUS_EXECUTION_FAILED, "workspace order record allocation failed");
+            o->ws = ws;
+            g_orders.push_back(o);
+        }
+    }
+    out = o;
+    if (!o->called || o->last == stream) return LV_STATUS_SUCCESS;
+    if (!o->ev && hipEventCreateWithFlags(&o->ev, hipEventDisableTiming) != hipSuccess)
+        return fail(LV_STATUS_EXECUTION_FAILED, "event creation failed");
+    if (!o->recorded) {  // the previous call ran on the null stream
+        if (hipEventRecord(o->ev, nullptr) != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "event record failed");
+        o->recorded = true;
+    }
+    if (hipStreamWaitEvent(stream, o->ev, 0) != hipSuccess)
+        return fail(LV_STATUS_EXECUTION_FAILED, "stream wait on the previous workspace user failed");
+    return LV_STATUS_SUCCESS;
+}
+
+// After a call's launches on `stream` were enqueued.
+static int order_after(WsOrder *o, hipStream_t stream) {
+    o->called = true;
+    o->last = stream;
+    o->recorded = false;
+    if (stream == nullptr) return LV_STATUS_SUCCESS;  // recorded late, if another stream needs it
+    if (!o->ev && hipEventCreateWithFlags(&o->ev, hipEventDisableTiming) != hipSuccess)
+        return fail(LV_STATUS_EXECUTION_FAILED, "event creation failed");
+    if (hipEventRecord(o->ev, stream) != hipSuccess) return fail(LV_STATUS_EXECUTION_FAILED, "event record failed");
+    o->recorded = true;
+    return LV_STATUS_SUCCESS;
+}
+
 // ------------------------------------------------------------------ launches
 
 // Unit launches of one class over args.total_units units, in pieces of at most kMaxGrid blocks
@@ -541,7 +605,36 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
     return LV_STATUS_SUCCESS;
 }
 
-static void fill_desc(Desc &D, const lv_tensor &T, const Item &it) {
+// Where a tensor's vector layout starts: the smallest h < 8 at which every stream the kernel moves
+// (param, grad, exp_avg, exp_avg_sq in the two-buffer modes, the master copy) is 16-byte aligned.
+// A view that starts h elements past an aligned address in all of its buffers (a slice of a
+// bucket, a shard) gets head h; buffers that disagree, or a tensor of at most h elements, get no
+// vector layout and go element by element.
+static bool vector_head(const lv_tensor &T, const Item &it, bool dual, uint32_t &head) {
+    struct Stream {
+        uintptr_t addr;
+        int bytes;
+    } st[5];
+    int ns = 0;
+    st[ns++] = {(uintptr_t)T.param, dtype_bytes(it.pt)};
+    st[ns++] = {(uintptr_t)T.grad, dtype_bytes(it.gt)};
+    st[ns++] = {(uintptr_t)T.exp_avg, dtype_bytes(it.st)};
+    if (dual) st[ns++] = {(uintptr_t)T.exp_avg_sq, dtype_bytes(it.st)};
+    if (it.master) st[ns++] = {(uintptr_t)T.master_param, 4};
+    head = 0;
+    for (uint32_t h = 0; h < 8; h++) {
+        bool ok = true;
+        for (int k = 0; k < ns && ok; k++) ok = ((st[k].addr + (uintptr_t)h * (uintptr_t)st[k].bytes) & 15u) == 0;
+        if (ok) {
+            if ((uint64_t)h >= T.numel) return false;
+            head = h;
+            return true;
+        }
+    }
+    return false;
+}
+
+static void fill_desc(Desc &D, const lv_tensor &T, const Item &it, bool dual) {
     D.p = T.param;
     D.g = T.grad;
     D.m = T.exp_avg;
@@ -552,8 +645,17 @@ static void fill_desc(Desc &D, const lv_tensor &T, const Item &it) {
     D.unit_begin = 0;
     D.pidx = (uint32_t)T.param_index;
     D.ibase = (uint32_t)T.index_base;
-    D.nskip = (uint32_t)T.n_inactive;
+    D.nskip = (uint32_t)T.n_inactive;  // < 2^24 (prepare_call)
+    uint32_t head = 0;
+    D.vec = vector_head(T, it, dual, head) ? 1u : 0u;
+    D.head = head;
     D.skip = T.n_inactive ? T.inactive : nullptr;
+}
+
+// Work units of a tensor: they start at its vector head, so an unaligned view may have one fewer
+// than an aligned tensor of the same size (never more: call_needs counts from element 0).
+static uint64_t desc_units(const Desc &D, uint32_t unit_elems) {
+    return units_of(D.n - (D.vec ? D.head : 0u), unit_elems);
 }
 
 static void fill_args_common(Args &args, const lv_config *cfg, const Item &h, int bound) {
@@ -637,7 +739,8 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
         if (cfg->master_weights != 0 && !mp_present && T.param_dtype != LV_DTYPE_F32)
             return fail(LV_STATUS_NULL_POINTER, "tensor %d: Master weight mode requires an initialized master_param buffer", i);
         if (T.n_inactive && !T.inactive) return fail(LV_STATUS_NULL_POINTER, "tensor %d: inactive ranges pointer is NULL", i);
-        if (T.n_inactive > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many inactive ranges", i);
+        if (T.n_inactive > 0xFFFFFFull)
+            return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many inactive ranges (at most 2^24 - 1)", i);
         Item it;
         it.idx = i;
         it.pt = T.param_dtype;
@@ -657,6 +760,7 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
 static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items, int nitems, const Layout &L,
                     hipStream_t stream, std::vector<TDesc> *tab_buf, const lv_step_record *rec = nullptr) {
     const int bound = (cfg->bound && cfg->bound_ratio > 0.0f) ? cfg->bound_type : LV_BOUND_NONE;
+    const bool dual = cfg->buffer == LV_BUFFER_DUAL || cfg->buffer == LV_BUFFER_T2;
     std::sort(items, items + nitems, item_less);
     for (int begin = 0; begin < nitems;) {
         const Item &h = items[begin];
@@ -677,8 +781,8 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
                 const lv_tensor &T = tensors[items[begin + k].idx];
                 TDesc &E = tab[(size_t)k];
                 std::memset(&E, 0, sizeof E);
-                fill_desc(E.d, T, items[begin + k]);
-                const uint64_t u = units_of(T.numel, unit_elems);
+                fill_desc(E.d, T, items[begin + k], dual);
+                const uint64_t u = desc_units(E.d, unit_elems);
                 E.d.unit_begin = (uint32_t)units;
                 units += u;
                 if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
@@ -717,9 +821,9 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             for (int k = begin; k < end; k++) {
                 Desc &D = args.d[k - begin];
                 const lv_tensor &T = tensors[items[k].idx];
-                fill_desc(D, T, items[k]);
+                fill_desc(D, T, items[k], dual);
                 D.unit_begin = (uint32_t)units;
-                units += units_of(T.numel, unit_elems);
+                units += desc_units(D, unit_elems);
                 if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");
             }
             args.total_units = (uint32_t)units;
@@ -862,7 +966,13 @@ static int step_f32_device(OwnedWorkspace &ws, float *param, const float *grad, 
     int rc = prepare_call(&c, &t, 1, &it, nitems, spans);
     if (rc == LV_STATUS_SUCCESS && nitems) {
         Layout L = make_layout(static_cast<char *>(ws.p), tslots, runits);
-        rc = run_call(&c, &t, &it, nitems, L, stream, nullptr);
+        WsOrder *order = nullptr;
+        rc = order_before(ws.p, stream, order);
+        if (rc == LV_STATUS_SUCCESS) {
+            rc = run_call(&c, &t, &it, nitems, L, stream, nullptr);
+            const int ro = order_after(order, stream);
+            if (rc == LV_STATUS_SUCCESS) rc = ro;
+        }
         if (rc == LV_STATUS_EXECUTION_FAILED) {
             // a launch failed part-way: its count words may hold partial counts; start clean
             if (hipStreamSynchronize(stream) == hipSuccess) (void)hipMemset(ws.p, 0, ws.bytes);
@@ -996,7 +1106,13 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count, voi
     }
     if (nitems == 0) return LV_STATUS_SUCCESS;
     const Layout L = make_layout(static_cast<char *>(workspace), tslots, runits);
-    return run_call(cfg, tensors, cs.items.data(), nitems, L, static_cast<hipStream_t>(stream_ptr), &cs.tab);
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    WsOrder *order = nullptr;
+    rc = order_before(workspace, stream, order);
+    if (rc != LV_STATUS_SUCCESS) return rc;
+    rc = run_call(cfg, tensors, cs.items.data(), nitems, L, stream, &cs.tab);
+    const int ro = order_after(order, stream);
+    return rc != LV_STATUS_SUCCESS ? rc : ro;
 }
 
 int lv_step_multi_noalloc(const lv_config *cfg, const lv_tensor *tensors, int count, void *stream_ptr) {

@@ -74,7 +74,13 @@ struct Desc {
     uint32_t unit_begin;  // first work unit of this tensor in the launch's unit space
     uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
     uint32_t ibase;       // low 32 bits of index_base (the SR offset is taken mod 2^32)
-    uint32_t nskip;       // inactive [begin, end) ranges in `skip` (sorted, disjoint)
+    uint32_t nskip : 24;  // inactive [begin, end) ranges in `skip` (sorted, disjoint)
+    // vec: every stream is 16-byte aligned at element `head` (< 8), so the tensor's work units
+    // start there and whole units take the vector path; the `head` elements before it are taken
+    // one per thread by the block of the tensor's last unit. Set by the host from the pointers.
+    uint32_t head : 3;
+    uint32_t vec : 1;
+    uint32_t : 4;
     const uint64_t *skip;
 };
 
@@ -882,7 +888,8 @@ struct View {
     uint32_t t_begin, t_end;  // the tensor's unit range in the launch
     uint32_t slot_base;       // its first count slot (64-byte index into Args::slots)
     uint64_t n;
-    bool vec_ok;              // every pointer 16-byte aligned: whole units take the vector path
+    bool vec_ok;              // every stream 16-byte aligned at element `head`: whole units vectorised
+    uint32_t head;            // elements before the first aligned group (vec_ok only; else 0)
     float cs, bs;             // cautious / radial scale read from the scratch (fused, apply)
     Seeds sd;
     uint32_t ibase;
@@ -894,16 +901,12 @@ struct View {
 // launches everything else a block reads before its arithmetic (open_step) waits until its stream
 // loads are in flight: each dependent scalar load before the first vector load delays every
 // block's loads by a scalar-cache round trip, and a block lives only a few microseconds.
-template <int MODE>
-__device__ __forceinline__ View open_view(const Desc &D, uint32_t flags) {
-    constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+__device__ __forceinline__ View open_view(const Desc &D) {
     View tv;
     tv.t_begin = D.unit_begin;
     tv.n = D.n;
-    uintptr_t al = (uintptr_t)D.p | (uintptr_t)D.g | (uintptr_t)D.m;
-    if (kDual) al |= (uintptr_t)D.v;
-    if (flags & kFMaster) al |= (uintptr_t)D.mp;
-    tv.vec_ok = (al & 15u) == 0;
+    tv.vec_ok = D.vec;
+    tv.head = D.vec ? D.head : 0u;
     return tv;
 }
 
@@ -1237,7 +1240,7 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const uint32_t unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
     const int t = find_tensor<TABLE>(a, unit);
     const Desc &D = desc_of<TABLE>(a, t);
-    View tv = open_view<MODE>(D, flags);
+    View tv = open_view(D);
     // Table launches (many small tensors, latency-bound, descriptors in device memory) read the
     // rest of the view first: issued behind the stream loads, those reads queue after them
     // (cfg2's 64-tensor launch: 20.6 vs 18.7 us). Inline launches stream and read it afterwards.
@@ -1250,7 +1253,8 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     constexpr int H = unit_halves(MODE, PT, ST);
     constexpr uint32_t HS = lane_split(H, FL);
     constexpr uint64_t kUnit = (uint64_t)kHalf * H;
-    const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit;
+    // units start at the tensor's first 16-byte aligned element (tv.head > 0: an unaligned view)
+    const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit + tv.head;
     int cover = 0;
     uint32_t first = 0;
     if (D.nskip) cover = inactive_cover(D, ubase, ubase + kUnit < tv.n ? ubase + kUnit : tv.n, first);
@@ -1279,8 +1283,10 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         }
         // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
         // its elements still enter the radial norms.
-        if (!kCounting && cover == 2) return;
-        if (fast) {
+        if (!kCounting && cover == 2 && !(tv.head && unit + 1 == tv.t_end)) return;
+        if (!kCounting && cover == 2) {
+            // only the head (below) is left to this block
+        } else if (fast) {
             // the partial last unit of an aligned tensor: the same groups of 4
 #pragma unroll
             for (int h = 0; h < H; h++) {
@@ -1292,11 +1298,30 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
                     scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
                 }
             }
+        } else if (cover == 0) {
+            // streams with no common 16-byte alignment: element by element, each wave reading 64
+            // consecutive elements of every stream per access
+#pragma unroll 1
+            for (uint32_t j = 0; j < 4u * H; j++) {
+                const uint64_t e = ubase + (uint64_t)j * kThreads + threadIdx.x;
+                if (e < tv.n) scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, e + 1, cnt, su, sp);
+            }
         } else if (cover != 2 || radial) {
             const uint64_t eb = ubase + (uint64_t)threadIdx.x * (4u * H);
             const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
             scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
         }
+    }
+    // An unaligned view's head [0, tv.head) (its streams are 16-byte aligned from element tv.head
+    // on): the block of the tensor's last unit takes it, one element per thread, after its unit.
+    // Block-uniform; its count joins cnt as the wave's (vector path) or the lane's count.
+    if (tv.head && unit + 1 == tv.t_end) {
+        uint32_t hc = 0, hfirst = 0;
+        const int hcover = D.nskip ? inactive_cover(D, 0, tv.head, hfirst) : 0;
+        if (threadIdx.x < tv.head && (kCounting || hcover != 2))
+            scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, threadIdx.x, threadIdx.x + 1, hc, su, sp,
+                                             hcover ? D.nskip : 0, hfirst);
+        if constexpr (kCounting) cnt += vec ? wave_sum(hc) : hc;
     }
     if constexpr (kCounting) {
         if (radial) {

@@ -942,14 +942,27 @@ class LuminaV(Optimizer):
         raw_state = state_dict.get("state", {})
         saved_groups = state_dict.get("param_groups", [])
         raw_param_state: Dict[Any, Dict[str, Any]] = {}
+        precision_of: Dict[int, str] = {}  # group position -> state precision of its saved state
         if len(self.param_groups) == len(saved_groups):
-            for group, sg in zip(self.param_groups, saved_groups):
+            for gi, (group, sg) in enumerate(zip(self.param_groups, saved_groups)):
+                half_state: Set[bool] = set()
                 for p, pid in zip(group["params"], sg.get("params", [])):
                     st = raw_state.get(pid)
                     if isinstance(st, dict):
                         raw_param_state[p] = {k: (v.detach().clone() if isinstance(v, torch.Tensor) else v) for k, v in st.items()}
+                        m = st.get("exp_avg")
+                        if p.dtype in (torch.float16, torch.bfloat16) and isinstance(m, torch.Tensor):
+                            half_state.add(m.dtype in (torch.float16, torch.bfloat16))
+                if "state_precision" not in sg and len(half_state) == 1:
+                    # A checkpoint without this build's state_precision key (the reference's own
+                    # format): keep the precision its 16-bit params' state was saved in. The
+                    # reference stores that state in the param dtype unless master_weights="full"
+                    # (python/luminamoon/optimizer/luminav.py:1666-1672).
+                    precision_of[gi] = "param" if half_state.pop() else "fp32"
         super().load_state_dict(state_dict)
-        for group in self.param_groups:
+        for gi, group in enumerate(self.param_groups):
+            if gi in precision_of:
+                group["state_precision"] = precision_of[gi]
             for k, v in self.defaults.items():
                 group.setdefault(k, v)
             self._validate_and_normalize_group(group)
@@ -1280,6 +1293,7 @@ class LuminaV(Optimizer):
 
         eparams = [r[0] for r in rows]
         egrads = [r[2] for r in rows]
+        stensors = [t for r in rows for t in (r[3], r[4], r[5], r[6]) if t is not None]
         return {
             "epoch": self._plan_epoch, "group": group, "layout": tuple(group.get(k) for k in self._LAYOUT_KEYS),
             "params": list(group["params"]), "ids": list(map(id, group["params"])), "active": active,
@@ -1290,13 +1304,16 @@ class LuminaV(Optimizer):
             "gweak": [weakref.ref(g, died) for g in egrads], "dead": dead, "died": died,
             "states": [r[9] for r in rows], "steps": [int(r[7]) for r in rows], "step_epoch": self._step_epoch,
             "keep": [t.untyped_storage() for r in rows for t in (r[3], r[4], r[5], r[6]) if t is not None],
+            # the state tensors themselves and where their data was: `t.data = u` or `t.set_(u)` on
+            # a state tensor moves its storage without replacing the state entry
+            "stensors": stensors, "sptrs": list(map(_data_ptr, stensors)),
             "prep": prep,
         }
 
     def _run_unfused_plan(self, group: Dict[str, Any]) -> bool:
         """Steps `group` from its packed descriptors when only grads and step counters changed:
-        the same params carry a grad, param storage is where it was and no state was replaced
-        (load_state_dict, add_param_group and replacing or removing a state entry bump the epoch; a
+        the same params carry a grad, param and state storage is where it was and no state was
+        replaced (load_state_dict, add_param_group and replacing or removing a state entry bump the epoch; a
         changed buffer count, master mode or state precision changes the recorded layout). The
         checks run as C-level maps over the whole group. Returns False, having changed nothing the
         slow path relies on, when anything else changed."""
@@ -1315,6 +1332,8 @@ class LuminaV(Optimizer):
                 return False
             grads = list(map(_get_grad, plan["eparams"]))
         if list(map(_data_ptr, plan["eparams"])) != plan["pptrs"]:  # a param's storage moved
+            return False
+        if list(map(_data_ptr, plan["stensors"])) != plan["sptrs"]:  # a state tensor's storage moved
             return False
         prep = plan["prep"]
         gids = list(map(id, grads))
@@ -1462,7 +1481,8 @@ class LuminaV(Optimizer):
             for k, t in held:
                 if dict.get(st, k) is not t:
                     return False
-        return True
+        # `t.data = u` or `t.set_(u)` on a state tensor moves its storage in place
+        return list(map(_data_ptr, entry["stensors"])) == entry["sptrs"]
 
     def _first_capturable_step(self, group: Dict[str, Any], rows: List[Tuple[int, torch.Tensor, torch.Tensor]],
                                key: Tuple[int, ...]) -> None:
@@ -1494,6 +1514,8 @@ class LuminaV(Optimizer):
         count = record[0]  # 0-dim view: the counter every replay advances
         for st in states:
             _dict_set(st, "step", count)
+        stensors = [t for st in states for k in ("exp_avg", "exp_avg_sq", "master_param", "scratch")
+                    for t in (dict.get(st, k),) if isinstance(t, torch.Tensor)]
         old = self._graph_steps.get(id(group))
         if old is not None:
             self._graph_retired += (old["record"], old["workspace"])
@@ -1502,4 +1524,5 @@ class LuminaV(Optimizer):
             "record": record, "workspace": workspace, "params": [p for _, p, _ in rows], "states": states,
             "held": [[(k, dict.get(st, k)) for k in self._HELD_KEYS] for st in states],
             "pptrs": [p.data_ptr() for _, p, _ in rows], "gptrs": [g.data_ptr() for _, _, g in rows],
+            "stensors": stensors, "sptrs": list(map(_data_ptr, stensors)),
         }

@@ -1,5 +1,5 @@
 """Builds the GPU check libraries of the tests (hipcc, gfx950, the library's own flags): the exact
-helpers' exhaustive check and the VALU issue-rate probe."""
+helpers' exhaustive check."""
 from __future__ import annotations
 
 import os
@@ -13,8 +13,6 @@ if ROOT not in sys.path:
 
 EXACT_SRC = os.path.join(HERE, "exact_check.hip")
 EXACT_LIB = os.path.join(HERE, "libexactcheck.so")
-RATE_SRC = os.path.join(HERE, "issue_rate.hip")
-RATE_LIB = os.path.join(HERE, "libissuerate.so")
 
 
 def _build_one(src: str, lib: str, verbose: bool) -> None:
@@ -33,9 +31,8 @@ def _build_one(src: str, lib: str, verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    """Builds libexactcheck.so and libissuerate.so; returns the first's path."""
+    """Builds libexactcheck.so; returns its path."""
     _build_one(EXACT_SRC, EXACT_LIB, verbose)
-    _build_one(RATE_SRC, RATE_LIB, verbose)
     return EXACT_LIB
 
 

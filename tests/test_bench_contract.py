@@ -128,17 +128,11 @@ def test_cpu_baseline_draws_student_t_grads_for_cfg5():
 
 
 def _probe_lib():
-    import ctypes
+    import shutil
 
-    from luminamoon_amd import build_ext
-
-    if not os.path.exists(build_ext.PROBE_OUT):
-        pytest.skip("libstream_probe.so is not built")
-    fn = ctypes.CDLL(build_ext.PROBE_OUT).lv_stream_probe
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
-    return fn
+    if not (os.path.exists(bench.PROBE_LIB) or shutil.which("hipcc") or os.path.exists("/opt/rocm/bin/hipcc")):
+        pytest.skip("hipcc is needed to build the stream probe")
+    return bench.stream_probe_fn()
 
 
 def test_stream_probe_rejects_invalid_arguments_before_any_launch():

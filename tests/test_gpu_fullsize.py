@@ -10,7 +10,8 @@
     GPU's pre-step scratch.
 * T1 with bf16 params, grads and m and an fp32 master past 2^32 elements: the split lane layout
   of 2048-element units, the same exact-count and slice checks.
-* shards: a tensor stepped as slices with index_base equals the whole tensor stepped at once.
+* shards: a tensor stepped as slices with index_base equals the whole tensor stepped at once, and
+  each shard equals the oracle stepped on it with the same index base (bases across 2^31 and 2^32).
 """
 from __future__ import annotations
 
@@ -58,6 +59,52 @@ def test_shards_with_index_base_equal_whole():
     assert_bitwise(torch.cat([s[0] for s in shards]), whole[0], "p")
     assert_bitwise(torch.cat([s[1] for s in shards]), whole[1], "m")
     assert_bitwise(torch.cat([s[2] for s in shards]), whole[2], "v")
+
+
+@pytest.mark.parametrize("sdt", ["f32", "bf16"])
+def test_shards_with_index_base_match_oracle(oracle_mod, sdt):
+    """HIP shards stepped with index_base against the oracle stepped on the same shards with the
+    same index bases, bit for bit (p, m, v, scratch after each of 3 steps: the two-pass first
+    step, then fused). Element i of a shard at index_base a hashes the offset (int32)(a + i): the
+    reference's `idx as i32` of the unsharded tensor (reference_cpu/dual.rs:54, prng.rs:4-26); the
+    oracle's index_base is pinned to its own whole-tensor run on the CPU (test_oracle_pins.py).
+    The shards are slices of flat buffers cut at unaligned points (every buffer of a shard starts
+    mid-vector, so they take the vector path after a head), with bf16 params, stochastic rounding
+    and cautious on (each shard its own tensor and scratch on both sides), and fp32 or bf16 state.
+    Index bases: the cut points themselves, then bases that straddle 2^31 and 2^32 and one past
+    2^32 + 2^31."""
+    _need_gpu()
+    from luminamoon_amd.optimizer.hip_backend import HipStepper
+
+    O = oracle_mod
+    n = 3 * (1 << 20) + 777
+    cuts = [0, 1_000_003, 2_500_001, n]
+    sizes = [b - a for a, b in zip(cuts, cuts[1:])]
+    st_dt = torch.float32 if sdt == "f32" else torch.bfloat16
+    group = group_dict(buffer="T2", lr=1e-3, state_precision="fp32" if sdt == "f32" else "param")
+    cfg = oracle_config(O, group)
+    two31, two32 = 1 << 31, 1 << 32
+    for bases in (cuts[:-1], [two31 - 400_000, two32 - 1_300_000, two32 + two31 + 5]):
+        print(f"[case] shards state={sdt} index_bases={bases}", flush=True)
+        gen = torch.Generator(device="cuda").manual_seed(3)
+        p = (torch.randn(n, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        m = torch.zeros(n, dtype=st_dt, device="cuda")
+        v = torch.zeros(n, dtype=st_dt, device="cuda")
+        dev = [(p[a:b], m[a:b], v[a:b], torch.tensor([0, 0, 0, 1, 1, 0.0], device="cuda"))
+               for a, b in zip(cuts, cuts[1:])]
+        host = [tuple(t.cpu().clone() for t in d) for d in dev]
+        st = HipStepper()
+        for t in (1, 2, 3):
+            g = (torch.randn(n, device="cuda", generator=gen) * 1e-3).to(torch.bfloat16)
+            gs = [g[a:b] for a, b in zip(cuts, cuts[1:])]
+            st.step(group, [d[0] for d in dev], gs, [d[1] for d in dev], [d[2] for d in dev], [None] * 3,
+                    [d[3] for d in dev], [t] * 3, [0] * 3, index_bases=bases)
+            O.step(cfg, [h[0] for h in host], [x.cpu() for x in gs], [h[1] for h in host], [h[2] for h in host],
+                   [None] * 3, [h[3] for h in host], [t] * 3, [0] * 3, threads=8, index_bases=bases)
+            torch.cuda.synchronize()
+            for k, (d, h) in enumerate(zip(dev, host)):
+                for name, x, y in zip(("p", "m", "v", "scratch"), h, d):
+                    assert_bitwise(x, y, f"step {t} shard {k} (base {bases[k]}, {sizes[k]} elements) {name}")
 
 
 def test_cfg5_full_bucket_count_and_wrap_slices(oracle_mod):

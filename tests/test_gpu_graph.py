@@ -358,16 +358,22 @@ def test_two_capturable_groups_in_one_graph(monkeypatch):
 
 
 @pytest.mark.parametrize("case", range(24))
-def test_capturable_random_options(case):
+def test_capturable_random_options(case, oracle_mod):
     """Seeded random option draws (mode, param dtype, state precision, master weights, cautious,
     stochastic rounding, coordinate or radial bound, weight decay, fused pass, lr, seed; 1-60
     ragged tensors) through LuminaV(capturable=True): two eager steps, a captured graph, four
     replays with new gradients; every buffer, the scratch and the step count equal a plain
-    LuminaV's eager steps bit for bit after each step."""
+    LuminaV's eager steps bit for bit after each step. The replays are also stepped on the CPU
+    oracle from the state after the eager steps (the reference's core, reference_cpu/dual.rs and
+    tdclm.rs), and every replay equals it bit for bit too."""
     _need_gpu()
+    import contextlib
     import warnings
 
     from luminamoon_amd import LuminaV
+    from tests.parity_util import assert_bitwise, oracle_config
+
+    O = oracle_mod
 
     rng = np.random.default_rng(7000 + case)
     pick = lambda xs: xs[int(rng.integers(len(xs)))]  # noqa: E731
@@ -392,12 +398,16 @@ def test_capturable_random_options(case):
         p.grad = g
     print(f"[case] capturable random {case}: {dt} {nten} tensors {kw}", flush=True)
 
+    fed = []
+
     def feed(s):
         gen = torch.Generator(device="cuda").manual_seed(case * 100 + s)
+        fed.clear()
         for gs, q in zip(static, pb):
             g = (torch.randn(q.shape, generator=gen, device="cuda") * 1e-3).to(q.dtype)
             gs.copy_(g)
             q.grad = g
+            fed.append(g)
 
     def check(s):
         for i, (x, y) in enumerate(zip(pa, pb)):
@@ -413,6 +423,14 @@ def test_capturable_random_options(case):
         ob.step()
         torch.cuda.synchronize()
         check(s)
+    # the oracle's copy of the state after the eager steps (p, m, v, master, scratch per tensor)
+    grp = oa.param_groups[0]
+    cfg = oracle_config(O, grp)
+    host = [(x.detach().cpu().clone(), oa.state[x]["exp_avg"].cpu().clone(),
+             oa.state[x]["exp_avg_sq"].cpu().clone() if "exp_avg_sq" in oa.state[x] else None,
+             oa.state[x]["master_param"].cpu().clone() if "master_param" in oa.state[x] else None,
+             oa.state[x]["scratch"].cpu().clone()) for x in pa]
+    radial = grp["bound"] and grp["bound_type"] == 1
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         oa.step()
@@ -422,3 +440,18 @@ def test_capturable_random_options(case):
         ob.step()
         torch.cuda.synchronize()
         check(s)
+        for h in host:  # the reference's host layer forces unused scale slots (luminav.py:1748-1751)
+            if not grp["cautious"]:
+                h[4][3] = 1.0
+            if not radial:
+                h[4][4] = 1.0
+        with (O.radial_sum_f64() if radial else contextlib.nullcontext()):
+            O.step(cfg, [h[0] for h in host], [g.cpu() for g in fed], [h[1] for h in host], [h[2] for h in host],
+                   [h[3] for h in host], [h[4] for h in host], [s] * nten, list(range(nten)))
+        for i, (x, h) in enumerate(zip(pa, host)):
+            st = oa.state[x]
+            for name, want, got in (("p", h[0], x.detach()), ("m", h[1], st["exp_avg"]),
+                                    ("v", h[2], st.get("exp_avg_sq")), ("master", h[3], st.get("master_param")),
+                                    ("scratch", h[4], st["scratch"])):
+                if want is not None:
+                    assert_bitwise(want, got, f"replay for step {s}, oracle vs graph, {name}[{i}]")

@@ -355,8 +355,9 @@ def test_mixed_steps_in_one_call(oracle_mod):
         host.assert_equal(dev, f"mixed round {rnd}")
 
 
-def test_unaligned_views_use_scalar_path(oracle_mod):
-    """Tensors at odd element offsets (not 16-byte aligned) take the per-element path."""
+def test_unaligned_views_by_one_element(oracle_mod):
+    """A tensor whose buffers all start one element past a 16-byte boundary: the vector path from
+    its first aligned element, with the 7-element head taken by its last block."""
     _need_gpu()
     O = oracle_mod
     group = group_dict(buffer=2, lr=1e-3)

@@ -179,8 +179,8 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     """Unfused groups reuse their packed descriptors while only grads and step counters change.
     Every way the plan can go stale is driven here -- grads updated in place, new grad tensors,
     a param losing and regaining its grad, param storage replaced, load_state_dict, a changed
-    hyper-parameter, new grads while the old ones live on, one grad replaced -- and each step is
-    compared bit for bit with the oracle."""
+    hyper-parameter, new grads while the old ones live on, one grad replaced, a state tensor's
+    storage moved in place -- and each step is compared bit for bit with the oracle."""
     _need_gpu()
     from luminamoon_amd import LuminaV
     from tests.parity_util import TensorSet, assert_bitwise, oracle_config, seeded_tensor
@@ -282,6 +282,20 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     run(21, "keep", True)
     run(22, "keep", True)
     run(23, "one", True)
+    # a state tensor's storage moved in place (t.data = u, t.set_(u)): the state entry is the same
+    # object, so only its data pointer shows it; the plan is dropped and the moved storage stepped
+    m0 = opt.state[params[0]]["exp_avg"]
+    m0.data = m0.data.clone()
+    run(24, "new", False)
+    run(25, "new", True)
+    v3 = opt.state[params[3]]["exp_avg_sq"]
+    v3.set_(v3.clone())
+    run(26, "new", False)
+    run(27, "new", True)
+    sc2 = opt.state[params[2]]["scratch"]
+    sc2.data = sc2.data.clone()
+    run(28, "new", False)
+    run(29, "new", True)
 
 
 def test_unfused_duplicate_param_raises_like_the_native_seam():
@@ -307,3 +321,44 @@ def test_unfused_duplicate_param_raises_like_the_native_seam():
     torch.cuda.synchronize()
     assert torch.equal(w.detach(), before)
     assert int(opt.state[w]["step"]) == 0
+
+
+def test_reference_checkpoint_keeps_its_state_dtype(oracle_mod):
+    """A checkpoint in the reference's own format -- no state_precision key, bf16 params with bf16
+    exp_avg/exp_avg_sq as the reference allocates them (python/luminamoon/optimizer/luminav.py:
+    1666-1672) -- resumes with bf16 state in a LuminaV built with the default fp32 state, and the
+    next three steps equal the oracle continuing from the same state, bit for bit."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+    from tests.parity_util import TensorSet, assert_bitwise, oracle_config
+
+    O = oracle_mod
+    sizes = [4099, 70_001]
+    host = TensorSet(sizes, "bf16", "bf16", "bf16", True, False, seed=21, m_scale=1e-3)
+    params = [nn.Parameter(t.clone().cuda()) for t in host.p]
+    opt = LuminaV(params, lr=1e-3, buffer="T2")
+    groups = [{k: v for k, v in g.items() if k != "state_precision"} for g in opt.state_dict()["param_groups"]]
+    scale = [1.25, 1.5]
+    state = {i: {"step": 7, "exp_avg": host.m[i].clone(), "exp_avg_sq": host.v[i].clone(),
+                 "scratch": torch.tensor([0.0, 0.0, 0.0, scale[i], 1.0, 0.0]), "buf_count": "T2"}
+             for i in range(len(sizes))}
+    opt.load_state_dict({"state": state, "param_groups": groups})
+    assert opt.param_groups[0]["state_precision"] == "param"
+    for p in params:
+        assert opt.state[p]["exp_avg"].dtype == torch.bfloat16 and opt.state[p]["exp_avg_sq"].dtype == torch.bfloat16
+    for i in range(len(sizes)):
+        host.sc[i] = torch.tensor([0.0, 0.0, 0.0, scale[i], 1.0, 0.0])
+    cfg = oracle_config(O, opt.param_groups[0])
+    for s in (8, 9, 10):
+        grads = host.grads(s, 21)
+        for p, g in zip(params, grads):
+            p.grad = g.cuda()
+        opt.step()
+        host.oracle_step(O, cfg, grads, s)
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            st = opt.state[p]
+            assert_bitwise(p.detach(), host.p[i], f"step {s} p[{i}]")
+            assert_bitwise(st["exp_avg"], host.m[i], f"step {s} m[{i}]")
+            assert_bitwise(st["exp_avg_sq"], host.v[i], f"step {s} v[{i}]")
+            assert_bitwise(st["scratch"], host.sc[i], f"step {s} scratch[{i}]")

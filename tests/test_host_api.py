@@ -280,3 +280,36 @@ def test_bucket_cut_rule():
     assert sizes(cut(mk(3, 50, 2), 100)) == [[3], [50], [2]]
     assert sizes(cut(mk(5, 5, 5, 5, 5, 5), 40)) == [[5, 5], [5, 5], [5, 5]]
     assert [i for c in cut(mk(7, 1, 30, 2, 2), 40) for i, _ in c] == [0, 1, 2, 3, 4]  # order kept
+
+
+def test_reference_checkpoint_state_precision_is_inferred():
+    """A checkpoint without this build's state_precision key (the reference's format) keeps the
+    precision its 16-bit params' state was saved in: bf16 m/v stay bf16 (the reference's default
+    for 16-bit params, luminav.py:1666-1672), fp32 m/v stay fp32, whatever the constructor said; a
+    checkpoint that carries the key keeps its own value."""
+    def make():
+        return [P(64, dtype=torch.bfloat16), P(10, dtype=torch.bfloat16)]
+
+    def ckpt(opt, dt, keep_key=False):
+        groups = [{k: v for k, v in g.items() if keep_key or k != "state_precision"}
+                  for g in opt.state_dict()["param_groups"]]
+        state = {i: {"step": 3, "exp_avg": torch.randn(n).to(dt), "exp_avg_sq": torch.rand(n).to(dt),
+                     "scratch": torch.tensor([0.0, 0.0, 0.0, 1.0, 1.0, 0.0]), "buf_count": 2}
+                 for i, n in enumerate((64, 10))}
+        return {"state": state, "param_groups": groups}
+
+    ps = make()
+    opt = LuminaV(ps, lr=1e-3)
+    opt.load_state_dict(ckpt(opt, torch.bfloat16))
+    assert opt.param_groups[0]["state_precision"] == "param"
+    assert all(opt.state[p][k].dtype == torch.bfloat16 for p in ps for k in ("exp_avg", "exp_avg_sq"))
+    ps = make()
+    opt = LuminaV(ps, lr=1e-3, state_precision="param")
+    opt.load_state_dict(ckpt(opt, torch.float32))
+    assert opt.param_groups[0]["state_precision"] == "fp32"
+    assert all(opt.state[p][k].dtype == torch.float32 for p in ps for k in ("exp_avg", "exp_avg_sq"))
+    ps = make()
+    opt = LuminaV(ps, lr=1e-3, state_precision="fp32")
+    opt.load_state_dict(ckpt(opt, torch.bfloat16, keep_key=True))  # this build's own checkpoint
+    assert opt.param_groups[0]["state_precision"] == "fp32"
+    assert all(opt.state[p][k].dtype == torch.float32 for p in ps for k in ("exp_avg", "exp_avg_sq"))

@@ -37,7 +37,7 @@ SRC = os.path.join(HERE, "gpu_checks", "valu_budget.hip")
 # v_mul_lo_u32, and a stored fp16 value half a v_cvt_pkrtz_f16_f32 (two per pack). A walk that
 # skipped real work (a branch the code never takes) would miss one of them. Stochastic rounding to
 # bf16 or fp16 is one integer add on the path (the v_cvt_sr_bf16_f32 / v_cvt_sr_f16_f32 converters
-# take about 3 times its issue time, tests/test_gpu_issue_rate.py), so they are anchored at zero.
+# take about 3 times its issue time on gfx950), so they are anchored at zero.
 #   T2: clm / env, the coordinate bound's quotient; sqrt(v). T1: the same without v.
 #   CLM: clm / sigma, the bound's step / b, two tanh quotients; sqrt(v), sqrt(p^2 + 1e-4).
 #   TD-CLM: clm / env, step / b, one tanh quotient; sqrt(p^2 + 1e-4).
