@@ -10,7 +10,10 @@ the wall clock over the same steps.
 
 Prints ONE JSON line with params/s (whole job), ms per step, achieved HBM GB/s against the
 8 TB/s peak (`roofline`), and the CPU oracle timed on a bounded sample on this host
-(`cpu_baseline`).
+(`cpu_baseline`). `value` and `roofline` come from the workload's first allocation in the
+process (what a user of the optimizer gets); `placement` adds the same workload allocated again
+after a 200 GiB reserve/release (skipped with --no-reserve), since the physical placement of the
+buffers moves this lockstep stream by a few percent.
 """
 from __future__ import annotations
 
@@ -20,6 +23,7 @@ import math
 import os
 import sys
 import time
+import warnings
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -306,7 +310,7 @@ def offset_ab(torch, n: int, offset: int, steps: int, rounds: int = 5) -> dict:
                  fuse_tensors=False, bucket_cap_mb=500.0, prewarm_jit=True, ema_decay="auto", fsdp_sync=False,
                  seed=1337, version=None, spec=None)
     LuminaV._validate_and_normalize_group(group)
-    slack = 16
+    slack = 128
     p, g = fill_inputs(torch, n + slack, torch.bfloat16, "student_t3", seed=77)
     m = torch.zeros(n + slack, dtype=torch.float32, device="cuda")
     v = torch.zeros(n + slack, dtype=torch.float32, device="cuda")
@@ -491,6 +495,81 @@ def cpu_threads() -> dict:
             "limited_by": binding, "limits": limits}
 
 
+def timed_pass(torch, args, wl: dict, sizes, pdt, with_floor: bool):
+    """Allocates the workload (inputs generated on the GPU, the drop-in LuminaV over them: configs
+    3-5 as their one bucket), takes the warm-up steps, then times args.steps steps back to back
+    between ONE pair of HIP events on the launch stream (per-step event records would add host
+    time to every step: about 6 us, a quarter of cfg2's). Frees everything before returning
+    (ms_avg, ms_wall, the per-step spread) and the stream floor when asked for."""
+    from luminamoon_amd import LuminaV
+
+    t0 = time.perf_counter()
+    params = []
+    for i, size in enumerate(sizes):
+        p_data, g_data = fill_inputs(torch, size, pdt, wl["grad"], seed=1234 + i)
+        p = torch.nn.Parameter(p_data, requires_grad=True)
+        p.grad = g_data
+        params.append(p)
+    del p_data, g_data
+    one_bucket = len(params) == 1
+    cap_mb = (params[0].numel() * params[0].element_size()) / (1 << 20) + 1.0 if one_bucket else 500.0
+    with warnings.catch_warnings():  # the reference's advice against fusion for language models
+        warnings.simplefilter("ignore", UserWarning)
+        opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"], bound_type=args.bound,
+                      state_precision=args.state, master_weights=args.master, fuse_tensors=one_bucket,
+                      bucket_cap_mb=cap_mb)
+    torch.cuda.synchronize()
+    log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        opt.step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms_avg = t_start.elapsed_time(t_end) / args.steps
+    ms_wall = wall * 1e3 / args.steps
+    # the per-step spread, from a short untimed pass with events around each step
+    spread = []
+    for _ in range(min(args.steps, 10)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        opt.step()
+        b.record(stream)
+        spread.append((a, b))
+    torch.cuda.synchronize()
+    per_step_ms = [a.elapsed_time(b) for a, b in spread]
+    log(f"timed steps: {ms_avg:.4f} ms per step on the stream (HIP events), wall {ms_wall:.4f}; "
+        f"untimed per-step check: min {min(per_step_ms):.4f} max {max(per_step_ms):.4f} ms")
+    for q in params:
+        sc = opt.state[q]["scratch"].tolist()
+        if not all(math.isfinite(x) for x in sc):
+            raise RuntimeError(f"non-finite scratch {sc}")
+    log(f"scratch of the last tensor after {args.warmup + args.steps + len(spread)} steps: {sc}")
+    floor = None
+    if with_floor:
+        if len(params) != 1 or args.master != "none":
+            log("--stream-floor: one-tensor configs without master weights only; skipped")
+        else:
+            st = opt.state[params[0]]
+            floor = stream_floor(torch, params[0].data, params[0].grad, st["exp_avg"], st.get("exp_avg_sq"),
+                                 reps=args.steps)
+            achieved = sizes[0] * wl["bytes_per_param"] / (ms_avg / 1e3) / 1e9
+            log(f"stream floor ({floor['kernel']}, {floor['bytes_per_param']} B/param, {floor['reps']} launches): "
+                f"{floor['ms']:.4f} ms, {floor['gb_per_s']:.0f} GB/s ({100 * floor['frac']:.1f}% of peak); "
+                f"the step: {ms_avg:.4f} ms, {achieved:.0f} GB/s ({100 * achieved / HBM_PEAK_GBS:.1f}%)")
+    del opt, params, p
+    torch.cuda.synchronize()
+    return {"ms_avg": ms_avg, "ms_wall": ms_wall, "per_step_ms": per_step_ms}, floor
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -508,7 +587,8 @@ def main() -> int:
                     help="param and grad dtype of a 16-bit config (default: the config's bf16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--no-reserve", action="store_true", help="skip the HBM reserve/release before allocating")
+    ap.add_argument("--no-reserve", action="store_true",
+                    help="skip the second pass (the workload allocated again after an HBM reserve/release)")
     ap.add_argument("--reserve-gb", type=float, default=200.0)
     ap.add_argument("--stream-floor", action="store_true",
                     help="after the timed steps, time a bare kernel that streams the step's own buffers "
@@ -530,7 +610,6 @@ def main() -> int:
 
     import torch
 
-    from luminamoon_amd import LuminaV
     from luminamoon_amd.optimizer import hip_backend
 
     hip_backend.load_library()
@@ -538,8 +617,8 @@ def main() -> int:
         log("no GPU visible")
         return 1
     if args.offset_ab is not None:
-        if not 0 < args.offset_ab < 16:
-            print(json.dumps({"error": "--offset-ab takes an element offset from 1 to 15"}), flush=True)
+        if not 0 < args.offset_ab < 128:
+            print(json.dumps({"error": "--offset-ab takes an element offset from 1 to 127"}), flush=True)
             return 2
         res = offset_ab(torch, args.elems, args.offset_ab, steps=args.steps if args.steps else 20)
         log(f"offset A/B: aligned {res['aligned_ms']:.4f} ms, +{args.offset_ab} elements {res['offset_ms']:.4f} ms "
@@ -564,80 +643,32 @@ def main() -> int:
         log("not enough HBM for this workload")
         return 1
 
-    # Reserve-and-release most of HBM once before allocating the workload (untimed, no writes,
-    # ~0.02 s). On a freshly booted box the first large allocations of the first process could
-    # land where this streaming step ran ~15% slower for the whole process lifetime; one
-    # allocate/free cycle avoided that. Placement still moves the step by about +-3% between
-    # processes (the driver chooses the physical pages).
-    if not args.no_reserve:
-        reserve = torch.empty(int(min(args.reserve_gb * (1 << 30), free * 0.9)), dtype=torch.uint8, device="cuda")
-        del reserve
-        torch.cuda.empty_cache()
-
-    t0 = time.perf_counter()
-    params = []
-    for i, size in enumerate(sizes):
-        p_data, g_data = fill_inputs(torch, size, pdt, wl["grad"], seed=1234 + i)
-        p = torch.nn.Parameter(p_data, requires_grad=True)
-        p.grad = g_data
-        params.append(p)
-    del p_data, g_data
-    opt = LuminaV(params, lr=1e-3, buffer=wl["buffer"], cautious=wl["cautious"], bound_type=args.bound,
-                  state_precision=args.state, master_weights=args.master)
-    torch.cuda.synchronize()
-    log(f"inputs ready in {time.perf_counter() - t0:.1f} s")
-
-    for _ in range(args.warmup):
-        opt.step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    # The timed steps run back to back between ONE pair of HIP events on the launch stream: per-step
-    # event records would add host time to every step (about 6 us per step, a quarter of cfg2's).
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    t_start.record(stream)
-    for _ in range(args.steps):
-        opt.step()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms_avg = t_start.elapsed_time(t_end) / args.steps
-    ms_wall = wall * 1e3 / args.steps
+    # The timed pass runs on the workload's first allocation in this process, the placement a user
+    # of the optimizer gets. On a freshly started device the first large allocations can land on
+    # physical pages where this lockstep stream runs 5-7% slower for the whole allocation's life
+    # (more DRAM credit stalls, the same address translation); LuminaV lays a bucket out in one
+    # allocation, which measured 1.5% slow there instead. The line also reports the same workload
+    # allocated again after a 200 GiB reserve/release (a placement away from those pages), unless
+    # --no-reserve.
+    first, floor = timed_pass(torch, args, wl, sizes, pdt, with_floor=args.stream_floor)
+    ms_avg, ms_wall = first["ms_avg"], first["ms_wall"]
     params_per_s = n / (ms_wall / 1e3)
     bytes_launch = n * wl["bytes_per_param"]
     achieved = bytes_launch / (ms_avg / 1e3) / 1e9
-    # the per-step spread, from a short untimed pass with events around each step
-    spread = []
-    for _ in range(min(args.steps, 10)):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        opt.step()
-        b.record(stream)
-        spread.append((a, b))
+    placement = {"first_allocation_ms": ms_avg, "first_allocation_frac": achieved / HBM_PEAK_GBS}
+    if not args.no_reserve:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        free_now, _ = torch.cuda.mem_get_info()
+        reserve = torch.empty(int(min(args.reserve_gb * (1 << 30), free_now * 0.9)), dtype=torch.uint8, device="cuda")
+        del reserve
+        torch.cuda.empty_cache()
+        again, _ = timed_pass(torch, args, wl, sizes, pdt, with_floor=False)
+        placement["after_reserve_ms"] = again["ms_avg"]
+        placement["after_reserve_frac"] = bytes_launch / (again["ms_avg"] / 1e3) / 1e9 / HBM_PEAK_GBS
+        log(f"the same workload allocated again after a {args.reserve_gb:.0f} GiB reserve/release: "
+            f"{again['ms_avg']:.4f} ms per step ({100 * placement['after_reserve_frac']:.1f}% of peak)")
     torch.cuda.synchronize()
-    per_step_ms = [a.elapsed_time(b) for a, b in spread]
-    log(f"timed steps: {ms_avg:.4f} ms per step on the stream (HIP events), wall {ms_wall:.4f}; "
-        f"untimed per-step check: min {min(per_step_ms):.4f} max {max(per_step_ms):.4f} ms")
-    for q in params:
-        sc = opt.state[q]["scratch"].tolist()
-        if not all(math.isfinite(x) for x in sc):
-            log(f"non-finite scratch {sc}")
-            return 1
-    log(f"scratch of the last tensor after {args.warmup + args.steps + len(spread)} steps: {sc}")
-    floor = None
-    if args.stream_floor:
-        if len(params) != 1 or args.master != "none":
-            log("--stream-floor: one-tensor configs without master weights only; skipped")
-        else:
-            st = opt.state[params[0]]
-            floor = stream_floor(torch, params[0].data, params[0].grad, st["exp_avg"], st.get("exp_avg_sq"),
-                                 reps=args.steps)
-            log(f"stream floor ({floor['kernel']}, {floor['bytes_per_param']} B/param, {floor['reps']} launches): "
-                f"{floor['ms']:.4f} ms, {floor['gb_per_s']:.0f} GB/s ({100 * floor['frac']:.1f}% of peak); "
-                f"the step: {ms_avg:.4f} ms, {achieved:.0f} GB/s ({100 * achieved / HBM_PEAK_GBS:.1f}%)")
-    del opt, params, p
     torch.cuda.empty_cache()
     copy_gbs = copy_probe(torch)
     log(f"copy probe (fp32 negate, 4 GiB in + 4 GiB out): {copy_gbs:.0f} GB/s")
@@ -694,6 +725,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    out["placement"] = placement
     if floor is not None:
         out["stream_floor"] = floor
     print(json.dumps(out), flush=True)

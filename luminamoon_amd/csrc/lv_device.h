@@ -75,12 +75,13 @@ struct Desc {
     uint32_t pidx;        // low 32 bits of param_index (seeds only need idx * 10007 mod 2^31)
     uint32_t ibase;       // low 32 bits of index_base (the SR offset is taken mod 2^32)
     uint32_t nskip : 24;  // inactive [begin, end) ranges in `skip` (sorted, disjoint)
-    // vec: every stream is 16-byte aligned at element `head` (< 8), so the tensor's work units
-    // start there and whole units take the vector path; the `head` elements before it are taken
-    // one per thread by the block of the tensor's last unit. Set by the host from the pointers.
-    uint32_t head : 3;
+    // vec: every stream is aligned at element `head` (< 64; to a 128-byte line where the views
+    // allow it, else to 16 bytes), so the tensor's work units start there and whole units take
+    // the vector path; the `head` elements before it are taken one per thread by the block of the
+    // tensor's last unit. Set by the host from the pointers.
+    uint32_t head : 6;
     uint32_t vec : 1;
-    uint32_t : 4;
+    uint32_t : 1;
     const uint64_t *skip;
 };
 
@@ -888,8 +889,8 @@ struct View {
     uint32_t t_begin, t_end;  // the tensor's unit range in the launch
     uint32_t slot_base;       // its first count slot (64-byte index into Args::slots)
     uint64_t n;
-    bool vec_ok;              // every stream 16-byte aligned at element `head`: whole units vectorised
-    uint32_t head;            // elements before the first aligned group (vec_ok only; else 0)
+    bool vec_ok;              // every stream aligned at element `head`: whole units vectorised
+    uint32_t head;            // elements before the first aligned element (vec_ok only; else 0)
     float cs, bs;             // cautious / radial scale read from the scratch (fused, apply)
     Seeds sd;
     uint32_t ibase;
@@ -1312,8 +1313,8 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
             scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
         }
     }
-    // An unaligned view's head [0, tv.head) (its streams are 16-byte aligned from element tv.head
-    // on): the block of the tensor's last unit takes it, one element per thread, after its unit.
+    // An unaligned view's head [0, tv.head) (its streams are aligned from element tv.head on): the
+    // block of the tensor's last unit takes it, one element per thread, after its unit.
     // Block-uniform; its count joins cnt as the wave's (vector path) or the lane's count.
     if (tv.head && unit + 1 == tv.t_end) {
         uint32_t hc = 0, hfirst = 0;

@@ -117,6 +117,50 @@ def _convert_state_buffer(src: torch.Tensor, device: torch.device, target: torch
     return buf.to(dtype=target).contiguous()
 
 
+# --------------------------------------------------------------------- bucket buffers in HBM
+
+_ARENA_ALIGN = 2 << 20  # every buffer of a bucket starts on a 2 MiB boundary of its allocation
+
+
+class _ArenaPart:
+    """One buffer of a bucket's device allocation, as an object that torch.as_tensor wraps without
+    a copy (the CUDA array interface). The tensor it makes has a storage of its own, exactly the
+    buffer's bytes (so torch.save of a model whose params live in a bucket writes only the params),
+    and keeps the whole allocation alive through this object."""
+
+    __slots__ = ("arena", "__cuda_array_interface__")
+
+    def __init__(self, arena: torch.Tensor, offset: int, nbytes: int) -> None:
+        self.arena = arena
+        self.__cuda_array_interface__ = {"shape": (nbytes,), "typestr": "|u1",
+                                         "data": (arena.data_ptr() + offset, False), "version": 2}
+
+
+def _bucket_buffers(device: torch.device, specs: List[Tuple[str, torch.dtype, int]]) -> Dict[str, torch.Tensor]:
+    """A bucket's flat buffers, in the order given. On a GPU they are laid out back to back, each on
+    a 2 MiB boundary, in ONE allocation. The step streams these buffers in lockstep (element i of
+    p, g, m and v at once); in physically fresh HBM (the first large allocations of a process on a
+    freshly started device) separately allocated buffers landed at relative physical offsets that
+    raised the memory controllers' DRAM credit stalls by half and slowed the cfg5 step by 5-7%,
+    while this packed order measured at full speed on the same pages (translation misses were
+    equal in both). Elsewhere the layout is neutral."""
+    if device.type != "cuda":
+        return {name: torch.empty(n, dtype=dt, device=device) for name, dt, n in specs}
+    offs, off = [], 0
+    for _, dt, n in specs:
+        offs.append(off)
+        nbytes = n * torch.empty((), dtype=dt).element_size()
+        off += (nbytes + _ARENA_ALIGN - 1) // _ARENA_ALIGN * _ARENA_ALIGN
+    arena = torch.empty(off + _ARENA_ALIGN, dtype=torch.uint8, device=device)
+    base = (-arena.data_ptr()) % _ARENA_ALIGN
+    out: Dict[str, torch.Tensor] = {}
+    for (name, dt, n), o in zip(specs, offs):
+        nbytes = n * torch.empty((), dtype=dt).element_size()
+        part = torch.as_tensor(_ArenaPart(arena, base + o, nbytes), device=device)
+        out[name] = part.view(dt)
+    return out
+
+
 _dict_set = dict.__setitem__
 _get_grad = operator.attrgetter("grad")
 _data_ptr = torch.Tensor.data_ptr
@@ -724,14 +768,15 @@ class LuminaV(Optimizer):
         sdt = self._state_dtype(dt, master_mode, group.get("state_precision", DEFAULT_STATE_PRECISION))
         numels = [int(p.numel()) for _, p in members]
         total = sum(numels)
-        flats: Dict[str, Optional[torch.Tensor]] = {
-            "p": torch.empty(total, dtype=dt, device=dev),
-            "g": torch.zeros(total, dtype=dt, device=dev),
-            "m": torch.zeros(total, dtype=sdt, device=dev),
-            "v": torch.zeros(total, dtype=sdt, device=dev) if dual else None,
-            "mp": (torch.empty(total, dtype=torch.float32, device=dev)
-                   if master_mode > 0 and dt in (torch.float16, torch.bfloat16) else None),
-        }
+        with_mp = master_mode > 0 and dt in (torch.float16, torch.bfloat16)
+        specs = [("p", dt, total), ("g", dt, total), ("m", sdt, total)]
+        specs += [("v", sdt, total)] if dual else []
+        specs += [("mp", torch.float32, total)] if with_mp else []
+        bufs = _bucket_buffers(dev, specs)
+        for name in ("g", "m", "v"):
+            if name in bufs:
+                bufs[name].zero_()
+        flats: Dict[str, Optional[torch.Tensor]] = {k: bufs.get(k) for k in ("p", "g", "m", "v", "mp")}
         parts = {k: (torch.split(f, numels) if f is not None else [None] * len(members)) for k, f in flats.items()}
         scratch = _new_scratch(dev)
         bucket = {

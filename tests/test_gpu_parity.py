@@ -357,7 +357,7 @@ def test_mixed_steps_in_one_call(oracle_mod):
 
 def test_unaligned_views_by_one_element(oracle_mod):
     """A tensor whose buffers all start one element past a 16-byte boundary: the vector path from
-    its first aligned element, with the 7-element head taken by its last block."""
+    its first element on a 128-byte line, with the head before it taken by its last block."""
     _need_gpu()
     O = oracle_mod
     group = group_dict(buffer=2, lr=1e-3)

@@ -2,8 +2,9 @@
 
 * Unaligned views. A view that starts k elements past a 16-byte boundary in every one of its
   buffers (a slice of a bucket, a shard) keeps the vector layout: its work units start at the
-  first aligned element and the k-element head is taken one element per thread by the tensor's
-  last block. Checked bit for bit against the oracle for k = 0..8, for f32, bf16 and 16-bit state
+  first element on a 128-byte line (16 bytes for short tensors) and the head before it is taken
+  one element per thread by the tensor's last block. Checked bit for bit against the oracle for
+  k = 0..8, 31, 33, 63, 64, 65, for f32, bf16 and 16-bit state
   (the 8-element lane layout), the split lane layout of a master copy beside 16-bit state, sizes
   around the unit size and the head, and inactive ranges that cover the head. Views whose buffers
   disagree on their offset (a shifted grad beside an aligned param and state) go element by element,
@@ -44,7 +45,7 @@ def _shifted(t: Optional[torch.Tensor], k: int) -> Optional[torch.Tensor]:
     """A copy of t on the GPU that starts k elements into a fresh (256-byte aligned) buffer."""
     if t is None:
         return None
-    big = torch.zeros(t.numel() + 16, dtype=t.dtype, device="cuda")
+    big = torch.zeros(t.numel() + 80, dtype=t.dtype, device="cuda")
     big[k:k + t.numel()].copy_(t.reshape(-1))
     return big[k:k + t.numel()]
 
@@ -118,12 +119,14 @@ VIEW_CASES = [
 
 @pytest.mark.parametrize("name,pdt,sdt,kw", VIEW_CASES, ids=[c[0] for c in VIEW_CASES])
 def test_views_at_every_offset_match_oracle(oracle_mod, name, pdt, sdt, kw):
-    """One call over 9 tensors, tensor k starting k elements past an aligned address in every
-    buffer (k = 0..8), of sizes around the unit and the head (1, k, k + 1, a unit plus the head,
-    whole units after the head, ragged)."""
+    """One call over 14 tensors, tensor k starting offs[k] elements past a 256-byte boundary in
+    every buffer: 0..8, 31, 33, 63, 64, 65 (heads up to 63 elements to the next 128-byte line,
+    or to 16 bytes when the tensor is shorter than that), of sizes around the unit and the head
+    (1, shorter than the head, a unit plus the head, whole units after the head, ragged)."""
     _need_gpu()
-    offs = list(range(9))
-    sizes = [1, 3, 3, 2048 + 3, 4096 + 4, 2 * 2048 + 5, 65_539, 100_000, 1024 + 7]
+    offs = [0, 1, 2, 3, 4, 5, 6, 7, 8, 31, 33, 63, 64, 65]
+    sizes = [1, 3, 3, 2048 + 61, 4096 + 60, 2 * 2048 + 5, 65_539, 100_000, 1024 + 7, 40, 2048 + 31, 5000, 3000,
+             2048 + 63]
     _views_case(oracle_mod, sizes, pdt, sdt, offs, **kw)
 
 
@@ -134,11 +137,11 @@ def test_views_with_inactive_ranges_over_the_head(oracle_mod):
     n = 3 * 1024 + 100
     sizes = [n, n, n, n]
     offs = [1, 5, 3, 7]
-    # bf16 p/g with f32 m/v at offset k: head (8 - k) mod 8
-    ranges = [[(0, 2), (500, 700)],          # part of the head (offset 1: head 7)
-              [(0, 3)],                      # the whole head (offset 5: head 3)
-              [(0, 1030), (2000, 2001)],     # the head and the first aligned unit (offset 3: head 5)
-              [(2 * 1024 + 1, n)]]           # the last unit wholly inactive (offset 7: head 1)
+    # bf16 p/g with f32 m/v at offset k: head (64 - k) mod 64 (the next 128-byte line)
+    ranges = [[(0, 2), (500, 700)],          # part of the head (offset 1: head 63)
+              [(0, 59)],                     # exactly the head (offset 5: head 59)
+              [(0, 1100), (2000, 2001)],     # the head and the first aligned unit (offset 3: head 61)
+              [(2106, n)]]                   # the last unit wholly inactive (offset 7: head 57)
     for kw in (dict(buffer="T2", lr=1e-3), dict(buffer=2, lr=1e-3, cautious=False),
                dict(buffer="T2", lr=1e-3, bound_type="radial")):
         with (oracle_mod.radial_sum_f64() if kw.get("bound_type") == "radial" else contextlib.nullcontext()):
