@@ -680,6 +680,7 @@ static void fill_args_common(Args &args, const lv_config *cfg, const Item &h, in
     args.lam1 = 0.5f * cfg->lam;
     args.neg_lr_wd = -(cfg->lr * cfg->weight_decay);
     args.ratio = cfg->bound_ratio;
+    args.bound_floor = cfg->bound_ratio >= 0x1p-40f ? 1u : 0u;
     StepCoeffs sc = step_coeffs(h.step, cfg->beta1, cfg->beta2, cfg->eps, cfg->tau, cfg->lam);
     args.c1 = sc.c1;
     args.c2 = sc.c2;

@@ -124,7 +124,7 @@ struct Args {
     uint32_t piece_units;  // radial launches: units of the current piece ([unit_base, + piece_units))
     uint32_t group;        // table launches: tensors per head (ubegin[h] is tensor h * group's first unit)
     uint32_t nheads;       // table launches: entries of ubegin
-    uint32_t pad_;
+    uint32_t bound_floor;  // 1 when bound_ratio >= 2^-40: the coordinate bound's b * b is a normal number
     uint64_t xcd_recip;  // unit launches: floor(2^40 / xcds) + 1, so b / xcds == (b * xcd_recip) >> 40
     unsigned long long *slots;    // counting launches: count slots (inline: kSlotWords per tensor, in order)
     unsigned long long *tickets;  // radial fold: finished chunks of the piece, per tensor (left zero)
@@ -382,12 +382,65 @@ __device__ __forceinline__ float tanh_pade(float x_in, const PadeK &c = kPade) {
     return (x * p) / q;
 }
 
-// math.rs:162-186
-template <bool TRI>
-__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio, const PadeK &c = kPade) {
+// IEEE f32 division without the scaling and fix-up steps. The compiler's correctly rounded
+// quotient is v_div_scale (both operands), v_rcp_f32, fma/mul refinement, v_div_fmas and
+// v_div_fixup: 11 instructions, about 15.5 integer adds of issue time on gfx950 (the scale, fmas
+// and fixup steps issue at about 1.6 each, v_rcp at 3). Where v_div_scale leaves both operands
+// as they are (vcc clear) v_div_fmas is a plain fma, and where v_div_fixup finds no special case
+// it only puts back the sign the quotient already has; the rest is the same v_rcp_f32 and the same
+// seven fma/mul in the same order, so this equals n / d bit for bit when: n and d are normal and
+// finite, |n| >= 2^-103, |n / d| is a normal number (no overflow, not below 2^-126), 1 / d is
+// normal and the exponents of n and d are less than 96 apart. Callers test their own sufficient
+// condition, wave-uniformly, and otherwise divide as usual.
+__device__ __forceinline__ float div_unscaled(float n, float d) {
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float e0 = __builtin_fmaf(-d, r0, 1.0f);
+    const float r1 = __builtin_fmaf(e0, r0, r0);
+    const float q0 = n * r1;
+    const float e1 = __builtin_fmaf(-d, q0, n);
+    const float q1 = __builtin_fmaf(e1, r1, q0);
+    const float e2 = __builtin_fmaf(-d, q1, n);
+    return __builtin_fmaf(e2, r1, q1);
+}
+
+// clm / env of T1, T2 and TD-CLM, where |clm| <= env up to rounding (env adds the
+// magnitudes of clm's two terms and non-negative ones): with |clm| >= 2^-100 and env <= 2^25,
+// env >= 2^-101 is normal, the quotient is at least 2^-125 and the exponents are at most one
+// apart, so div_unscaled is exact. NaNs and infinities fail one of the two compares.
+__device__ __forceinline__ float div_envelope(float n, float d) {
+    const uint64_t small = __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(n) >= 0x1p-100f));
+    const uint64_t large = __builtin_amdgcn_ballot_w64(!(d <= 0x1p25f));
+    if (__builtin_expect((small | large) == 0, 1)) return div_unscaled(n, d);
+    return n / d;
+}
+
+// (bb * s) / (s * s + bb) of the rational bounds, bb = b (b + |s|) > 0. Its magnitude is at most
+// sqrt(bb) / 2 <= sqrt(d) / 2 (AM-GM), so |n| >= 2^-100 puts d above 2^-66, and with d <= 2^25
+// the quotient lies in [2^-125, 2^12.5]: div_unscaled is exact. A NaN or infinite d fails the
+// test. `zero_lane`: this lane's step is a masked cautious step, an exact +-0 (so n is one and
+// d = bb, a normal number below 2^25 when the caller knows a floor on b); div_unscaled then
+// gives a zero of either sign, and that sign is lost anyway where the caller also knows weight
+// decay is on: the decayed param p + (-lr wd) p is never -0, and p_dec - (+-0) is the same for
+// every other p_dec.
+// `zero_lanes` is a wave mask (the ballot of the lanes whose step is such a zero, or 0), and the
+// test's masks are combined on the scalar unit: a ballot of a combined condition would go through
+// a VGPR (a select and a compare per element).
+__device__ __forceinline__ float div_bound(float n, float d, uint64_t zero_lanes) {
+    const uint64_t small = __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(n) >= 0x1p-100f));
+    const uint64_t large = __builtin_amdgcn_ballot_w64(!(d <= 0x1p25f));
+    if (__builtin_expect(((small & ~zero_lanes) | large) == 0, 1)) return div_unscaled(n, d);
+    return n / d;
+}
+
+// math.rs:162-186. TRI: zero_lanes as for div_bound, with the floor b >= ratio * 0.01 >= 2^-46.7
+// (the caller's bound_floor) giving bb >= 2^-93.
+template <bool TRI, bool FAST = false>
+__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio, const PadeK &c = kPade,
+                                                  uint64_t zero_lanes = 0) {
     if constexpr (TRI) {
         float b = ratio * (fabsf(p_init) + 1.0e-2f);
         float bb = b * (b + fabsf(step));
+        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes);
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
         // p^2 + 1e-4 is at least 1e-4 (or NaN or +inf), where the root needs no rescaling
@@ -396,11 +449,15 @@ __device__ __forceinline__ float coordinate_bound(float step, float p_init, floa
     }
 }
 
-template <bool TRI>
-__device__ __forceinline__ float fp16_safety_bound(float step, float p_init, const PadeK &c = kPade) {
+// TRI: zero_lanes as for div_bound; here b >= 1.5e-4 always (f32::max returns 1.5e-4 for a NaN
+// p too), so bb >= 2.25e-8.
+template <bool TRI, bool FAST = false>
+__device__ __forceinline__ float fp16_safety_bound(float step, float p_init, const PadeK &c = kPade,
+                                                   uint64_t zero_lanes = 0) {
     float b = __builtin_fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);
     if constexpr (TRI) {
         float bb = b * (b + fabsf(step));
+        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes);
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
         return b * tanh_pade(step / b, c);
@@ -453,7 +510,10 @@ struct LaneK {
 
 // u, m_new, v_new for one element.
 // CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
-template <int MODE>
+// FAST: the triangle envelope's quotient through div_envelope (kernels whose time is their VALU
+// work: 16-bit state or fp16 params; the f32-state kernels stream at the HBM's rate and measured
+// level or 1.3% slower with the guard's branches).
+template <int MODE, bool FAST = false>
 __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, const LaneK &lk, bool clamp_v, float g,
                                            float m, float v, float &m_new, float &v_new) {
     m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
@@ -473,7 +533,7 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, c
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
         float env = __builtin_fmaf(k.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
-        return clm / env;
+        return FAST ? div_envelope(clm, env) : clm / env;
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
         float diff = clamp_defect(g - m);
@@ -481,7 +541,7 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, c
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
         v_new = 0.0f;
-        return clm / env;
+        return FAST ? div_envelope(clm, env) : clm / env;
     }
 }
 
@@ -660,17 +720,24 @@ __device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
 // dual.rs / tdclm.rs): the cautious scale cs, the radial scale bs or the coordinate bound, the
 // fp16 safety bound, weight decay. u_eff is the masked direction whose square feeds the radial
 // norm (dual.rs:176-180).
-template <int MODE, int PT>
+// active_lanes: the ballot of `active`, taken where the compare is (a lane mask kept across
+// branches would be rebuilt from a VGPR).
+template <int MODE, int PT, bool FAST = false>
 __device__ __forceinline__ float param_update(const Args &a, const LaneK &lk, uint32_t flags, float cs, float bs,
-                                              float p_init, float u, bool active, float &u_eff) {
+                                              float p_init, float u, bool active, uint64_t active_lanes,
+                                              float &u_eff) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
     float m_mask = active ? 1.0f : 0.0f;
     u_eff = (flags & kFCautious) ? u * m_mask : u;
     float delta = (flags & kFCautious) ? u_eff * cs : u;
     float step = a.lr * delta;
+    // masked steps are exact +-0s whose sign the weight decay makes irrelevant (div_bound): the
+    // wave's mask of them, from the ballot of the cautious compare itself
+    const uint64_t masked = ((flags & kFCautious) && (flags & kFWeightDecay)) ? ~active_lanes : 0;
     if (flags & kFRadial) step *= bs;
-    else if (flags & kFCoordinate) step = coordinate_bound<kTri>(step, p_init, a.ratio, lk.pade);
-    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri>(step, p_init, lk.pade);
+    else if (flags & kFCoordinate)
+        step = coordinate_bound<kTri, FAST>(step, p_init, a.ratio, lk.pade, a.bound_floor ? masked : 0);
+    if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri, FAST>(step, p_init, lk.pade, masked);
     float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
     return p_dec - step;
 }
@@ -684,15 +751,17 @@ __device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, c
                                            float cs, float bs, float p_init, float g_raw, float &m_io,
                                            float &v_io, float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
+    constexpr bool kFast = ST != LV_DTYPE_F32;  // the guarded divisions where VALU work is the bound
     const bool sr = flags & kFSR;
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    float u = compute_u<MODE, kFast>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
     bool active = (u * g) > 0.0f;
+    const uint64_t active_lanes = __builtin_amdgcn_ballot_w64(active);
     tally<TALLY>(cnt, active);
     m_io = quantize<ST>(m_new, z.m, sr);
     if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
-    float p_upd = param_update<MODE, PT>(a, lk, flags, cs, bs, p_init, u, active, u_eff);
+    float p_upd = param_update<MODE, PT, kFast>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff);
     if (flags & kFMaster) {
         mp_out = p_upd;
         p_out = quantize<PT>(p_upd, z.p, false);
@@ -702,20 +771,21 @@ __device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, c
 }
 
 // apply_elem without the quantisation: m_io and v_io receive m' and v', p_out the updated param
-// (and mp_out too, with master weights), all in f32, for quantize_lane.
-template <int MODE, int PT, int TALLY>
+// (and mp_out too, with master weights), all in f32, for quantize_lane. FAST as for compute_u.
+template <int MODE, int PT, int TALLY, bool FAST>
 __device__ __forceinline__ void update_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags,
                                             float cs, float bs, float p_init, float g_raw, float &m_io, float &v_io,
                                             float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    float u = compute_u<MODE, FAST>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
     bool active = (u * g) > 0.0f;
+    const uint64_t active_lanes = __builtin_amdgcn_ballot_w64(active);
     tally<TALLY>(cnt, active);
     m_io = m_new;
     if constexpr (kDual) v_io = v_new;
-    p_out = param_update<MODE, PT>(a, lk, flags, cs, bs, p_init, u, active, u_eff);
+    p_out = param_update<MODE, PT, FAST>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff);
     if (flags & kFMaster) mp_out = p_out;
 }
 
@@ -1036,8 +1106,8 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
             if constexpr (PT == LV_DTYPE_F16) {
                 // fp16 params: the lane's values are quantised together below (2% faster on the
                 // fp16-container cfg4 step than element by element)
-                update_elem<MODE, PT, kTally>(a, tv.k, lk, flags, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j], mpout[j],
-                                              ue, cnt);
+                update_elem<MODE, PT, kTally, ST != LV_DTYPE_F32>(a, tv.k, lk, flags, tv.cs, tv.bs, pin[j], g[j], m[j], vj,
+                                                                   pout[j], mpout[j], ue, cnt);
             } else {
                 // quantised element by element: each hash then overlaps the next element's arithmetic
                 // (quantising the lane's bf16 values together after all of them measured 4% slower)

@@ -13,7 +13,8 @@
 //   pack_f16_rtz on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
 //   sr_f16_add + pack_f16_rtz against the reference's fp16 stochastic rounding (prng.rs:98-130,
 //     restated here) on every input of its domain (sr_f16_domain) with 6 noise values per input (0, 1, 0xFFF,
-//     0x1000, 0x1FFF and a hash of the input), and the domain test against its definition, 2^32.
+//     0x1000, 0x1FFF and a hash of the input), and the domain test against its definition, 2^32;
+//   the guarded fast divisions (div_envelope, div_bound) against IEEE division (div_check).
 // Test infrastructure: built by __graft_entry__.build() into tests/gpu_checks/libexactcheck.so
 // and run by tests/test_gpu_exact_exhaustive.py.
 #include <hip/hip_runtime.h>
@@ -199,6 +200,93 @@ extern "C" int exact_check(unsigned long long *host_counts /* kCounters */, uint
         rc = -3;
     if (rc == 0 && hipMemcpy(host_examples, ex, 8 * kCounters * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess)
         rc = -3;
+    (void)hipFree(out);
+    (void)hipFree(ex);
+    return rc;
+}
+
+namespace {
+
+// A float with the exponent drawn from [lo, hi] (unbiased exponents) and a random mantissa.
+__device__ float rand_float(uint32_t h, int lo, int hi) {
+    const uint32_t span = (uint32_t)(hi - lo + 1);
+    const int e = lo + (int)((h >> 23) % span);
+    return __uint_as_float(((uint32_t)(e + 127) << 23) | (mix32(h) & 0x007FFFFFu));
+}
+
+__device__ bool same_bits(float a, float b) {
+    const uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    return x == y || (is_nan(x) && is_nan(y));
+}
+
+// The guarded fast divisions (lv_device.h: div_unscaled under div_envelope's and div_bound's
+// tests) against the IEEE quotient the compiler's own division gives. Counters: [0] div_envelope
+// on all 2^32 numerators x 3 denominators in [|n| / 2, 2^25]; [1] T2's clm / env from its own
+// formula (compute_u) on all 2^32 gradient bit patterns x a random state; [2] the rational bound
+// (bb * s) / (s * s + bb) through div_bound on all 2^32 step bit patterns x a random b (a zero
+// quotient may differ in sign there: zero_ok); [3] the pairs checked in [0], sampled one input in
+// 2^16 (not mismatches: the size of the domain checked).
+__global__ void check_div(uint32_t base, unsigned long long *out, uint32_t *ex) {
+    const uint32_t i = base + blockIdx.x * blockDim.x + threadIdx.x;
+    const float n = __uint_as_float(i);
+    const float an = __builtin_fabsf(n);
+    // [0]: d from |n| / 2 (at least 2^-101) to 2^25, when that range is not empty
+    if (an >= 0x1p-100f && an <= 0x1p25f) {
+        const int elo = (int)((__float_as_uint(an) >> 23) & 0xFFu) - 128;  // exponent of |n| / 2
+        const float ds[3] = {an, rand_float(mix32(i ^ 0x1234567u), elo < -101 ? -101 : elo, 24),
+                             __builtin_fmaxf(an * 0.5f, 0x1p-101f)};
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const float d = ds[k];
+            if (!(d >= an * 0.5f && d <= 0x1p25f)) continue;
+            if (!same_bits(lv::div_envelope(n, d), n / d)) record(&out[0], ex + 0, i);
+            if ((i & 0xFFFFu) == 0u) atomicAdd(&out[3], 1ull);  // sampled: one in 2^16
+        }
+    }
+    // [1]: T2's masked direction, g = the input bits, m, v from a hash of it
+    {
+        const uint32_t h = mix32(i * 0x9E3779B9u);
+        const float g = n;
+        const float m = (h & 1u ? -1.0f : 1.0f) * rand_float(h, -40, 4);
+        const float v = rand_float(mix32(h), -60, 2);
+        const float b1sq = 0.9f * 0.9f, omb1sq = 1.0f - b1sq, lam1 = 0.15f, eps = 1e-8f, c_sigma = 0.1503f;
+        const float clm = __builtin_fmaf(b1sq, m, omb1sq * g);
+        const float diff = g - m;
+        const float env0 = __builtin_fmaf(b1sq, __builtin_fabsf(m), eps);
+        const float env1 = __builtin_fmaf(omb1sq, __builtin_fabsf(g), env0);
+        const float env2 = __builtin_fmaf(lam1, __builtin_fabsf(diff), env1);
+        const float env = __builtin_fmaf(c_sigma, __builtin_sqrtf(v), env2);
+        if (!same_bits(lv::div_envelope(clm, env), clm / env)) record(&out[1], ex + 8, i);
+    }
+    // [2]: the rational bound over every step value s, b = ratio * (|p| + 0.01) for a random p
+    {
+        const uint32_t h = mix32(i ^ 0xA5A5A5A5u);
+        const float s = n;
+        const float b = rand_float(h, -50, 6);
+        const float bb = b * (b + __builtin_fabsf(s));
+        const float num = bb * s, den = __builtin_fmaf(s, s, bb);
+        const float got = lv::div_bound(num, den, __builtin_amdgcn_ballot_w64(s == 0.0f && b >= 0x1p-46f));
+        const float want = num / den;
+        const bool ok = same_bits(got, want) || (got == 0.0f && want == 0.0f);
+        if (!ok) record(&out[2], ex + 16, i);
+    }
+}
+
+}  // namespace
+
+extern "C" int div_check(unsigned long long *host_counts /* 4 */, uint32_t *host_examples /* 8 x 4 */) {
+    unsigned long long *out = nullptr;
+    uint32_t *ex = nullptr;
+    if (hipMalloc(&out, 4 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMalloc(&ex, 32 * sizeof(uint32_t)) != hipSuccess) return -1;
+    if (hipMemset(out, 0, 4 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMemset(ex, 0, 32 * sizeof(uint32_t)) != hipSuccess) return -1;
+    const uint32_t per = 1u << 24;
+    for (uint64_t b = 0; b < (1ull << 32); b += per) check_div<<<per / 256, 256>>>((uint32_t)b, out, ex);
+    int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -2;
+    if (rc == 0 && hipMemcpy(host_counts, out, 4 * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
+        rc = -3;
+    if (rc == 0 && hipMemcpy(host_examples, ex, 32 * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) rc = -3;
     (void)hipFree(out);
     (void)hipFree(ex);
     return rc;

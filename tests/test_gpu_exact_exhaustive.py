@@ -19,7 +19,12 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   reference's fp16 quantisation never yields an infinity);
 * sr_f16_add + pack_f16_rtz (the integer add and round-toward-zero pack) against the reference's
   integer recipe (prng.rs:98-130) on every input of its domain (+-0 and 2^-14 <= |x| < 65504) x 6
-  noise values, and its domain test on all 2^32 inputs.
+  noise values, and its domain test on all 2^32 inputs;
+* the guarded fast divisions (div_envelope, div_bound: v_rcp_f32 and the IEEE sequence's own
+  fma refinement without its scaling and fix-up steps, taken when a wave-uniform test proves
+  them unneeded) against IEEE division: every 2^32 numerator with denominators from n/2 to 2^25,
+  T2's clm / env from its own formula for every gradient bit pattern, and the rational bound for
+  every step value.
 """
 from __future__ import annotations
 
@@ -65,3 +70,21 @@ def test_exact_helpers_on_every_input():
     # 2^16 in [0x38800000, 0x477FE000)
     per_sign = 1 + len(range(0x38800000, 0x477FE000, 65536))
     assert counts[10] == 2 * per_sign
+
+
+def test_guarded_fast_divisions_equal_ieee_division():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    lib = _lib()
+    lib.div_check.restype = ctypes.c_int
+    lib.div_check.argtypes = [ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_uint32)]
+    counts = (ctypes.c_ulonglong * 4)()
+    ex = (ctypes.c_uint32 * 32)()
+    print("[case] guarded fast divisions, 2^32 inputs x 5 quotients", flush=True)
+    assert lib.div_check(counts, ex) == 0
+    assert counts[0] == 0, ("div_envelope", [hex(x) for x in ex[0:8]])
+    assert counts[1] == 0, ("T2 clm / env", [hex(x) for x in ex[8:16]])
+    assert counts[2] == 0, ("div_bound", [hex(x) for x in ex[16:24]])
+    # numerators with 2^-100 <= |n| <= 2^25: 2 signs x 125 binades x 2^23, sampled one in 2^16,
+    # with at least 2 of the 3 denominators in range each
+    assert counts[3] >= 2 * 125 * 128 * 2
