@@ -25,6 +25,8 @@ KERNEL_SRC = os.path.join(CSRC, "lv_kernels.hip")
 SRC = HOST_SRC
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libluminav_hip.so")
+HOST_PTRS_SRC = os.path.join(CSRC, "host_ptrs.cpp")
+HOST_PTRS_OUT = os.path.join(OUT_DIR, "_lv_host.so")
 ARCH = os.environ.get("LUMINAV_OFFLOAD_ARCH", "gfx950")
 MODES = (1, 2, 3, 4)  # LV_BUFFER_TDCLM, _DUAL, _T1, _T2
 
@@ -72,5 +74,24 @@ def build(verbose: bool = False) -> str:
     return OUT
 
 
+def build_host(verbose: bool = False) -> str:
+    """Builds _lv_host.so (csrc/host_ptrs.cpp: the step plans' data-pointer checks, CPU code against
+    libtorch's Python API) with torch.utils.cpp_extension, into _lib/."""
+    import shutil
+    import tempfile
+
+    from torch.utils import cpp_extension
+
+    os.makedirs(OUT_DIR, exist_ok=True)
+    with tempfile.TemporaryDirectory() as tmp:
+        cpp_extension.load(name="_lv_host", sources=[HOST_PTRS_SRC], build_directory=tmp, extra_cflags=["-O2"],
+                           verbose=verbose, is_python_module=False)
+        tmp_out = HOST_PTRS_OUT + ".tmp"
+        shutil.copyfile(os.path.join(tmp, "_lv_host.so"), tmp_out)
+        os.replace(tmp_out, HOST_PTRS_OUT)
+    return HOST_PTRS_OUT
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_host(verbose=True))

@@ -94,9 +94,10 @@ struct TDesc {
     uint32_t slot_base;
 };
 
-// Count slots of a tensor of `units` work units in a table launch: the smallest power of two that
-// keeps every slot at <= 64 blocks, at most kSlots. Inline launches give every tensor
-// min(kSlots, units) slots instead (their slot words are preallocated).
+// Count slots of a tensor of `units` work units: the smallest power of two that keeps every slot at
+// <= 64 blocks, at most kSlots (a tensor of <= 64 units has one, whose last block finalises it
+// without the fold word). Inline launches reserve kSlotWords slot words per tensor; table
+// launches lay the tensors' slots out back to back.
 __host__ __device__ inline uint32_t table_count_slots(uint32_t units) {
     const uint32_t c = (units + 63u) >> 6;
     if (c <= 1u) return 1u;
@@ -1236,11 +1237,13 @@ __device__ __forceinline__ int find_tensor(const Args &a, uint32_t unit) {
 // Counting unit launches: thread 0 of every block reports its exact mask count and the block's
 // completion in ONE 64-bit atomic (count << kTicketBits | 1) on one of the tensor's S count slots
 // (slot = unit index in the tensor mod S, 64 B apart, so the atomics spread over L2 channels;
-// S = kSlots inline, table_count_slots(units) in table launches). The block whose report
-// completes a slot (its ticket reaches the slot's block count) holds that slot's whole count in
-// the value its own atomic returned, re-zeroes the slot and reports count << kFoldBits | 1 on the
-// tensor's fold slot (the one after its count slots); the block that completes the fold slot
-// holds the tensor's exact count and finalises the scratch. Every decision reads only the value
+// S = table_count_slots(units): the smallest power of two keeping every slot at <= 64 blocks, at
+// most 64). The block whose report completes a slot (its ticket reaches the slot's block count)
+// holds that slot's whole count in the value its own atomic returned and re-zeroes the slot; a
+// tensor of one slot (<= 64 units) is then complete, and that block finalises the scratch. With
+// more slots it reports count << kFoldBits | 1 on the tensor's fold slot (the one after its count
+// slots), and the block that completes the fold slot holds the tensor's exact count and
+// finalises the scratch. Every decision reads only the value
 // returned by an atomic on that same word, so no fence is needed (a device-scope release fence
 // per block measured 7x slower); integer sums are exact in any order, so the result is
 // deterministic. Wholly inactive units report a zero count.
@@ -1250,7 +1253,7 @@ __device__ __forceinline__ void report_count(const Args &a, const Desc &D, const
     const uint32_t n_units = tv.t_end - tv.t_begin;
     const uint32_t k = unit - tv.t_begin;
     // slot s of S takes units k = s (mod S): n_units / S blocks, plus one for s < n_units % S
-    const uint32_t S = TABLE ? table_count_slots(n_units) : kSlots;  // a power of two
+    const uint32_t S = table_count_slots(n_units);  // a power of two, <= 64 blocks per slot
     const uint32_t s = k & (S - 1u);
     const uint32_t nslots = n_units < S ? n_units : S;
     unsigned long long *words = a.slots + (size_t)tv.slot_base * kSlotStride;
@@ -1262,6 +1265,10 @@ __device__ __forceinline__ void report_count(const Args &a, const Desc &D, const
     if ((uint32_t)(old & kTicketMask) + 1u != expect) return;
     const unsigned long long slot_count = (old >> kTicketBits) + count;
     __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (nslots == 1u) {  // a tensor of <= 64 units: its one slot holds its whole count
+        finalize_scratch<MODE, PASS>(a, false, D, slot_count, 0.0f, 0.0f);
+        return;
+    }
     unsigned long long *fold = words + (size_t)nslots * kSlotStride;
     const unsigned long long prev = __hip_atomic_fetch_add(fold, (slot_count << kFoldBits) | 1ull, __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_AGENT);

@@ -94,6 +94,24 @@ EXPORTED_SYMBOLS = (
 _lib: Optional[ctypes.CDLL] = None
 _lib_lock = threading.Lock()
 
+HOST_EXT_PATH = os.path.join(_LIB_DIR, "_lv_host.so")
+
+
+def load_host_ext() -> Any:
+    """The plans' data-pointer checks (_lv_host.so, built from csrc/host_ptrs.cpp), or None when it
+    is not built (the optimizer then compares pointers in Python: same results, more host time)."""
+    if not os.path.exists(HOST_EXT_PATH):
+        return None
+    try:
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("_lv_host", HOST_EXT_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        return mod
+    except (ImportError, OSError):
+        return None
+
 
 class HipBackendUnavailable(RuntimeError):
     pass

@@ -21,6 +21,7 @@ import functools
 import logging
 import math
 import operator
+import struct
 import warnings
 import weakref
 from collections import defaultdict
@@ -164,6 +165,30 @@ def _bucket_buffers(device: torch.device, specs: List[Tuple[str, torch.dtype, in
 _dict_set = dict.__setitem__
 _get_grad = operator.attrgetter("grad")
 _data_ptr = torch.Tensor.data_ptr
+
+# Data-pointer records of the cached step plans: _ptr_record(tensors) records where a list of
+# tensors' data is, _same_ptrs(tensors, record) tells whether it is still there (False for any
+# entry that is not a tensor), _pack_ptrs(ints) makes a record from pointers. One C loop each
+# when _lv_host.so is built, Python maps otherwise.
+_host = hip_backend.load_host_ext()
+if _host is not None:
+    _ptr_record = _host.ptrs
+    _same_ptrs = _host.same_ptrs
+
+    def _pack_ptrs(ptrs: List[int]) -> bytes:
+        return struct.pack(f"={len(ptrs)}Q", *ptrs)
+else:
+    def _ptr_record(tensors: List[Any]) -> List[int]:
+        return list(map(_data_ptr, tensors))
+
+    def _same_ptrs(tensors: List[Any], record: List[int]) -> bool:
+        try:
+            return list(map(_data_ptr, tensors)) == record
+        except (AttributeError, TypeError):  # an entry that is not a tensor (a grad of None)
+            return False
+
+    def _pack_ptrs(ptrs: List[int]) -> List[int]:
+        return list(ptrs)
 _profiler_enabled = getattr(torch._C._autograd, "_profiler_enabled", lambda: True)
 
 
@@ -1240,12 +1265,12 @@ class LuminaV(Optimizer):
             sl = b["slices"]
             fast = b["fast"] = {
                 "slices": sl, "params": [x[0] for x in sl], "g_views": [x[2] for x in sl],
-                "p_ptrs": [x[3] for x in sl], "states": [x[5] for x in sl], "prep": None,
+                "p_ptrs": _pack_ptrs([x[3] for x in sl]), "states": [x[5] for x in sl], "prep": None,
             }
         params = fast["params"]
         if not all(map(operator.is_, map(_get_grad, params), fast["g_views"])):
             return False
-        if list(map(_data_ptr, params)) != fast["p_ptrs"]:
+        if not _same_ptrs(params, fast["p_ptrs"]):
             return False
         step_t = int(b["step"]) + 1
         prep = fast["prep"]
@@ -1344,14 +1369,14 @@ class LuminaV(Optimizer):
             "params": list(group["params"]), "ids": list(map(id, group["params"])), "active": active,
             # every param has a grad and elements, so the entries follow the params one to one
             "all_active": len(rows) == len(group["params"]),
-            "eparams": eparams, "pptrs": list(map(_data_ptr, eparams)),
-            "gids": list(map(id, egrads)), "gptrs": list(map(_data_ptr, egrads)),
+            "eparams": eparams, "pptrs": _ptr_record(eparams),
+            "gids": list(map(id, egrads)), "gptrs": list(map(_data_ptr, egrads)), "gptr_rec": _ptr_record(egrads),
             "gweak": [weakref.ref(g, died) for g in egrads], "dead": dead, "died": died,
             "states": [r[9] for r in rows], "steps": [int(r[7]) for r in rows], "step_epoch": self._step_epoch,
             "keep": [t.untyped_storage() for r in rows for t in (r[3], r[4], r[5], r[6]) if t is not None],
             # the state tensors themselves and where their data was: `t.data = u` or `t.set_(u)` on
             # a state tensor moves its storage without replacing the state entry
-            "stensors": stensors, "sptrs": list(map(_data_ptr, stensors)),
+            "stensors": stensors, "sptrs": _ptr_record(stensors),
             "prep": prep,
         }
 
@@ -1376,15 +1401,16 @@ class LuminaV(Optimizer):
             if [p.grad is not None for p in params] != plan["active"]:
                 return False
             grads = list(map(_get_grad, plan["eparams"]))
-        if list(map(_data_ptr, plan["eparams"])) != plan["pptrs"]:  # a param's storage moved
+        if not _same_ptrs(plan["eparams"], plan["pptrs"]):  # a param's storage moved
             return False
-        if list(map(_data_ptr, plan["stensors"])) != plan["sptrs"]:  # a state tensor's storage moved
+        if not _same_ptrs(plan["stensors"], plan["sptrs"]):  # a state tensor's storage moved
             return False
         prep = plan["prep"]
         gids = list(map(id, grads))
-        if plan["dead"][0] or gids != plan["gids"] or list(map(_data_ptr, grads)) != plan["gptrs"]:
+        if plan["dead"][0] or gids != plan["gids"] or not _same_ptrs(grads, plan["gptr_rec"]):
             if not self._refresh_plan_grads(plan, grads, gids):
                 return False
+            plan["gptr_rec"] = _ptr_record(grads)
         # nothing above touched the step counters, so a False return leaves them for the slow path
         states = plan["states"]
         if plan["step_epoch"] != self._step_epoch:  # a counter was set from outside: read them again
@@ -1527,7 +1553,7 @@ class LuminaV(Optimizer):
                 if dict.get(st, k) is not t:
                     return False
         # `t.data = u` or `t.set_(u)` on a state tensor moves its storage in place
-        return list(map(_data_ptr, entry["stensors"])) == entry["sptrs"]
+        return _same_ptrs(entry["stensors"], entry["sptrs"])
 
     def _first_capturable_step(self, group: Dict[str, Any], rows: List[Tuple[int, torch.Tensor, torch.Tensor]],
                                key: Tuple[int, ...]) -> None:
@@ -1569,5 +1595,5 @@ class LuminaV(Optimizer):
             "record": record, "workspace": workspace, "params": [p for _, p, _ in rows], "states": states,
             "held": [[(k, dict.get(st, k)) for k in self._HELD_KEYS] for st in states],
             "pptrs": [p.data_ptr() for _, p, _ in rows], "gptrs": [g.data_ptr() for _, _, g in rows],
-            "stensors": stensors, "sptrs": list(map(_data_ptr, stensors)),
+            "stensors": stensors, "sptrs": _ptr_record(stensors),
         }
