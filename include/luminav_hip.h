@@ -151,7 +151,10 @@ int lv_step_multi(const lv_config *cfg, const lv_tensor *tensors, int count,
  * pass, a first step (record->step == 0 before the call) is refused on the device (status 1, the
  * counter and every buffer unchanged); take it through lv_step_multi and set record->step to 1.
  * Results are bit for bit lv_step_multi's for the same step counts. Workspace: as lv_step_multi
- * without table count slots.
+ * without table count slots, but the library does not order these calls across streams (a
+ * capturing stream cannot wait on an event recorded outside its capture): calls that share a
+ * workspace must be ordered by the caller, e.g. one workspace per set of tensors stepped
+ * together, as the tensors themselves require.
  */
 typedef struct lv_step_record {
     uint64_t step;          /* steps taken; each call adds one on the device before stepping */

@@ -681,6 +681,9 @@ static void fill_args_common(Args &args, const lv_config *cfg, const Item &h, in
     args.neg_lr_wd = -(cfg->lr * cfg->weight_decay);
     args.ratio = cfg->bound_ratio;
     args.bound_floor = cfg->bound_ratio >= 0x1p-40f ? 1u : 0u;
+    // facts the kernels' stochastic roundings rely on (kRangeM, kRangeP): false for NaNs
+    if (std::fabs(args.b1) <= 0x1p64f && std::fabs(args.omb1) <= 0x1p64f) args.ranges |= kRangeM;
+    if (args.bound_floor && std::fabs(args.neg_lr_wd) <= 0x1p32f) args.ranges |= kRangeP;
     StepCoeffs sc = step_coeffs(h.step, cfg->beta1, cfg->beta2, cfg->eps, cfg->tau, cfg->lam);
     args.c1 = sc.c1;
     args.c2 = sc.c2;

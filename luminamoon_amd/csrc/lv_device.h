@@ -126,6 +126,7 @@ struct Args {
     uint32_t group;        // table launches: tensors per head (ubegin[h] is tensor h * group's first unit)
     uint32_t nheads;       // table launches: entries of ubegin
     uint32_t bound_floor;  // 1 when bound_ratio >= 2^-40: the coordinate bound's b * b is a normal number
+    uint32_t ranges;       // kRange* facts about the hyper-parameters (the host tests them per launch)
     uint64_t xcd_recip;  // unit launches: floor(2^40 / xcds) + 1, so b / xcds == (b * xcd_recip) >> 40
     unsigned long long *slots;    // counting launches: count slots (inline: kSlotWords per tensor, in order)
     unsigned long long *tickets;  // radial fold: finished chunks of the piece, per tensor (left zero)
@@ -149,6 +150,12 @@ constexpr int kTableHeads = kMaxDesc * (int)(sizeof(Desc) / sizeof(uint32_t));  
 static_assert(sizeof(Desc) == 80, "descriptor layout");
 static_assert(sizeof(TDesc) == 88, "table descriptor layout");
 static_assert(sizeof(Args) <= 4096, "kernel arguments must fit in 4 KiB");
+
+// Args::ranges. kRangeM: |beta1| and |1 - beta1| are at most 2^64, so m' = beta1 m + (1 - beta1) g
+// stays below 2^126 whenever |g| <= 1e18 and |g - m| <= 1e18. kRangeP: bound_floor, and
+// |lr * weight_decay| is at most 2^32, so a param the coordinate bound's fast quotient took
+// (|p| <= 2^52.5, |step| <= 2^11.5: div_bound) decays and steps to below 2^86.
+enum : uint32_t { kRangeM = 1u, kRangeP = 2u };
 
 // ------------------------------------------------------------------ per-step coefficients
 
@@ -340,6 +347,22 @@ __device__ __forceinline__ float clamp_defect(float d) {
     return __builtin_isnan(d) ? d : __builtin_amdgcn_fmed3f(d, -1.0e18f, 1.0e18f);
 }
 
+// The same, telling whether every lane of the wave took the identity (|d| <= 1e18, no NaN).
+__device__ __forceinline__ float clamp_defect(float d, bool &identity) {
+    identity = wave_all(fabsf(d) <= 1.0e18f);
+    if (__builtin_expect(identity, 1)) return d;
+    return __builtin_isnan(d) ? d : __builtin_amdgcn_fmed3f(d, -1.0e18f, 1.0e18f);
+}
+
+// fma(a, |x|, c) as ONE v_fma_f32 with the abs source modifier (a wave-uniform). Written as
+// __builtin_fmaf(a, fabsf(x), c) the compiler materialises |x| with a v_and_b32 and uses the
+// 2-operand v_fmac_f32: one more VALU instruction for the same result.
+__device__ __forceinline__ float fma_abs(float a, float x, float c) {
+    float r;
+    asm("v_fma_f32 %0, %1, |%2|, %3" : "=v"(r) : "s"(a), "v"(x), "v"(c));
+    return r;
+}
+
 // Correctly rounded sqrt (sqrt_rn in lv_exact.h) with its small-input rescaling skipped when no
 // lane of the wave needs it (x >= 2^-96, +-0, +inf and NaN need none).
 __device__ __forceinline__ float sqrt_cr(float x) {
@@ -426,22 +449,27 @@ __device__ __forceinline__ float div_envelope(float n, float d) {
 // `zero_lanes` is a wave mask (the ballot of the lanes whose step is such a zero, or 0), and the
 // test's masks are combined on the scalar unit: a ballot of a combined condition would go through
 // a VGPR (a select and a compare per element).
-__device__ __forceinline__ float div_bound(float n, float d, uint64_t zero_lanes) {
+// `fast` tells the caller which way the wave went: on the fast side every lane has d <= 2^25.
+__device__ __forceinline__ float div_bound(float n, float d, uint64_t zero_lanes, bool &fast) {
     const uint64_t small = __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(n) >= 0x1p-100f));
     const uint64_t large = __builtin_amdgcn_ballot_w64(!(d <= 0x1p25f));
-    if (__builtin_expect(((small & ~zero_lanes) | large) == 0, 1)) return div_unscaled(n, d);
+    fast = ((small & ~zero_lanes) | large) == 0;
+    if (__builtin_expect(fast, 1)) return div_unscaled(n, d);
     return n / d;
 }
 
 // math.rs:162-186. TRI: zero_lanes as for div_bound, with the floor b >= ratio * 0.01 >= 2^-46.7
-// (the caller's bound_floor) giving bb >= 2^-93.
+// (the caller's bound_floor) giving bb >= 2^-93. `fast`: the wave took div_bound's fast side,
+// where d = step^2 + bb <= 2^25 bounds b^2 <= bb, so |p_init| <= 2^12.5 / ratio, and the result,
+// at most sqrt(bb) / 2, is at most 2^11.5 (false when FAST is off).
 template <bool TRI, bool FAST = false>
-__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio, const PadeK &c = kPade,
-                                                  uint64_t zero_lanes = 0) {
+__device__ __forceinline__ float coordinate_bound(float step, float p_init, float ratio, const PadeK &c, uint64_t zero_lanes,
+                                                  bool &fast) {
+    fast = false;
     if constexpr (TRI) {
         float b = ratio * (fabsf(p_init) + 1.0e-2f);
         float bb = b * (b + fabsf(step));
-        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes);
+        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes, fast);
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
         // p^2 + 1e-4 is at least 1e-4 (or NaN or +inf), where the root needs no rescaling
@@ -458,7 +486,8 @@ __device__ __forceinline__ float fp16_safety_bound(float step, float p_init, con
     float b = __builtin_fmaxf(fabsf(p_init) * 0.01f, 1.5e-4f);
     if constexpr (TRI) {
         float bb = b * (b + fabsf(step));
-        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes);
+        bool fast;
+        if constexpr (FAST) return div_bound(bb * step, __builtin_fmaf(step, step, bb), zero_lanes, fast);
         return (bb * step) / __builtin_fmaf(step, step, bb);
     } else {
         return b * tanh_pade(step / b, c);
@@ -509,14 +538,26 @@ struct LaneK {
     PadeK pade;
 };
 
+// What compute_u<FAST> found out about the wave (wave-uniform bits):
+// kKnownM: every lane's defect |g - m| is at most 1e18 (clamp_defect was the identity), so with
+//   |g| <= 1e18 (sanitize) |m| <= 2e18; with Args::ranges' kRangeM, m' is then below 2^126.
+// kKnownV (T2): every lane's v' lies in [2^-96, the largest finite bf16]: no lane's root needs the
+//   small-input rescaling or the clamp at 0, and no lane's bf16 rounding of v' needs the
+//   saturation or NaN handling (sr_bf16_checked).
+enum : uint32_t { kKnownM = 1u, kKnownV = 2u };
+
 // u, m_new, v_new for one element.
 // CLM: dual.rs:63-74.  T2: dual.rs:492-506.  TD-CLM / T1: tdclm.rs:102-109.
 // FAST: the triangle envelope's quotient through div_envelope (kernels whose time is their VALU
 // work: 16-bit state or fp16 params; the f32-state kernels stream at the HBM's rate and measured
-// level or 1.3% slower with the guard's branches).
-template <int MODE, bool FAST = false>
+// level or 1.3% slower with the guard's branches), and `known` (kKnown*) for T1 and T2. T2's root
+// of v' takes one range test for both of kKnownV's facts (a subtraction and one unsigned compare
+// of the bits: below 2^-96, negative, NaN and above the largest bf16 all fall outside) instead of
+// the clamp at 0 and the root's own two compares.
+template <int MODE, bool FAST>
 __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, const LaneK &lk, bool clamp_v, float g,
-                                           float m, float v, float &m_new, float &v_new) {
+                                           float m, float v, float &m_new, float &v_new, uint32_t &known) {
+    known = 0;
     m_new = __builtin_fmaf(a.b1, m, a.omb1 * g);
     if constexpr (MODE == LV_BUFFER_DUAL) {
         float clm = __builtin_fmaf(a.b1, m_new, a.omb1 * g);
@@ -527,6 +568,21 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, c
         return tanh_pade(clm / __builtin_fmaxf(sigma, 1.0e-12f), lk.pade);
     } else if constexpr (MODE == LV_BUFFER_T2) {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        if constexpr (FAST) {
+            bool defect_ok;
+            const float diff = clamp_defect(g - m, defect_ok);
+            v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
+            if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
+            const float env0 = __builtin_fmaf(a.b1sq, fabsf(m), lk.eps);
+            const float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+            const float env2 = fma_abs(a.lam1, diff, env1);
+            const bool v_ok = wave_all(f_bits(v_new) - 0x0F800000u <= kBf16MaxBits - 0x0F800000u);
+            float root;
+            if (__builtin_expect(v_ok, 1)) root = sqrt_rn_normal(v_new);
+            else root = sqrt_cr(__builtin_fmaxf(v_new, 0.0f));
+            known = (defect_ok ? kKnownM : 0u) | (v_ok ? kKnownV : 0u);
+            return div_envelope(clm, __builtin_fmaf(k.c_sigma, root, env2));
+        }
         float diff = clamp_defect(g - m);
         v_new = __builtin_fmaf(a.b2, v, a.omb2 * (diff * diff));
         if (clamp_v) v_new = __builtin_fminf(v_new, 65000.0f);
@@ -534,16 +590,31 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, c
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env2 = __builtin_fmaf(a.lam1, fabsf(diff), env1);
         float env = __builtin_fmaf(k.c_sigma, sqrt_cr(__builtin_fmaxf(v_new, 0.0f)), env2);
-        return FAST ? div_envelope(clm, env) : clm / env;
+        return clm / env;
     } else {
         float clm = __builtin_fmaf(a.b1sq, m, a.omb1sq * g);
+        v_new = 0.0f;
+        if constexpr (FAST && MODE == LV_BUFFER_T1) {
+            bool defect_ok;
+            const float diff = clamp_defect(g - m, defect_ok);
+            const float env0 = __builtin_fmaf(a.b1sq, fabsf(m), lk.eps);
+            const float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
+            known = defect_ok ? kKnownM : 0u;
+            return div_envelope(clm, fma_abs(a.lam, diff, env1));
+        }
         float diff = clamp_defect(g - m);
         float env0 = __builtin_fmaf(a.b1sq, fabsf(m), lk.eps);
         float env1 = __builtin_fmaf(a.omb1sq, fabsf(g), env0);
         float env = __builtin_fmaf(a.lam, fabsf(diff), env1);
-        v_new = 0.0f;
         return FAST ? div_envelope(clm, env) : clm / env;
     }
+}
+
+template <int MODE, bool FAST = false>
+__device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, const LaneK &lk, bool clamp_v, float g,
+                                           float m, float v, float &m_new, float &v_new) {
+    uint32_t known;
+    return compute_u<MODE, FAST>(a, k, lk, clamp_v, g, m, v, m_new, v_new, known);
 }
 
 // ------------------------------------------------------------------ loads / stores
@@ -723,70 +794,115 @@ __device__ __forceinline__ HashIn hash_in(const Seeds &sd, uint32_t off) {
 // norm (dual.rs:176-180).
 // active_lanes: the ballot of `active`, taken where the compare is (a lane mask kept across
 // branches would be rebuilt from a VGPR).
+// The cautious scale cs of a unit for its active lanes, and 0 * cs for its masked ones: the
+// reference's (u * mask) * cs (dual.rs:150-160) is u * cs where mask = 1 and (u * 0) * cs where
+// mask = 0, and (u * 0) * cs equals u * (0 * cs) bit for bit for every u and cs (a zero whose sign
+// is sign(u) xor sign(cs), or NaN when u or cs is NaN or infinite), so an element's delta is ONE
+// multiply by a select of the two. The vector path keeps both in VGPRs (a select reads at most one
+// scalar operand).
+struct CsPair {
+    float on, off;
+};
+
+__device__ __forceinline__ CsPair cs_pair(float cs) { return {cs, 0.0f * cs}; }
+
+// Both in VGPRs, copied once per unit.
+__device__ __forceinline__ CsPair cs_pair_vgpr(float cs) {
+    CsPair r;
+    asm("v_mov_b32 %0, %1" : "=v"(r.on) : "s"(cs));
+    asm("v_mul_f32 %0, 0, %1" : "=v"(r.off) : "v"(r.on));
+    return r;
+}
+
+// p_fast: the coordinate bound took div_bound's fast side in every lane of the wave (FAST only), so
+// with Args::ranges' kRangeP the updated param is finite and below 2^86 in every lane.
 template <int MODE, int PT, bool FAST = false>
-__device__ __forceinline__ float param_update(const Args &a, const LaneK &lk, uint32_t flags, float cs, float bs,
+__device__ __forceinline__ float param_update(const Args &a, const LaneK &lk, uint32_t flags, const CsPair &cs, float bs,
                                               float p_init, float u, bool active, uint64_t active_lanes,
-                                              float &u_eff) {
+                                              float &u_eff, bool &p_fast) {
     constexpr bool kTri = (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_T2);
     float m_mask = active ? 1.0f : 0.0f;
-    u_eff = (flags & kFCautious) ? u * m_mask : u;
-    float delta = (flags & kFCautious) ? u_eff * cs : u;
+    u_eff = (flags & kFCautious) ? u * m_mask : u;  // read by the radial passes only
+    float delta = (flags & kFCautious) ? u * (active ? cs.on : cs.off) : u;
     float step = a.lr * delta;
     // masked steps are exact +-0s whose sign the weight decay makes irrelevant (div_bound): the
     // wave's mask of them, from the ballot of the cautious compare itself
     const uint64_t masked = ((flags & kFCautious) && (flags & kFWeightDecay)) ? ~active_lanes : 0;
+    p_fast = false;
     if (flags & kFRadial) step *= bs;
     else if (flags & kFCoordinate)
-        step = coordinate_bound<kTri, FAST>(step, p_init, a.ratio, lk.pade, a.bound_floor ? masked : 0);
+        step = coordinate_bound<kTri, FAST>(step, p_init, a.ratio, lk.pade, a.bound_floor ? masked : 0, p_fast);
     if constexpr (PT == LV_DTYPE_F16) step = fp16_safety_bound<kTri, FAST>(step, p_init, lk.pade, masked);
     float p_dec = (flags & kFWeightDecay) ? __builtin_fmaf(a.neg_lr_wd, p_init, p_init) : p_init;
     return p_dec - step;
+}
+
+// quantize<DT> where the caller may know (`in_range`, wave-uniform) that every lane's value is
+// finite and at most the largest finite bf16: then a bf16 stochastic rounding is the add alone,
+// without sr_bf16_checked's compare.
+template <int DT>
+__device__ __forceinline__ float quantize_known(float v, uint32_t z0, bool sr, bool in_range) {
+    if constexpr (DT == LV_DTYPE_BF16) {
+        if (!sr) return rne_bf16(v);
+        const uint32_t noise = xor_fold16((uint32_t)prng_mixed(z0));
+        if (__builtin_expect(in_range, 1)) return sr_bf16_add(v, noise);
+        return sr_bf16_checked(v, noise);
+    } else {
+        return quantize<DT>(v, z0, sr);
+    }
 }
 
 // Apply path for one element. Counts the cautious mask bit into cnt (TALLY). m and v are
 // quantised as soon as they are known: the hashes of their stochastic rounding then overlap the
 // param's bound (each wave-uniform guard limits how far the compiler moves code). With master
 // weights p is rounded to nearest from the master (the master keeps the f32 value).
+// With 16-bit state (kFast) the roundings skip the range tests compute_u and param_update have
+// already settled for the whole wave (kKnownM with kRangeM for m', kKnownV for v', the coordinate
+// bound's fast side with kRangeP for p).
 template <int MODE, int PT, int ST, int TALLY>
 __device__ __forceinline__ void apply_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags, const HashIn &z,
-                                           float cs, float bs, float p_init, float g_raw, float &m_io,
+                                           const CsPair &cs, float bs, float p_init, float g_raw, float &m_io,
                                            float &v_io, float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     constexpr bool kFast = ST != LV_DTYPE_F32;  // the guarded divisions where VALU work is the bound
     const bool sr = flags & kFSR;
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE, kFast>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    uint32_t known;
+    float u = compute_u<MODE, kFast>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new, known);
     bool active = (u * g) > 0.0f;
     const uint64_t active_lanes = __builtin_amdgcn_ballot_w64(active);
     tally<TALLY>(cnt, active);
-    m_io = quantize<ST>(m_new, z.m, sr);
-    if constexpr (kDual) v_io = quantize<ST>(v_new, z.v, sr);
-    float p_upd = param_update<MODE, PT, kFast>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff);
+    m_io = quantize_known<ST>(m_new, z.m, sr, (known & kKnownM) && (a.ranges & kRangeM));
+    if constexpr (kDual) v_io = quantize_known<ST>(v_new, z.v, sr, known & kKnownV);
+    bool p_fast;
+    float p_upd = param_update<MODE, PT, kFast>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff, p_fast);
     if (flags & kFMaster) {
         mp_out = p_upd;
         p_out = quantize<PT>(p_upd, z.p, false);
     } else {
-        p_out = quantize<PT>(p_upd, z.p, sr);
+        p_out = quantize_known<PT>(p_upd, z.p, sr, p_fast && (a.ranges & kRangeP));
     }
 }
 
 // apply_elem without the quantisation: m_io and v_io receive m' and v', p_out the updated param
 // (and mp_out too, with master weights), all in f32, for quantize_lane. FAST as for compute_u.
+// `known` receives compute_u's facts (kKnown*).
 template <int MODE, int PT, int TALLY, bool FAST>
 __device__ __forceinline__ void update_elem(const Args &a, const StepCoeffs &k, const LaneK &lk, uint32_t flags,
-                                            float cs, float bs, float p_init, float g_raw, float &m_io, float &v_io,
-                                            float &p_out, float &mp_out, float &u_eff, uint32_t &cnt) {
+                                            const CsPair &cs, float bs, float p_init, float g_raw, float &m_io, float &v_io,
+                                            float &p_out, float &mp_out, float &u_eff, uint32_t &cnt, uint32_t &known) {
     constexpr bool kDual = (MODE == LV_BUFFER_DUAL || MODE == LV_BUFFER_T2);
     float g = sanitize(g_raw);
     float m_new, v_new;
-    float u = compute_u<MODE, FAST>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new);
+    float u = compute_u<MODE, FAST>(a, k, lk, flags & kFClampV, g, m_io, v_io, m_new, v_new, known);
     bool active = (u * g) > 0.0f;
     const uint64_t active_lanes = __builtin_amdgcn_ballot_w64(active);
     tally<TALLY>(cnt, active);
     m_io = m_new;
     if constexpr (kDual) v_io = v_new;
-    p_out = param_update<MODE, PT, FAST>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff);
+    bool p_fast;
+    p_out = param_update<MODE, PT, FAST>(a, lk, flags, cs, bs, p_init, u, active, active_lanes, u_eff, p_fast);
     if (flags & kFMaster) mp_out = p_out;
 }
 
@@ -797,18 +913,22 @@ __device__ __forceinline__ void update_elem(const Args &a, const StepCoeffs &k, 
 // lane's values to round is NaN or has |x| above the largest finite bf16 in any lane of the wave,
 // all of them go through sr_bf16_prep first (the identity for the others). The maximum of the
 // magnitudes is NaN-propagating (v_maximum3_f32), so the test `!(max <= largest)` sees NaNs.
+// mv_known (wave-uniform): every lane's m (and v) values are known finite and at most the largest
+// finite bf16 (kKnownM with kRangeM, and kKnownV), so they stay out of the test.
 template <int ST, int PT, bool kDual, int N, uint32_t HS>
-__device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, float m[8], float v[8], float p[8]) {
+__device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, float m[8], float v[8], float p[8],
+                                              bool mv_known = false) {
     const bool sr = flags & kFSR;
     const bool psr = sr && !(flags & kFMaster);
     constexpr bool kBfMV = ST == LV_DTYPE_BF16;  // m (and v) rounded stochastically to bf16 when sr
     constexpr bool kBfP = PT == LV_DTYPE_BF16;   // p rounded stochastically to bf16 when psr
     const bool mv_sr = kBfMV && sr, p_sr = kBfP && psr;
-    if (mv_sr || p_sr) {
+    const bool mv_test = mv_sr && !mv_known;
+    if (mv_test || p_sr) {
         float mx = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; j++) {
-            if (mv_sr) {
+            if (mv_test) {
                 mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(m[j]));
                 if constexpr (kDual) mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(v[j]));
             }
@@ -817,7 +937,7 @@ __device__ __forceinline__ void quantize_lane(uint32_t flags, const HashIn &zb, 
         if (__builtin_expect(!wave_all(mx <= __uint_as_float(kBf16MaxBits)), 0)) {
 #pragma unroll
             for (int j = 0; j < N; j++) {
-                if (mv_sr) {
+                if (mv_test) {
                     m[j] = sr_bf16_prep(m[j]);
                     if constexpr (kDual) v[j] = sr_bf16_prep(v[j]);
                 }
@@ -1051,13 +1171,12 @@ __device__ __forceinline__ Inflight issue_at(const Desc &D, uint32_t flags, bool
 
 // The LaneK of the vector path: VGPR copies of the constants that mode reads with another uniform
 // operand. eps is read by T1, T2 and TD-CLM, the tanh constants by CLM and TD-CLM (tanh_pade).
-// The two-buffer modes with 16-bit state (T2, CLM) keep them as they are: there the extra VGPRs
-// would cost some of their kernels a wave of occupancy.
+// CLM with 16-bit state keeps the tanh constants as they are: there the extra VGPRs would cost
+// some of its kernels a wave of occupancy (T2's eps costs none of its kernels one).
 template <int MODE, int H>
 __device__ __forceinline__ LaneK lane_consts(const Args &a) {
     LaneK lk{a.eps, kPade};
-    if constexpr (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_TDCLM || (MODE == LV_BUFFER_T2 && H == 1))
-        lk.eps = in_vgpr(a.eps);
+    if constexpr (MODE == LV_BUFFER_T1 || MODE == LV_BUFFER_TDCLM || MODE == LV_BUFFER_T2) lk.eps = in_vgpr(a.eps);
     if constexpr (MODE == LV_BUFFER_TDCLM || (MODE == LV_BUFFER_DUAL && H == 1))
         lk.pade = PadeK{in_vgpr(kPade.hi), in_vgpr(kPade.p0), in_vgpr(kPade.q0)};
     return lk;
@@ -1100,6 +1219,8 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
         else decode_raw<PT, H>(cur.p, pin);
         // the thread's hash inputs at its first element (offsets wrap at 2^32 as (int32)idx does)
         const HashIn zb = hash_in(tv.sd, (uint32_t)e0 + tv.ibase);
+        const CsPair csp = cs_pair_vgpr(tv.cs);
+        uint32_t known_all = ~0u;  // the kKnown* facts that hold for all of the lane's elements
 #pragma unroll
         for (int j = 0; j < 4 * H; j++) {
             float vj = kDual ? v[j] : 0.0f;
@@ -1107,14 +1228,16 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
             if constexpr (PT == LV_DTYPE_F16) {
                 // fp16 params: the lane's values are quantised together below (2% faster on the
                 // fp16-container cfg4 step than element by element)
-                update_elem<MODE, PT, kTally, ST != LV_DTYPE_F32>(a, tv.k, lk, flags, tv.cs, tv.bs, pin[j], g[j], m[j], vj,
-                                                                   pout[j], mpout[j], ue, cnt);
+                uint32_t known;
+                update_elem<MODE, PT, kTally, ST != LV_DTYPE_F32>(a, tv.k, lk, flags, csp, tv.bs, pin[j], g[j], m[j], vj,
+                                                                   pout[j], mpout[j], ue, cnt, known);
+                known_all &= known;
             } else {
                 // quantised element by element: each hash then overlaps the next element's arithmetic
                 // (quantising the lane's bf16 values together after all of them measured 4% slower)
                 const uint32_t off = j < 4 ? (uint32_t)j : HS + (uint32_t)(j - 4);  // element offset from e0
                 const HashIn zj = {zb.m + off, zb.p + off, zb.v + off};
-                apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, tv.cs, tv.bs, pin[j], g[j], m[j], vj, pout[j],
+                apply_elem<MODE, PT, ST, kTally>(a, tv.k, lk, flags, zj, csp, tv.bs, pin[j], g[j], m[j], vj, pout[j],
                                                  mpout[j], ue, cnt);
             }
             if constexpr (kDual) v[j] = vj;
@@ -1123,7 +1246,11 @@ __device__ __forceinline__ void process_at(const Args &a, const Desc &D, const V
                 sp += (double)(pin[j] * pin[j]);
             }
         }
-        if constexpr (PT == LV_DTYPE_F16) quantize_lane<ST, PT, kDual, 4 * H, HS>(flags, zb, m, v, pout);
+        if constexpr (PT == LV_DTYPE_F16) {
+            const bool m_known = (known_all & kKnownM) && (a.ranges & kRangeM);
+            const bool v_known = !kDual || (known_all & kKnownV);
+            quantize_lane<ST, PT, kDual, 4 * H, HS>(flags, zb, m, v, pout, m_known && v_known);
+        }
         store_raw<PT, H, HS>(D.p, e0, pout);
         if (master) store_raw<LV_DTYPE_F32, H, HS>(D.mp, e0, mpout);
         store_raw<ST, H, HS>(D.m, e0, m);
@@ -1166,7 +1293,7 @@ __device__ __forceinline__ void scalar_range(const Args &a, const Desc &D, const
             float pin = master ? D.mp[i] : load1<PT>(D.p, i);
             float pout, mpout, ue;
             apply_elem<MODE, PT, ST, kCounting ? kTallyLane : kTallyNone>(
-                a, tv.k, LaneK{a.eps, kPade}, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), tv.cs, tv.bs, pin, g, m, v,
+                a, tv.k, LaneK{a.eps, kPade}, flags, hash_in(tv.sd, (uint32_t)i + tv.ibase), cs_pair(tv.cs), tv.bs, pin, g, m, v,
                 pout, mpout, ue, cnt);
             if (!inactive) {
                 store1<PT>(D.p, i, pout);

@@ -362,3 +362,43 @@ def test_reference_checkpoint_keeps_its_state_dtype(oracle_mod):
             assert_bitwise(st["exp_avg"], host.m[i], f"step {s} m[{i}]")
             assert_bitwise(st["exp_avg_sq"], host.v[i], f"step {s} v[{i}]")
             assert_bitwise(st["scratch"], host.sc[i], f"step {s} scratch[{i}]")
+
+
+def test_bucket_buffers_are_parts_of_one_allocation():
+    """A fused bucket's flat p, g, m, v (and master) are parts of ONE device allocation, each on a
+    2 MiB boundary in the order p|g|m|v|master, and each is a tensor with a storage of exactly its
+    own bytes: torch.save of the params writes the params only, and the allocation lives while
+    any part does (the params after the optimizer is gone)."""
+    _need_gpu()
+    from luminamoon_amd import LuminaV
+
+    sizes = (1000, 3000, 5, 70_001)
+    params = [nn.Parameter(torch.randn(n, device="cuda", dtype=torch.bfloat16) * 0.02) for n in sizes]
+    for p in params:
+        p.grad = torch.randn_like(p) * 1e-3
+    opt = LuminaV(params, lr=1e-3, buffer="T2", fuse_tensors=True, master_weights="full")
+    opt.step()
+    (b,) = opt._fused_buckets
+    n = sum(sizes)
+    flats = [b["flat_p"], b["flat_g"], b["flat_m"], b["flat_v"], b["flat_mp"]]
+    ptrs = [f.data_ptr() for f in flats]
+    align = 2 << 20
+    assert all(q % align == 0 for q in ptrs)
+    for f, q, q_next in zip(flats, ptrs, ptrs[1:]):
+        assert q_next - q == -(-f.numel() * f.element_size() // align) * align
+    for f in flats:
+        assert f.numel() == n
+        assert f.untyped_storage().nbytes() == n * f.element_size()
+        assert f.untyped_storage().data_ptr() == f.data_ptr()
+    buf = io.BytesIO()
+    torch.save([p.detach() for p in params], buf)
+    assert buf.tell() < n * 2 + 64 * 1024  # the bf16 params, not the whole allocation
+    before = [p.detach().clone() for p in params]
+    del opt, b, flats
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    junk = torch.full((1 << 22,), 7.0, device="cuda")  # reuse of freed memory would show here
+    torch.cuda.synchronize()
+    for p, q in zip(params, before):
+        assert torch.equal(p.detach(), q)
+    del junk

@@ -78,20 +78,20 @@ def issue_units(op: str) -> float:
 IEEE2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 2}
 FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
-    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 92.5,
+    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 92.0,
                               {**IEEE2, "v_sqrt_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 115.0,
+    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 107.0,
                                {**FAST2, "v_sqrt_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.0,
+    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 73.5,
                             {**IEEE2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 80.5,
+    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 76.0,
                              {**FAST2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 103.0,
+    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 101.0,
                                        {"v_rcp_f32": 3, "v_div_fixup_f32": 0, "v_mul_lo_u32": 4,
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
-    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 146.5,
+    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 146.0,
                      {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
-    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 111.0,
+    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 110.5,
                                {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_sqrt_f32": 1, "v_mul_lo_u32": 0}),
 }
 
