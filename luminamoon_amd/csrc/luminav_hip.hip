@@ -778,7 +778,6 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
         const Item &h = items[begin];
         int cls_end = begin + 1;
         while (cls_end < nitems && same_class(items[cls_end], h)) cls_end++;
-        const uint32_t unit_elems = kHalf * unit_halves(cfg->buffer, h.pt, h.st);
         const bool radial = bound == LV_BOUND_RADIAL && h.pass != kSingle;
         const bool table = !radial && L.table_slots > 0 && tab_buf && cls_end - begin > kMaxDesc;
         if (table) {
@@ -786,6 +785,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             Args args;
             fill_args_common(args, cfg, h, bound);
             args.step_rec = rec;
+            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags);
             std::vector<TDesc> &tab = *tab_buf;
             if (tab.size() < (size_t)n) tab.resize((size_t)n);
             uint64_t units = 0, slot = 0;
@@ -828,6 +828,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             Args args;
             fill_args_common(args, cfg, h, bound);
             args.step_rec = rec;
+            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags);
             args.ndesc = end - begin;
             uint64_t units = 0;
             for (int k = begin; k < end; k++) {

@@ -28,6 +28,7 @@ constexpr int unit_halves(int mode, int pt, int st) {
     (void)pt;
     return st == LV_DTYPE_F32 ? 1 : 2;
 }
+
 constexpr int kMaxDesc = 48;                 // tensors per inline launch (kernel argument table, < 4 KiB)
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
 constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
@@ -44,9 +45,9 @@ constexpr uint32_t kRadialPiece = 1u << 22;
 constexpr uint32_t kFoldChunk = 4096;  // fold blocks per full piece: kRadialPiece / kFoldChunk
 constexpr int kFoldBatch = 16;         // unit records a fold thread loads before adding them
 constexpr uint32_t kMaxChunks = kRadialPiece / kFoldChunk + kMaxDesc;  // chunks of one piece
-// A chunk's mask count (<= kFoldChunk units x 2048 elements) fits the u32 chunk sums; the
+// A chunk's mask count (<= kFoldChunk units x 4096 elements) fits the u32 chunk sums; the
 // sums over chunks run in u64.
-static_assert((uint64_t)kFoldChunk * 2048u <= 0xFFFFFFFFull, "chunk counts fit 32 bits");
+static_assert((uint64_t)kFoldChunk * 4096u <= 0xFFFFFFFFull, "chunk counts fit 32 bits");
 
 enum Pass : int { kSingle = 0, kFused = 1, kCount = 2, kApply = 3 };
 
@@ -60,6 +61,39 @@ enum Flags : uint32_t {
     kFRadial = 1u << 5,
     kFCoordinate = 1u << 6,
 };
+
+// Flag word of the specialised ("static") instantiation: the reference defaults (cautious in
+// the counting passes, stochastic rounding, weight decay, coordinate bound, no master, grad
+// dtype = param dtype, v clamp for fp16 params).
+constexpr uint32_t static_flags(int PT, int PASS) {
+    return (PASS != kSingle ? (uint32_t)kFCautious : 0u) | (uint32_t)kFSR | (uint32_t)kFWeightDecay |
+           (uint32_t)kFCoordinate | (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8);
+}
+
+// Sub-units per work unit (each 1024 * unit_halves elements) of the kernel for this mode, dtypes,
+// pass and flag word (the launch's word; the run-time-flag kernels have 1). A block of 2 issues
+// the loads of both sub-units before it computes the first, so the second's memory latency hides
+// behind the first's arithmetic. That pays where the step is VALU-bound and the kernel keeps full
+// occupancy with the extra registers: T1 with 16-bit state and 16-bit params, reference-default
+// flags (in one process, bf16-state cfg4 1.653 -> 1.612 ms, fp16 cfg4 1.996 -> 1.904 ms). With
+// 2 sub-units the T2 and TD-CLM 16-bit kernels and T1's other flag words need more registers than
+// 8 waves per SIMD leave, and spill.
+constexpr int unit_subs(int mode, int pt, int st, int pass, uint32_t flags) {
+    return (mode == LV_BUFFER_T1 && st != LV_DTYPE_F32 && pt != LV_DTYPE_F32 && flags == static_flags(pt, pass)) ? 2 : 1;
+}
+
+// Blocks per CU a unit kernel must fit (its launch bounds). Without a bound the compiler takes the
+// registers for a second sub-unit's loads out of occupancy (102 SGPRs: 7 waves per SIMD, where
+// the bound keeps 8 and 78 SGPRs): 1.635 against 1.612 ms for bf16-state cfg4.
+constexpr int unit_min_blocks(int mode, int pt, int st, int pass, uint32_t flags) {
+    return unit_subs(mode, pt, st, pass, flags) > 1 ? 8 : 1;
+}
+
+// Elements per work unit of a unit launch.
+constexpr uint32_t unit_elems(int mode, int pt, int st, int pass, uint32_t flags) {
+    return kHalf * (uint32_t)unit_halves(mode, pt, st) * (uint32_t)unit_subs(mode, pt, st, pass, flags);
+}
+constexpr uint32_t kMaxUnitElems = 4 * kHalf;
 
 // One tensor of a launch (80 bytes): in the kernel arguments (inline launches) or in the
 // workspace (table launches).
@@ -1412,7 +1446,43 @@ constexpr uint32_t lane_split(int H, uint32_t FL) {
     return (H == 2 && ((FL & kFDynamic) || (FL & kFMaster) || ((FL >> 8) & 3u) == LV_DTYPE_F32)) ? kHalf : 4u;
 }
 
-// Unit launch: each block updates exactly one work unit (1024 or 2048 elements, unit_halves) and
+// One sub-unit [ub, ub + 1024 * H) of a block that does not take the whole-unit vector path: the
+// partial last unit of an aligned tensor (whole groups of 4 as vectors), streams with no common
+// 16-byte alignment (element by element, coalesced across the wave), or inactive ranges
+// (`cover`: 0 none, 1 partly, 2 wholly; `first` the first range that ends after ub). cnt
+// accumulates the lane's own count.
+template <int MODE, int PT, int ST, int PASS, int H, uint32_t HS>
+__device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
+                                               uint64_t ub, int cover, uint32_t first, uint32_t &cnt, double &su,
+                                               double &sp) {
+    constexpr bool kCounting = (PASS == kFused || PASS == kCount);
+    if (!kCounting && cover == 2) return;  // wholly inactive: nothing to write
+    if (cover == 0 && tv.vec_ok) {
+        const uint64_t es = ub + (uint64_t)threadIdx.x * (HS == 4 ? 4u * H : 4u);
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const uint64_t e = es + (uint64_t)h * HS;
+            if (e + 4u <= tv.n) {
+                const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
+                process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
+            } else if (e < tv.n) {
+                scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
+            }
+        }
+    } else if (cover == 0) {
+#pragma unroll 1
+        for (uint32_t j = 0; j < 4u * H; j++) {
+            const uint64_t e = ub + (uint64_t)j * kThreads + threadIdx.x;
+            if (e < tv.n) scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, e + 1, cnt, su, sp);
+        }
+    } else if (cover != 2 || radial) {
+        const uint64_t eb = ub + (uint64_t)threadIdx.x * (4u * H);
+        const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
+        scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
+    }
+}
+
+// Unit launch: each block updates exactly one work unit (1024, 2048 or 4096 elements: unit_elems) and
 // exits.
 // The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
 // arithmetic of others without a software pipeline; on MI355X this launch shape streams HBM
@@ -1428,7 +1498,7 @@ constexpr uint32_t lane_split(int H, uint32_t FL) {
 // which case every option test folds at compile time and the per-element code is straight-line.
 // TABLE: the tensor table is in device memory (a.dtab) and the heads in a.ubegin.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL, bool TABLE>
-__global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
+__global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, FL)) unit_kernel(const Args a) {
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
     __shared__ BlockSums sh;
 
@@ -1456,8 +1526,10 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     uint32_t cnt = 0;
     double su = 0.0, sp = 0.0;  // radial: sum u_eff^2, sum p^2
     constexpr int H = unit_halves(MODE, PT, ST);
+    constexpr int S = unit_subs(MODE, PT, ST, PASS, FL);
     constexpr uint32_t HS = lane_split(H, FL);
-    constexpr uint64_t kUnit = (uint64_t)kHalf * H;
+    constexpr uint64_t kSub = (uint64_t)kHalf * H;  // elements per sub-unit
+    constexpr uint64_t kUnit = kSub * S;
     // units start at the tensor's first 16-byte aligned element (tv.head > 0: an unaligned view)
     const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit + tv.head;
     int cover = 0;
@@ -1469,7 +1541,10 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
     const bool vec = fast && ubase + kUnit <= tv.n;
     const uint64_t e0 = ubase + (uint64_t)threadIdx.x * (HS == 4 ? 4u * H : 4u);  // the first group
     if (vec) {
-        const Inflight f = issue_at<MODE, PT, ST, PASS, H, HS>(D, flags, radial, e0);
+        Inflight f[S];
+#pragma unroll
+        for (int sub = 0; sub < S; sub++)
+            f[sub] = issue_at<MODE, PT, ST, PASS, H, HS>(D, flags, radial, e0 + (uint64_t)sub * kSub);
         if constexpr (!TABLE) {
             __builtin_amdgcn_sched_barrier(0);  // every stream load is issued before the step's reads
             open_step<MODE, PASS, TABLE>(a, D, t, unit, tv);
@@ -1480,7 +1555,10 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
         // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
         __builtin_amdgcn_s_setprio(1);
-        process_at<MODE, PT, ST, PASS, H, true, HS>(a, D, tv, flags, radial, f, e0, cnt, su, sp);
+#pragma unroll
+        for (int sub = 0; sub < S; sub++)
+            process_at<MODE, PT, ST, PASS, H, true, HS>(a, D, tv, flags, radial, f[sub], e0 + (uint64_t)sub * kSub, cnt,
+                                                       su, sp);
     } else {
         if constexpr (!TABLE) {
             open_step<MODE, PASS, TABLE>(a, D, t, unit, tv);
@@ -1489,32 +1567,17 @@ __global__ void __launch_bounds__(kThreads) unit_kernel(const Args a) {
         // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
         // its elements still enter the radial norms.
         if (!kCounting && cover == 2 && !(tv.head && unit + 1 == tv.t_end)) return;
-        if (!kCounting && cover == 2) {
-            // only the head (below) is left to this block
-        } else if (fast) {
-            // the partial last unit of an aligned tensor: the same groups of 4
-#pragma unroll
-            for (int h = 0; h < H; h++) {
-                const uint64_t e = e0 + (uint64_t)h * HS;
-                if (e + 4u <= tv.n) {
-                    const Inflight f = issue_at<MODE, PT, ST, PASS, 1>(D, flags, radial, e);
-                    process_at<MODE, PT, ST, PASS, 1, false>(a, D, tv, flags, radial, f, e, cnt, su, sp);
-                } else if (e < tv.n) {
-                    scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, tv.n, cnt, su, sp);
-                }
-            }
-        } else if (cover == 0) {
-            // streams with no common 16-byte alignment: element by element, each wave reading 64
-            // consecutive elements of every stream per access
+        if constexpr (S == 1) {
+            subunit_nonvec<MODE, PT, ST, PASS, H, HS>(a, D, tv, flags, radial, ubase, cover, first, cnt, su, sp);
+        } else {
 #pragma unroll 1
-            for (uint32_t j = 0; j < 4u * H; j++) {
-                const uint64_t e = ubase + (uint64_t)j * kThreads + threadIdx.x;
-                if (e < tv.n) scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, e + 1, cnt, su, sp);
+            for (int sub = 0; sub < S; sub++) {
+                const uint64_t ub = ubase + (uint64_t)sub * kSub;  // this sub-unit's first element
+                if (ub >= tv.n) break;
+                uint32_t sfirst = 0;
+                const int scover = D.nskip ? inactive_cover(D, ub, ub + kSub < tv.n ? ub + kSub : tv.n, sfirst) : 0;
+                subunit_nonvec<MODE, PT, ST, PASS, H, HS>(a, D, tv, flags, radial, ub, scover, sfirst, cnt, su, sp);
             }
-        } else if (cover != 2 || radial) {
-            const uint64_t eb = ubase + (uint64_t)threadIdx.x * (4u * H);
-            const uint64_t ee = eb + 4u * H < tv.n ? eb + 4u * H : tv.n;
-            scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, eb, ee, cnt, su, sp, cover ? D.nskip : 0, first);
         }
     }
     // An unaligned view's head [0, tv.head) (its streams are aligned from element tv.head on): the
@@ -1668,13 +1731,6 @@ __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
 
 using KernelFn = void (*)(Args);
 
-// Flag word of the specialised ("static") instantiation: the reference defaults (cautious in
-// the counting passes, stochastic rounding, weight decay, coordinate bound, no master, grad
-// dtype = param dtype, v clamp for fp16 params).
-constexpr uint32_t static_flags(int PT, int PASS) {
-    return (PASS != kSingle ? (uint32_t)kFCautious : 0u) | (uint32_t)kFSR | (uint32_t)kFWeightDecay |
-           (uint32_t)kFCoordinate | (PT == LV_DTYPE_F16 ? (uint32_t)kFClampV : 0u) | ((uint32_t)PT << 8);
-}
 
 // The same defaults with bound_type="radial" (the radial passes never run SINGLE).
 constexpr uint32_t radial_flags(int PT) {

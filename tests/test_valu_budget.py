@@ -6,8 +6,8 @@ path over a whole unit (from the `s_setprio 1` that follows the unit's loads to 
 reduction's `s_barrier`) with every wave-uniform guard on its fast side: the cheapest path
 through the control-flow graph, where a guard's slow side is a detour that adds work and an
 exec-mask skip (`s_cbranch_execz`) is never taken (some lanes run its body). The path's VALU
-instructions per element (4 * H per lane) are what `SQ_INSTS_VALU` per wave counts per element,
-less the unit's prologue and reduction.
+instructions per element (4 * H * S per lane: S sub-units of 4 * H elements each) are what
+`SQ_INSTS_VALU` per wave counts per element, less the unit's prologue and reduction.
 
 Each kernel's cost must stay within its budget, in issue units: every VALU instruction priced
 by its measured issue time on gfx950 (a v_add_u32 is one unit; most 3-operand and bit ops about
@@ -78,18 +78,18 @@ def issue_units(op: str) -> float:
 IEEE2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 2}
 FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
-    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 92.0,
+    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 93.0,
                               {**IEEE2, "v_sqrt_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
     "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 107.0,
                                {**FAST2, "v_sqrt_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 73.5,
+    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.0,
                             {**IEEE2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 76.0,
+    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 16, 76.0,
                              {**FAST2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 8, 101.0,
+    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 16, 101.0,
                                        {"v_rcp_f32": 3, "v_div_fixup_f32": 0, "v_mul_lo_u32": 4,
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
-    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 146.0,
+    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 147.0,
                      {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
     "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 110.5,
                                {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_sqrt_f32": 1, "v_mul_lo_u32": 0}),
