@@ -39,8 +39,9 @@ def _stepper():
 
 
 def _ranges(n: int) -> List[Tuple[int, int]]:
-    """Sorted, disjoint ranges exercising every unit-coverage case for 1024- and 2048-element
-    units: start of tensor, straddling, whole units, single elements, several in one unit, tail."""
+    """Sorted, disjoint ranges exercising every unit-coverage case for 1024-, 2048- and
+    4096-element units (the last as two 2048-element sub-units): start of tensor, straddling a
+    unit or a sub-unit boundary, whole units, single elements, several in one unit, tail."""
     rs = [(0, 5), (1000, 1030), (2048, 5120), (6000, 6001), (6003, 6004), (6010, 6100), (9000, 12288),
           (20000, 20001), (n - 700, n)]
     return [(b, min(e, n)) for b, e in rs if b < n and b < min(e, n)]
@@ -78,6 +79,8 @@ CASES = [
     dict(name="T1 bf16 no cautious (single pass)", pdt="bf16", sdt="f32", kw=dict(buffer="T1", cautious=False)),
     dict(name="TD-CLM f16 master full", pdt="f16", sdt="f32", kw=dict(buffer=1, master_weights="full")),
     dict(name="T2 bf16 bf16-state no SR", pdt="bf16", sdt="bf16", kw=dict(buffer="T2", stochastic_rounding=False)),
+    dict(name="T1 bf16 bf16-state cautious (two sub-units)", pdt="bf16", sdt="bf16", kw=dict(buffer="T1")),
+    dict(name="T1 f16 fp16-container cautious (two sub-units)", pdt="f16", sdt="f16", kw=dict(buffer="T1")),
     dict(name="radial T2 bf16 cautious", pdt="bf16", sdt="f32", kw=dict(buffer="T2", bound_type="radial"), radial=True),
     dict(name="radial CLM f32 no cautious", pdt="f32", sdt="f32", kw=dict(buffer=2, bound_type="radial", cautious=False),
          radial=True),

@@ -113,8 +113,9 @@ def assert_workspace_zero(stepper, label):
     (1000, 2, "bf16", "f32", {"master_weights": "full"}),
     (1000, 2, "f32", "f32", {"cautious": False}),
     (1000, "T1", "bf16", "bf16", {"state_precision": "param", "fused_single_pass": False}),
+    (1000, "T1", "f16", "f16", {"state_precision": "param"}),
 ], ids=["T2-bf16-1000", "TDCLM-f32-2000", "TDCLM-f32-5000", "CLM-master-1000", "CLM-nocautious-1000",
-        "T1-bf16state-twopass-1000"])
+        "T1-bf16state-twopass-1000", "T1-f16-fp16container-1000"])
 def test_table_launches_thousands_of_tensors(oracle_mod, count, buffer, pdt, sdt, extra):
     """More tensors than the kernel-argument table holds: every class is ONE table launch (pair)
     whatever its tensor count, its descriptors in a device table and every group-th tensor's first
