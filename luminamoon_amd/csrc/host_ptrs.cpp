@@ -8,6 +8,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <exception>
 
 #include <torch/csrc/autograd/python_variable.h>
 
@@ -21,13 +22,18 @@ PyObject *same_ptrs(PyObject *, PyObject *args) {
     const Py_ssize_t n = PyList_GET_SIZE(tensors);
     if (PyBytes_GET_SIZE(recorded) != n * (Py_ssize_t)sizeof(uint64_t)) Py_RETURN_FALSE;
     const char *want = PyBytes_AS_STRING(recorded);
-    for (Py_ssize_t i = 0; i < n; i++) {
-        PyObject *o = PyList_GET_ITEM(tensors, i);
-        if (!THPVariable_Check(o)) Py_RETURN_FALSE;
-        const at::Tensor &t = THPVariable_Unpack(o);
-        uint64_t w;
-        std::memcpy(&w, want + i * sizeof(uint64_t), sizeof w);
-        if ((uint64_t)(uintptr_t)t.data_ptr() != w) Py_RETURN_FALSE;
+    try {
+        for (Py_ssize_t i = 0; i < n; i++) {
+            PyObject *o = PyList_GET_ITEM(tensors, i);
+            if (!THPVariable_Check(o)) Py_RETURN_FALSE;
+            const at::Tensor &t = THPVariable_Unpack(o);
+            uint64_t w;
+            std::memcpy(&w, want + i * sizeof(uint64_t), sizeof w);
+            if ((uint64_t)(uintptr_t)t.data_ptr() != w) Py_RETURN_FALSE;
+        }
+    } catch (const std::exception &e) {  // a tensor without storage: data_ptr raises, as in Python
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
     }
     Py_RETURN_TRUE;
 }
@@ -40,15 +46,21 @@ PyObject *ptrs(PyObject *, PyObject *args) {
     PyObject *out = PyBytes_FromStringAndSize(nullptr, n * (Py_ssize_t)sizeof(uint64_t));
     if (!out) return nullptr;
     char *dst = PyBytes_AS_STRING(out);
-    for (Py_ssize_t i = 0; i < n; i++) {
-        PyObject *o = PyList_GET_ITEM(tensors, i);
-        if (!THPVariable_Check(o)) {
-            Py_DECREF(out);
-            PyErr_SetString(PyExc_TypeError, "ptrs: a list of tensors is expected");
-            return nullptr;
+    try {
+        for (Py_ssize_t i = 0; i < n; i++) {
+            PyObject *o = PyList_GET_ITEM(tensors, i);
+            if (!THPVariable_Check(o)) {
+                Py_DECREF(out);
+                PyErr_SetString(PyExc_TypeError, "ptrs: a list of tensors is expected");
+                return nullptr;
+            }
+            const uint64_t p = (uint64_t)(uintptr_t)THPVariable_Unpack(o).data_ptr();
+            std::memcpy(dst + i * sizeof(uint64_t), &p, sizeof p);
         }
-        const uint64_t p = (uint64_t)(uintptr_t)THPVariable_Unpack(o).data_ptr();
-        std::memcpy(dst + i * sizeof(uint64_t), &p, sizeof p);
+    } catch (const std::exception &e) {
+        Py_DECREF(out);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
     }
     return out;
 }

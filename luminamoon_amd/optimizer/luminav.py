@@ -144,20 +144,21 @@ def _bucket_buffers(device: torch.device, specs: List[Tuple[str, torch.dtype, in
     freshly started device), separately allocated buffers ran the 6.7e9-element T2 step 4-7%
     slower than the same buffers allocated later in the process. Packed in the order p|g|m|v, in
     the same fresh memory, it ran within 2.5% of the later allocations; the order m|p|v|g of the
-    same pack ran 5.5% slower than p|g|m|v. Elsewhere the layout is neutral."""
+    same pack ran 5.5% slower than p|g|m|v. Elsewhere the layout is neutral.
+    The parts' storages are not blocks of torch's caching allocator: `record_stream` on a part does
+    not reach the allocation, which the allocator may reuse once the last part is freed (code that
+    uses bucket tensors on a side stream keeps them alive until that stream is done with them)."""
     if device.type != "cuda":
         return {name: torch.empty(n, dtype=dt, device=device) for name, dt, n in specs}
     offs, off = [], 0
     for _, dt, n in specs:
         offs.append(off)
-        nbytes = n * torch.empty((), dtype=dt).element_size()
-        off += (nbytes + _ARENA_ALIGN - 1) // _ARENA_ALIGN * _ARENA_ALIGN
+        off += (n * dt.itemsize + _ARENA_ALIGN - 1) // _ARENA_ALIGN * _ARENA_ALIGN
     arena = torch.empty(off + _ARENA_ALIGN, dtype=torch.uint8, device=device)
     base = (-arena.data_ptr()) % _ARENA_ALIGN
     out: Dict[str, torch.Tensor] = {}
     for (name, dt, n), o in zip(specs, offs):
-        nbytes = n * torch.empty((), dtype=dt).element_size()
-        part = torch.as_tensor(_ArenaPart(arena, base + o, nbytes), device=device)
+        part = torch.as_tensor(_ArenaPart(arena, base + o, n * dt.itemsize), device=device)
         out[name] = part.view(dt)
     return out
 

@@ -313,3 +313,28 @@ def test_reference_checkpoint_state_precision_is_inferred():
     opt.load_state_dict(ckpt(opt, torch.bfloat16, keep_key=True))  # this build's own checkpoint
     assert opt.param_groups[0]["state_precision"] == "fp32"
     assert all(opt.state[p][k].dtype == torch.float32 for p in ps for k in ("exp_avg", "exp_avg_sq"))
+
+
+def test_plan_pointer_helpers_agree_with_python():
+    """The step plans' data-pointer checks (the C module _lv_host when built, else Python maps)
+    record where each tensor's data is and notice any move; an entry that is not a tensor (a grad
+    of None) never matches, and a tensor without storage raises as Tensor.data_ptr does."""
+    import luminamoon_amd.optimizer.luminav as L
+    from luminamoon_amd.optimizer import hip_backend
+
+    ts = [torch.zeros(3), torch.zeros(5, dtype=torch.bfloat16), torch.zeros(2, 2)[1]]
+    rec = L._ptr_record(ts)
+    assert L._same_ptrs(ts, rec)
+    assert L._same_ptrs(list(ts), L._pack_ptrs([t.data_ptr() for t in ts]))
+    moved = [ts[0], ts[1].clone(), ts[2]]
+    assert not L._same_ptrs(moved, rec)
+    assert not L._same_ptrs(ts[:2], rec)  # a different count
+    assert not L._same_ptrs([ts[0], None, ts[2]], rec)
+    ts[0].data = ts[0].data.clone()  # storage moved in place, same tensor object
+    assert not L._same_ptrs(ts, rec)
+    host = hip_backend.load_host_ext()
+    if host is not None:
+        with pytest.raises(RuntimeError):
+            host.ptrs([torch.zeros(4).to_sparse()])
+        with pytest.raises(TypeError):
+            host.ptrs([torch.zeros(1), 3])
