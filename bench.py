@@ -219,15 +219,46 @@ def build_stream_probe() -> str:
     return PROBE_LIB
 
 
-def stream_probe_fn():
-    """lv_stream_probe(param_bytes, state_bytes, nstate, p, g, m, v, n, stream) -> 0 or 1."""
+def stream_probe_lib():
+    """The stream probe library with its signatures declared."""
     import ctypes
 
-    fn = ctypes.CDLL(build_stream_probe()).lv_stream_probe
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    lib = ctypes.CDLL(build_stream_probe())
+    args = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    lib.lv_stream_probe.restype = ctypes.c_int
+    lib.lv_stream_probe.argtypes = args
+    lib.lv_stream_probe_shape.restype = ctypes.c_int
+    lib.lv_stream_probe_shape.argtypes = [ctypes.c_int] + args
+    lib.lv_stream_probe_shapes.restype = ctypes.c_int
+    lib.lv_stream_probe_shapes.argtypes = []
+    lib.lv_stream_probe_shape_info.restype = ctypes.c_int
+    lib.lv_stream_probe_shape_info.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+    return lib
+
+
+def stream_probe_fn():
+    """lv_stream_probe(param_bytes, state_bytes, nstate, p, g, m, v, n, stream) -> 0 or 1."""
+    return stream_probe_lib().lv_stream_probe
+
+
+def stream_shape_fn(lib, shape: int):
+    """lv_stream_probe_shape bound to one shape: the signature of lv_stream_probe."""
+    def fn(*a):
+        return lib.lv_stream_probe_shape(shape, *a)
     return fn
+
+
+def stream_shape_desc(lib, shape: int) -> str:
+    import ctypes
+
+    info = (ctypes.c_int * 5)()
+    if lib.lv_stream_probe_shape_info(shape, info) != 0:
+        raise RuntimeError(f"unknown stream shape {shape}")
+    t, g, nt, persist, xcd = list(info)
+    return (f"{t} threads x {4 * g} elements ({g} group{'s' if g > 1 else ''} of 4 per thread), "
+            f"{'non-temporal' if nt else 'plain'} accesses{', persistent grid (8 blocks per CU)' if persist else ''}"
+            f"{', XCD-contiguous' if xcd else ''}")
 
 
 def check_stream_probe(torch, fn, pb: int, sb: int, ns: int) -> None:
@@ -258,6 +289,42 @@ def check_stream_probe(torch, fn, pb: int, sb: int, ns: int) -> None:
         for k in ("p", "g", "m", "v"):
             if not np.array_equal(dev[k].cpu().numpy().view(np.uint32), exp[k]):
                 raise RuntimeError(f"stream probe check failed: {k} (pb={pb} sb={sb} ns={ns} n={n})")
+
+
+def stream_shapes(torch, p, g, m, v, reps: int) -> list:
+    """--stream-shapes: the bare stream of --stream-floor in each of stream_probe.hip's access
+    shapes (threads per block, groups per thread, cache policy, persistent grid, XCD mapping) on the
+    step's own buffers, each checked first, then `reps` launches back to back between HIP events.
+    Shape 0 is --stream-floor's kernel; shape 7 adds the step's XCD-contiguous block mapping."""
+    lib = stream_probe_lib()
+    pb, sb, ns, n = p.element_size(), m.element_size(), 1 if v is None else 2, p.numel()
+    stream = torch.cuda.current_stream()
+    bpp = 3 * pb + 2 * sb * ns
+    out = []
+    for shape in range(lib.lv_stream_probe_shapes()):
+        fn = stream_shape_fn(lib, shape)
+        check_stream_probe(torch, fn, pb, sb, ns)
+
+        def launch():
+            rc = fn(pb, sb, ns, p.data_ptr(), g.data_ptr(), m.data_ptr(), None if v is None else v.data_ptr(), n,
+                    stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"lv_stream_probe_shape({shape}) returned {rc}")
+
+        for _ in range(3):
+            launch()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch()
+        b.record(stream)
+        b.synchronize()
+        ms = a.elapsed_time(b) / reps
+        gbs = n * bpp / (ms / 1e3) / 1e9
+        out.append({"shape": shape, "desc": stream_shape_desc(lib, shape), "ms": ms, "gb_per_s": gbs,
+                    "frac": gbs / HBM_PEAK_GBS})
+        log(f"stream shape {shape} ({out[-1]['desc']}): {ms:.4f} ms, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}%)")
+    return out
 
 
 def stream_floor(torch, p, g, m, v, reps: int) -> dict:
@@ -495,12 +562,13 @@ def cpu_threads() -> dict:
             "limited_by": binding, "limits": limits}
 
 
-def timed_pass(torch, args, wl: dict, sizes, pdt, with_floor: bool):
+def timed_pass(torch, args, wl: dict, sizes, pdt, with_floor: bool, with_shapes: bool = False):
     """Allocates the workload (inputs generated on the GPU, the drop-in LuminaV over them: configs
     3-5 as their one bucket), takes the warm-up steps, then times args.steps steps back to back
     between ONE pair of HIP events on the launch stream (per-step event records would add host
     time to every step: about 6 us, a quarter of cfg2's). Frees everything before returning
-    (ms_avg, ms_wall, the per-step spread) and the stream floor when asked for."""
+    (ms_avg, ms_wall, the per-step spread) and the stream floor (with_floor) or the floor in every
+    access shape (with_shapes) when asked for."""
     from luminamoon_amd import LuminaV
 
     t0 = time.perf_counter()
@@ -554,9 +622,13 @@ def timed_pass(torch, args, wl: dict, sizes, pdt, with_floor: bool):
             raise RuntimeError(f"non-finite scratch {sc}")
     log(f"scratch of the last tensor after {args.warmup + args.steps + len(spread)} steps: {sc}")
     floor = None
-    if with_floor:
+    if with_floor or with_shapes:
         if len(params) != 1 or args.master != "none":
-            log("--stream-floor: one-tensor configs without master weights only; skipped")
+            log("--stream-floor / --stream-shapes: one-tensor configs without master weights only; skipped")
+        elif with_shapes:
+            st = opt.state[params[0]]
+            floor = stream_shapes(torch, params[0].data, params[0].grad, st["exp_avg"], st.get("exp_avg_sq"),
+                                  reps=args.steps)
         else:
             st = opt.state[params[0]]
             floor = stream_floor(torch, params[0].data, params[0].grad, st["exp_avg"], st.get("exp_avg_sq"),
@@ -593,6 +665,9 @@ def main() -> int:
     ap.add_argument("--stream-floor", action="store_true",
                     help="after the timed steps, time a bare kernel that streams the step's own buffers "
                          "(one-tensor configs without master weights)")
+    ap.add_argument("--stream-shapes", action="store_true",
+                    help="like --stream-floor, in each access shape of stream_probe.hip (threads per block, "
+                         "elements per thread, cache policy, persistent grid, XCD mapping)")
     ap.add_argument("--offset-ab", type=int, default=None, metavar="K",
                     help="instead of a config: a T2 bf16/fp32-state tensor stepped as a view K elements into "
                          "its buffers against the aligned view of the same buffers (prints its own JSON line)")
@@ -650,7 +725,8 @@ def main() -> int:
     # allocation, which measured 1.5% slow there instead. The line also reports the same workload
     # allocated again after a 200 GiB reserve/release (a placement away from those pages), unless
     # --no-reserve.
-    first, floor = timed_pass(torch, args, wl, sizes, pdt, with_floor=args.stream_floor)
+    first, floor = timed_pass(torch, args, wl, sizes, pdt, with_floor=args.stream_floor,
+                              with_shapes=args.stream_shapes)
     ms_avg, ms_wall = first["ms_avg"], first["ms_wall"]
     params_per_s = n / (ms_wall / 1e3)
     bytes_launch = n * wl["bytes_per_param"]
@@ -727,7 +803,7 @@ def main() -> int:
     }
     out["placement"] = placement
     if floor is not None:
-        out["stream_floor"] = floor
+        out["stream_shapes" if args.stream_shapes else "stream_floor"] = floor
     print(json.dumps(out), flush=True)
     return 0
 

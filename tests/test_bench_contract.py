@@ -147,6 +147,47 @@ def test_stream_probe_rejects_invalid_arguments_before_any_launch():
         assert fn(c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"], None) == 1, change
 
 
+def test_stream_probe_shapes_reject_invalid_arguments_before_any_launch():
+    """lv_stream_probe_shape makes lv_stream_probe's checks in every shape and rejects unknown
+    shapes; lv_stream_probe_shape_info describes each shape, shape 0 being the step's own."""
+    import ctypes
+
+    _probe_lib()
+    lib = bench.stream_probe_lib()
+    count = lib.lv_stream_probe_shapes()
+    assert count >= 2
+    info = (ctypes.c_int * 5)()
+    assert lib.lv_stream_probe_shape_info(0, info) == 0 and list(info) == [256, 1, 1, 0, 0]
+    for shape in range(count):
+        assert lib.lv_stream_probe_shape_info(shape, info) == 0
+        assert info[0] in (64, 128, 256, 1024) and info[1] in (1, 2, 4) and all(x in (0, 1) for x in info[2:])
+        assert bench.stream_shape_desc(lib, shape)
+    assert lib.lv_stream_probe_shape_info(count, info) == 1
+    assert lib.lv_stream_probe_shape_info(-1, info) == 1
+    assert lib.lv_stream_probe_shape_info(0, None) == 1
+    a = 1 << 20
+    ok = dict(pb=2, sb=4, ns=2, p=a, g=a, m=a, v=a, n=4096)
+    bad = [dict(pb=3), dict(sb=8), dict(ns=3), dict(p=None), dict(v=None), dict(n=0), dict(n=4098),
+           dict(p=a + 8), dict(n=(1 << 24) * 1024)]
+    for shape in range(count):
+        fn = bench.stream_shape_fn(lib, shape)
+        for change in bad:
+            c = {**ok, **change}
+            assert fn(c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"], None) == 1, (shape, change)
+    # a one-wave XCD-contiguous grid at lv_stream_probe's largest n would be 2^32 threads
+    wave_xcd = [s for s in range(count)
+                if lib.lv_stream_probe_shape_info(s, info) == 0 and info[0] == 64 and info[1] == 1 and info[4]]
+    assert wave_xcd
+    for shape in wave_xcd:
+        c = {**ok, "n": ((1 << 24) - 1) * 1024}
+        assert bench.stream_shape_fn(lib, shape)(c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"],
+                                                 None) == 1
+    for shape in (-1, count):
+        c = ok
+        assert lib.lv_stream_probe_shape(shape, c["pb"], c["sb"], c["ns"], c["p"], c["g"], c["m"], c["v"], c["n"],
+                                         None) == 1
+
+
 def test_every_config_has_default_steps_and_warmup():
     """Each workload times about half a second of steps or more by default (cfg2's ~20 us step
     needs thousands for the bracketing synchronizations to vanish) and warms up first."""
