@@ -91,7 +91,7 @@ KERNELS = {
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
     "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 147.0,
                      {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
-    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 110.5,
+    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 99.0,
                                {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_sqrt_f32": 1, "v_mul_lo_u32": 0}),
 }
 
