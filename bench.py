@@ -85,7 +85,7 @@ PMC_TRAFFIC = {
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
                                                 fetch_kib=965684.1562, write_kib=1451873.4062, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
-                                                fetch_kib=20713.6250, write_kib=27582.4219, **_PROBE),
+                                                fetch_kib=20746.9141, write_kib=27580.0938, **_PROBE),
 }
 
 # Untimed steps before the timed ones unless --warmup is given. After the inputs are generated the
