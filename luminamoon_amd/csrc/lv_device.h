@@ -1586,8 +1586,11 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
             if (tv.skip) return;
         }
         // Waves whose loads are in flight outrank freshly started ones, so a SIMD finishes (and
-        // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput.
-        __builtin_amdgcn_s_setprio(1);
+        // stores) the units it holds before new blocks add loads: ~0.5% more HBM throughput. The
+        // two-sub-unit kernels already hold their next loads in flight and keep the default
+        // priority (fp16 cfg4 0.995x and 0.991x, bf16-state cfg4 0.9995x, in one process each); the
+        // explicit priority 0 costs one scalar instruction and marks the same point in the code.
+        __builtin_amdgcn_s_setprio(S == 1 ? 1 : 0);
 #pragma unroll
         for (int sub = 0; sub < S; sub++)
             process_at<MODE, PT, ST, PASS, H, true, HS>(a, D, tv, flags, radial, f[sub], e0 + (uint64_t)sub * kSub, cnt,

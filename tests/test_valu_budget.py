@@ -2,7 +2,7 @@
 
 `tests/gpu_checks/valu_budget.hip` instantiates the unit kernel of each bench workload; hipcc
 compiles it to assembly with the library's own flags. The hot path of a kernel is its vector
-path over a whole unit (from the `s_setprio 1` that follows the unit's loads to the block
+path over a whole unit (from the `s_setprio` that follows the unit's loads to the block
 reduction's `s_barrier`) with every wave-uniform guard on its fast side: the cheapest path
 through the control-flow graph, where a guard's slow side is a detour that adds work and an
 exec-mask skip (`s_cbranch_execz`) is never taken (some lanes run its body). The path's VALU
@@ -217,10 +217,10 @@ def _successors(blocks, k, flags):
 
 def hot_path(path: str, name: str) -> list[str]:
     """Instructions of the cheapest path (in VALU instructions) from the block holding
-    `s_setprio 1` to the first block holding `s_barrier`."""
+    `s_setprio` (1, or 0 in the two-sub-unit kernels) to the first block holding `s_barrier`."""
     lines = open(path).read().split("\n")
     blocks = _blocks(lines, name)
-    start = next(n for n, (_, ins) in enumerate(blocks) if any("s_setprio 1" in x for x in ins))
+    start = next(n for n, (_, ins) in enumerate(blocks) if any(x.startswith("s_setprio") for x in ins))
     cost = [sum(1 for x in ins if x.startswith("v_")) for _, ins in blocks]
     # Dijkstra over (block, known flags)
     s0 = (start, ())
@@ -251,7 +251,7 @@ def hot_path(path: str, name: str) -> list[str]:
     for n in reversed(order):
         ins = blocks[n][1]
         if n == start:
-            ins = ins[next(i for i, x in enumerate(ins) if "s_setprio 1" in x):]
+            ins = ins[next(i for i, x in enumerate(ins) if x.startswith("s_setprio")):]
         if n == end[0]:
             ins = ins[:next(i for i, x in enumerate(ins) if x.startswith("s_barrier"))]
         out.extend(ins)
