@@ -315,6 +315,69 @@ def test_reference_checkpoint_state_precision_is_inferred():
     assert all(opt.state[p][k].dtype == torch.float32 for p in ps for k in ("exp_avg", "exp_avg_sq"))
 
 
+def test_steady_plan_check_and_counter_advance():
+    """_lv_host.steady is True exactly while the params, their grad objects and every param, grad
+    and state tensor's data are the recorded ones; advance returns the counters plus one and
+    stores each in its state dict, bypassing a dict subclass's __setitem__ as the Python path does."""
+    import luminamoon_amd.optimizer.luminav as L
+    from luminamoon_amd.optimizer import hip_backend
+
+    host = hip_backend.load_host_ext()
+    if host is None or not hasattr(host, "steady"):
+        pytest.skip("_lv_host.so is not built")
+    params = [torch.nn.Parameter(torch.zeros(n)) for n in (3, 4, 5)]
+    for p in params:
+        p.grad = torch.ones_like(p)
+    states = [torch.zeros(3), torch.zeros(4), torch.zeros(5)]
+
+    def rec():
+        grads = [p.grad for p in params]
+        return (L._pack_ptrs(list(map(id, params))), L._ptr_record(params), L._pack_ptrs(list(map(id, grads))),
+                L._ptr_record(grads), L._ptr_record(states))
+
+    pid, pp, gid, gp, sp = rec()
+    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    assert not host.steady(params[:2], pid, pp, gid, gp, states, sp)  # records of another length
+    assert not host.steady([params[1], params[0], params[2]], pid, pp, gid, gp, states, sp)
+    g0 = params[0].grad
+    params[0].grad = torch.ones_like(params[0])  # a new grad object
+    assert not host.steady(params, pid, pp, gid, gp, states, sp)
+    params[0].grad = g0
+    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    params[1].grad = None
+    assert not host.steady(params, pid, pp, gid, gp, states, sp)
+    params[1].grad = torch.ones_like(params[1])
+    pid, pp, gid, gp, sp = rec()
+    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    params[2].grad.data = params[2].grad.data.clone()  # the same grad object, its data moved
+    assert not host.steady(params, pid, pp, gid, gp, states, sp)
+    pid, pp, gid, gp, sp = rec()
+    params[2].data = params[2].data.clone()  # a param's data moved
+    assert not host.steady(params, pid, pp, gid, gp, states, sp)
+    pid, pp, gid, gp, sp = rec()
+    states[1].set_(states[1].clone())  # a state tensor's data moved
+    assert not host.steady(params, pid, pp, gid, gp, states, sp)
+    pid, pp, gid, gp, sp = rec()
+    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    with pytest.raises(TypeError):
+        host.steady(tuple(params), pid, pp, gid, gp, states, sp)
+
+    class Guarded(dict):
+        def __setitem__(self, k, v):
+            raise AssertionError("the counters bypass __setitem__, as dict.__setitem__ does")
+
+    ds = [{"step": 7}, Guarded(step=2**40), {}]
+    out = host.advance(ds, [7, 2**40, 0], "step")
+    assert out == [8, 2**40 + 1, 1] and [d["step"] for d in ds] == out
+    assert all(a is d["step"] for a, d in zip(out, ds))
+    with pytest.raises(ValueError):
+        host.advance(ds, [1, 2], "step")
+    with pytest.raises(TypeError):
+        host.advance([{}, 3], [1, 2], "step")
+    with pytest.raises(TypeError):
+        host.advance([{}], ["x"], "step")
+
+
 def test_plan_pointer_helpers_agree_with_python():
     """The step plans' data-pointer checks (the C module _lv_host when built, else Python maps)
     record where each tensor's data is and notice any move; an entry that is not a tensor (a grad
