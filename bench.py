@@ -75,13 +75,13 @@ PMC_TRAFFIC = {
     (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
                                                 fetch_kib=39495825.9688, write_kib=66010492.8750, **_PROBE),
     (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=26327836.3750, write_kib=39585747.7500, **_PROBE),
+                                                 fetch_kib=26327611.5625, write_kib=39585768.0000, **_PROBE),
     (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
                                                 fetch_kib=3726628.2812, write_kib=5614386.1875, **_PROBE),
     (4, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 1, 1, 331u, false>",
-                                                 fetch_kib=2793143.3125, write_kib=3730813.0938, **_PROBE),
+                                                 fetch_kib=2793180.5625, write_kib=3730814.8438, **_PROBE),
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
-                                                    fetch_kib=2793118.7812, write_kib=3730811.9688, **_PROBE),
+                                                    fetch_kib=2793131.0000, write_kib=3730812.5938, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
                                                 fetch_kib=965684.1562, write_kib=1451873.4062, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",

@@ -175,7 +175,7 @@ def test_tied_weights_and_grad_none_isolation_in_bucket():
     assert torch.count_nonzero(m_frozen) == 0
 
 
-def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
+def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod, monkeypatch):
     """Unfused groups reuse their packed descriptors while only grads and step counters change.
     Every way the plan can go stale is driven here -- grads updated in place, new grad tensors,
     a param losing and regaining its grad, param storage replaced, load_state_dict, a changed
@@ -199,6 +199,19 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
         return ok
 
     opt._run_unfused_plan = spy
+    # the one-call check of a steady step (_lv_host.steady), when built: count its verdicts
+    import luminamoon_amd.optimizer.luminav as L
+
+    steady_real = L._steady
+    verdicts = {True: 0, False: 0}
+
+    def steady_spy(*a):
+        ok = steady_real(*a)
+        verdicts[bool(ok)] += 1
+        return ok
+
+    if steady_real is not None:
+        monkeypatch.setattr(L, "_steady", steady_spy)
     host_steps = [0] * len(sizes)
     kept = []
 
@@ -296,6 +309,12 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod):
     sc2.data = sc2.data.clone()
     run(28, "new", False)
     run(29, "new", True)
+    # steady steps: the same grad objects updated in place, checked and counted in one C call each
+    hits = verdicts[True]
+    for s in (30, 31, 32):
+        run(s, "inplace", True)
+    if steady_real is not None:
+        assert verdicts[True] - hits == 3, verdicts
 
 
 def test_unfused_duplicate_param_raises_like_the_native_seam():
