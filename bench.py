@@ -96,8 +96,8 @@ DEFAULT_WARMUP = {5: 3, 4: 25, 3: 100, 2: 100}
 
 # Timed steps unless --steps is given: about half a second of step time or more, so the two
 # synchronizations and the events that bracket the timed region stay below 0.1% of it (cfg2's
-# step is ~20 us: 20 steps read 28 us per step, 2,000 read the loop's 20.7).
-DEFAULT_STEPS = {5: 20, 4: 200, 3: 1000, 2: 20000}
+# step is ~15 us; with a ~20 us step, 20 steps read 28 us per step and 2,000 the loop's 20.7).
+DEFAULT_STEPS = {5: 20, 4: 200, 3: 1000, 2: 30000}
 
 
 def workload(config: int, bound: str = "coordinate", state: str = "fp32", master: str = "none",

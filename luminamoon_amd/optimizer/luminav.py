@@ -1401,8 +1401,8 @@ class LuminaV(Optimizer):
         params = group["params"]
         prep = plan["prep"]
         # The common case in one C call: the same params, each with the same grad object, and every
-        # param, grad and state tensor where it was (cfg2's 64 tensors: 11.2 of an 18.2 us step
-        # were these checks and the counters in Python).
+        # param, grad and state tensor where it was (cfg2's 64 tensors: in Python these checks and
+        # the counters took 11.2 us of an 18.2 us step; with these two C calls the step is 14.6 us).
         if not (_steady is not None and plan["all_active"] and not plan["dead"][0] and type(params) is list
                 and _steady(params, plan["pid_rec"], plan["pptrs"], plan["gid_rec"], plan["gptr_rec"],
                             plan["stensors"], plan["sptrs"])):

@@ -189,9 +189,9 @@ def test_stream_probe_shapes_reject_invalid_arguments_before_any_launch():
 
 
 def test_every_config_has_default_steps_and_warmup():
-    """Each workload times about half a second of steps or more by default (cfg2's ~20 us step
+    """Each workload times about half a second of steps or more by default (cfg2's ~15 us step
     needs thousands for the bracketing synchronizations to vanish) and warms up first."""
-    step_ms = {5: 23.1, 4: 2.13, 3: 0.57, 2: 0.021}
+    step_ms = {5: 23.1, 4: 2.13, 3: 0.57, 2: 0.0146}
     for c in bench.WORKLOADS:
         assert bench.DEFAULT_STEPS[c] > 0 and bench.DEFAULT_WARMUP[c] > 0
         assert bench.DEFAULT_STEPS[c] * step_ms[c] >= 400.0, c
