@@ -3,14 +3,16 @@
 // plan of 64 tensors checks its params, grads and state tensors (about 250 tensors) before every
 // step; through Python's Tensor.data_ptr each costs a method call, a quarter of a small step's
 // whole host time. `steady` makes all of a steady step's checks in one call (the params, their
-// grads and the state tensors), and `advance` moves the step counters. Not part of the step
-// itself: the optimizer falls back to Python when this module is not built.
+// grads and the state tensors), `advance` moves the step counters, and `fit` checks a whole new
+// set of grads and records them (after zero_grad(set_to_none=True) every step has one). Not part
+// of the step itself: the optimizer falls back to Python when this module is not built.
 #include <Python.h>
 
 #include <cstdint>
 #include <cstring>
 #include <exception>
 
+#include <torch/csrc/Dtype.h>
 #include <torch/csrc/autograd/python_variable.h>
 
 namespace {
@@ -154,11 +156,87 @@ PyObject *advance(PyObject *, PyObject *args) {
     return out;
 }
 
+// fit(grads: list, dtypes: list of torch.dtype, numels: list of int, device: int, callback) ->
+// (bytes, bytes, list) or None. None unless every grads[i] is a dense, contiguous tensor of
+// dtypes[i] with numels[i] elements on GPU `device` (what a step's descriptor i accepts); else the
+// grads' data pointers and their ids, each as packed native-endian uint64, and a weak reference to
+// each grad with `callback`.
+PyObject *fit(PyObject *, PyObject *args) {
+    PyObject *grads = nullptr, *dtypes = nullptr, *numels = nullptr, *callback = nullptr;
+    int device = -1;
+    if (!PyArg_ParseTuple(args, "O!O!O!iO", &PyList_Type, &grads, &PyList_Type, &dtypes, &PyList_Type, &numels, &device,
+                          &callback))
+        return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(grads);
+    if (PyList_GET_SIZE(dtypes) != n || PyList_GET_SIZE(numels) != n) {
+        PyErr_SetString(PyExc_ValueError, "fit: as many dtypes and sizes as grads are expected");
+        return nullptr;
+    }
+    PyObject *out = PyBytes_FromStringAndSize(nullptr, n * (Py_ssize_t)sizeof(uint64_t));
+    if (!out) return nullptr;
+    char *dst = PyBytes_AS_STRING(out);
+    try {
+        for (Py_ssize_t i = 0; i < n; i++) {
+            PyObject *o = PyList_GET_ITEM(grads, i);
+            PyObject *dt = PyList_GET_ITEM(dtypes, i);
+            if (!THPDtype_Check(dt)) {
+                Py_DECREF(out);
+                PyErr_SetString(PyExc_TypeError, "fit: a list of torch.dtype is expected");
+                return nullptr;
+            }
+            const long long want = PyLong_AsLongLong(PyList_GET_ITEM(numels, i));
+            if (want == -1 && PyErr_Occurred()) {
+                Py_DECREF(out);
+                return nullptr;
+            }
+            if (!THPVariable_Check(o)) {  // a grad of None
+                Py_DECREF(out);
+                Py_RETURN_NONE;
+            }
+            const at::Tensor &t = THPVariable_Unpack(o);
+            if (t.scalar_type() != reinterpret_cast<THPDtype *>(dt)->scalar_type || t.layout() != c10::kStrided ||
+                !t.is_cuda() || t.get_device() != device || t.numel() != want || !t.is_contiguous()) {
+                Py_DECREF(out);
+                Py_RETURN_NONE;
+            }
+            const uint64_t p = (uint64_t)(uintptr_t)t.data_ptr();
+            std::memcpy(dst + i * sizeof(uint64_t), &p, sizeof p);
+        }
+    } catch (const std::exception &e) {
+        Py_DECREF(out);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    PyObject *ids = PyBytes_FromStringAndSize(nullptr, n * (Py_ssize_t)sizeof(uint64_t));
+    PyObject *refs = ids ? PyList_New(n) : nullptr;
+    if (!refs) {
+        Py_XDECREF(ids);
+        Py_DECREF(out);
+        return nullptr;
+    }
+    char *idst = PyBytes_AS_STRING(ids);
+    for (Py_ssize_t i = 0; i < n; i++) {
+        PyObject *g = PyList_GET_ITEM(grads, i);
+        const uint64_t id = (uint64_t)(uintptr_t)g;
+        std::memcpy(idst + i * sizeof(uint64_t), &id, sizeof id);
+        PyObject *r = PyWeakref_NewRef(g, callback);
+        if (!r) {
+            Py_DECREF(refs);
+            Py_DECREF(ids);
+            Py_DECREF(out);
+            return nullptr;
+        }
+        PyList_SET_ITEM(refs, i, r);
+    }
+    return Py_BuildValue("(NNN)", out, ids, refs);
+}
+
 PyMethodDef kMethods[] = {
     {"same_ptrs", same_ptrs, METH_VARARGS, "Do these tensors still have the recorded data pointers?"},
     {"ptrs", ptrs, METH_VARARGS, "The tensors' data pointers as packed uint64."},
     {"steady", steady, METH_VARARGS, "Are the params, their grads and the state tensors the recorded ones?"},
     {"advance", advance, METH_VARARGS, "The step counters plus one, also stored in the state dicts."},
+    {"fit", fit, METH_VARARGS, "Check a new set of grads against the descriptors; their pointers and weak references."},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -258,6 +258,11 @@ class PreparedStep:
         self._gptrs[:] = ptrs
         return True
 
+    def set_grad_record(self, rec: bytes) -> None:
+        """Point every descriptor at the grad pointers of a packed native-endian uint64 record
+        (already checked against the descriptors, as set_grads checks them)."""
+        self._gptrs[:] = np.frombuffer(rec, dtype=np.uint64)
+
     def set_step(self, i: int, step: int) -> None:
         struct.pack_into("<Q", self.buf, i * _TENSOR.size + _STEP_OFFSET, int(step))
 

@@ -378,6 +378,28 @@ def test_steady_plan_check_and_counter_advance():
         host.advance([{}], ["x"], "step")
 
 
+def test_new_grad_set_check_rejects_what_a_descriptor_does_not_take():
+    """_lv_host.fit records a new set of grads only when every one is a dense, contiguous GPU tensor
+    of its descriptor's dtype and size on the plan's device; anything else (None, a CPU tensor)
+    gives None, and malformed arguments raise (the accepting case runs in the GPU plan tests)."""
+    from luminamoon_amd.optimizer import hip_backend
+
+    host = hip_backend.load_host_ext()
+    if host is None or not hasattr(host, "fit"):
+        pytest.skip("_lv_host.so is not built")
+    g = [torch.zeros(3), torch.zeros(4, dtype=torch.bfloat16)]
+    dts, ns = [torch.float32, torch.bfloat16], [3, 4]
+    assert host.fit(g, dts, ns, 0, None) is None  # CPU tensors
+    assert host.fit([None, g[1]], dts, ns, 0, None) is None
+    assert host.fit([], [], [], 0, None) == (b"", b"", [])
+    with pytest.raises(ValueError):
+        host.fit(g, dts[:1], ns, 0, None)
+    with pytest.raises(TypeError):
+        host.fit(g, ["float32", torch.bfloat16], ns, 0, None)
+    with pytest.raises(TypeError):
+        host.fit(g, dts, ["3", 4], 0, None)
+
+
 def test_plan_pointer_helpers_agree_with_python():
     """The step plans' data-pointer checks (the C module _lv_host when built, else Python maps)
     record where each tensor's data is and notice any move; an entry that is not a tensor (a grad
