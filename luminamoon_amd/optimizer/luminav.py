@@ -172,12 +172,10 @@ _data_ptr = torch.Tensor.data_ptr
 # entry that is not a tensor), _pack_ptrs(ints) makes a record from pointers. One C loop each
 # when _lv_host.so is built, Python maps otherwise.
 _host = hip_backend.load_host_ext()
-# One C call for all of a steady step's checks of a plan whose every param has a grad, and one for
-# its step counters (None without _lv_host.so, or with an older build of it).
-_steady = getattr(_host, "steady", None)
+# One C call for all of a step's checks of a plan whose every param has a grad, and one for its
+# step counters (None without _lv_host.so, or with an older build of it).
+_grad_record = getattr(_host, "grad_record", None)
 _advance = getattr(_host, "advance", None)
-# ... and one that checks and records a whole new set of grads (zero_grad(set_to_none=True))
-_fit = getattr(_host, "fit", None)
 if _host is not None:
     _ptr_record = _host.ptrs
     _same_ptrs = _host.same_ptrs
@@ -1378,7 +1376,7 @@ class LuminaV(Optimizer):
             "all_active": len(rows) == len(group["params"]),
             "eparams": eparams, "pptrs": _ptr_record(eparams),
             "gids": list(map(id, egrads)), "gptrs": list(map(_data_ptr, egrads)), "gptr_rec": _ptr_record(egrads),
-            "pid_rec": _pack_ptrs(list(map(id, group["params"]))), "gid_rec": _pack_ptrs(list(map(id, egrads))),
+            "pid_rec": _pack_ptrs(list(map(id, group["params"]))),
             "gweak": [weakref.ref(g, died) for g in egrads], "dead": dead, "died": died,
             "states": [r[9] for r in rows], "steps": [int(r[7]) for r in rows], "step_epoch": self._step_epoch,
             "keep": [t.untyped_storage() for r in rows for t in (r[3], r[4], r[5], r[6]) if t is not None],
@@ -1402,29 +1400,25 @@ class LuminaV(Optimizer):
             return False
         params = group["params"]
         prep = plan["prep"]
-        # The common case in one C call: the same params, each with the same grad object, and every
-        # param, grad and state tensor where it was (cfg2's 64 tensors: in Python these checks and
-        # the counters took 11.2 us of an 18.2 us step; with these two C calls the step is 14.6 us).
-        if not (_steady is not None and plan["all_active"] and not plan["dead"][0] and type(params) is list
-                and _steady(params, plan["pid_rec"], plan["pptrs"], plan["gid_rec"], plan["gptr_rec"],
-                            plan["stensors"], plan["sptrs"])):
-            # one check at a time: what changed, with grads re-pointed where only they did
-            if list(map(id, params)) != plan["ids"]:  # the plan holds the params: equal ids, same objects
-                return False
-            if plan["all_active"]:
-                grads = list(map(_get_grad, params))
-            else:
-                if [p.grad is not None for p in params] != plan["active"]:
-                    return False
-                grads = list(map(_get_grad, plan["eparams"]))
-            if not _same_ptrs(plan["eparams"], plan["pptrs"]):  # a param's storage moved
-                return False
-            if not _same_ptrs(plan["stensors"], plan["sptrs"]):  # a state tensor's storage moved
-                return False
-            gids = list(map(id, grads))
-            if plan["dead"][0] or gids != plan["gids"] or not _same_ptrs(grads, plan["gptr_rec"]):
-                if not self._refresh_plan_grads(plan, grads, gids):
-                    return False
+        # Every check in one C call (_lv_host.grad_record): the same param objects at their data
+        # pointers, the state tensors at theirs, and each param's grad a dense, contiguous GPU tensor
+        # of its descriptor's dtype and size. It returns where the grads are, so new grad objects
+        # (zero_grad(set_to_none=True)) are taken as they come. cfg2's 64 tensors: in Python these
+        # checks and the counters took 11.2 us of an 18.2 us step; with the two C calls the step is
+        # 14.6 us. 2,000 tensors with new grads every step: 1.77 ms in Python.
+        rec = None
+        if _grad_record is not None and plan["all_active"] and type(params) is list:
+            rec = _grad_record(params, plan["pid_rec"], plan["pptrs"], plan["stensors"], plan["sptrs"],
+                               prep.gdtypes, prep.numels, prep.index)
+        if rec is not None:
+            if rec != plan["gptr_rec"]:
+                prep.set_grad_record(rec)
+                plan["gptr_rec"] = rec
+            # the Python checks' record of the grads' identities is not kept on this path: should
+            # they run, they re-point every grad
+            plan["dead"][0] = True
+        elif not self._check_plan_in_python(plan, params):
+            return False
         # nothing above touched the step counters, so a False return leaves them for the slow path
         states = plan["states"]
         if plan["step_epoch"] != self._step_epoch:  # a counter was set from outside: read them again
@@ -1440,29 +1434,38 @@ class LuminaV(Optimizer):
         self._stepper.launch(group, prep)
         return True
 
+    def _check_plan_in_python(self, plan: Dict[str, Any], params: List[Any]) -> bool:
+        """The plan's checks one at a time: False when anything but the grads changed (the params,
+        which of them have grads, where a param or state tensor's data is), else True with the
+        grads that changed re-pointed (or False if one does not fit its descriptor)."""
+        if list(map(id, params)) != plan["ids"]:  # the plan holds the params: equal ids, same objects
+            return False
+        if plan["all_active"]:
+            grads = list(map(_get_grad, params))
+        else:
+            if [p.grad is not None for p in params] != plan["active"]:
+                return False
+            grads = list(map(_get_grad, plan["eparams"]))
+        if not _same_ptrs(plan["eparams"], plan["pptrs"]):  # a param's storage moved
+            return False
+        if not _same_ptrs(plan["stensors"], plan["sptrs"]):  # a state tensor's storage moved
+            return False
+        gids = list(map(id, grads))
+        if plan["dead"][0] or gids != plan["gids"] or not _same_ptrs(grads, plan["gptr_rec"]):
+            if not self._refresh_plan_grads(plan, grads, gids):
+                return False
+            plan["gptr_rec"] = _ptr_record(grads)
+        return True
+
     def _refresh_plan_grads(self, plan: Dict[str, Any], grads: List[Any], gids: List[int]) -> bool:
         """Re-points the descriptors of grads that changed (each validated: dtype, device, numel,
-        contiguity, dense), re-arms the weak references and records the grads' ids and pointers.
-        False if a grad does not fit."""
+        contiguity, dense) and re-arms the weak references. False if a grad does not fit."""
         prep = plan["prep"]
         dead = plan["dead"]
-        old_ids, weak = plan["gids"], plan["gweak"]
+        old_ids, old_ptrs, weak = plan["gids"], plan["gptrs"], plan["gweak"]
         if dead[0] or 4 * sum(map(operator.ne, gids, old_ids)) > len(gids):
             # the common case after zero_grad(set_to_none=True): (nearly) every grad is a new
-            # tensor, so re-point them all at once: one C call (_lv_host.fit) checks them, packs
-            # their pointers and ids and makes the weak references (2,000 tensors: ~1.6 ms of
-            # Python otherwise)
-            if _fit is not None:
-                got = _fit(grads, prep.gdtypes, prep.numels, prep.index, plan["died"])
-                if got is None:
-                    return False
-                rec, plan["gid_rec"], plan["gweak"] = got
-                prep.set_grad_record(rec)
-                plan["gids"] = gids
-                plan["gptrs"] = None  # unpacked from gptr_rec when one grad at a time changes
-                plan["gptr_rec"] = rec
-                dead[0] = False
-                return True
+            # tensor, so re-point them all at once (one check loop, one pointer write, weakrefs by map)
             if any(map(operator.is_, grads, repeat(None))):
                 return False
             ptrs = list(map(_data_ptr, grads))
@@ -1471,13 +1474,8 @@ class LuminaV(Optimizer):
             plan["gweak"] = list(map(weakref.ref, grads, repeat(plan["died"])))
             plan["gids"] = gids
             plan["gptrs"] = ptrs
-            plan["gptr_rec"] = _ptr_record(grads)
-            plan["gid_rec"] = _pack_ptrs(gids)
             dead[0] = False
             return True
-        old_ptrs = plan["gptrs"]
-        if old_ptrs is None:
-            old_ptrs = plan["gptrs"] = list(struct.unpack(f"={len(gids)}Q", plan["gptr_rec"]))
         for k, g in enumerate(grads):
             if g is None:
                 return False
@@ -1490,8 +1488,6 @@ class LuminaV(Optimizer):
             old_ids[k] = gids[k]
             old_ptrs[k] = g.data_ptr()
         dead[0] = False
-        plan["gptr_rec"] = _ptr_record(grads)
-        plan["gid_rec"] = _pack_ptrs(old_ids)
         return True
 
     # ------------------------------------------------------------------ capturable groups

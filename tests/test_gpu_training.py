@@ -199,19 +199,19 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod, monkeypatch)
         return ok
 
     opt._run_unfused_plan = spy
-    # the one-call check of a steady step (_lv_host.steady), when built: count its verdicts
+    # the one-call check of a step (_lv_host.grad_record), when built: count the steps it took
     import luminamoon_amd.optimizer.luminav as L
 
-    steady_real = L._steady
-    verdicts = {True: 0, False: 0}
+    record_real = L._grad_record
+    taken = {"n": 0}
 
-    def steady_spy(*a):
-        ok = steady_real(*a)
-        verdicts[bool(ok)] += 1
-        return ok
+    def record_spy(*a):
+        rec = record_real(*a)
+        taken["n"] += rec is not None
+        return rec
 
-    if steady_real is not None:
-        monkeypatch.setattr(L, "_steady", steady_spy)
+    if record_real is not None:
+        monkeypatch.setattr(L, "_grad_record", record_spy)
     host_steps = [0] * len(sizes)
     kept = []
 
@@ -309,12 +309,13 @@ def test_unfused_descriptor_plan_reuse_and_invalidation(oracle_mod, monkeypatch)
     sc2.data = sc2.data.clone()
     run(28, "new", False)
     run(29, "new", True)
-    # steady steps: the same grad objects updated in place, checked and counted in one C call each
-    hits = verdicts[True]
-    for s in (30, 31, 32):
-        run(s, "inplace", True)
-    if steady_real is not None:
-        assert verdicts[True] - hits == 3, verdicts
+    # the same grad objects updated in place, then new grad objects every step
+    # (zero_grad(set_to_none=True)): each step checked and its grads recorded in one C call
+    n0 = taken["n"]
+    for s, mode in ((30, "inplace"), (31, "inplace"), (32, "new"), (33, "new"), (34, "keep"), (35, "one")):
+        run(s, mode, True)
+    if record_real is not None:
+        assert taken["n"] - n0 == 6, taken
 
 
 def test_unfused_duplicate_param_raises_like_the_native_seam():

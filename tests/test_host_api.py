@@ -315,52 +315,37 @@ def test_reference_checkpoint_state_precision_is_inferred():
     assert all(opt.state[p][k].dtype == torch.float32 for p in ps for k in ("exp_avg", "exp_avg_sq"))
 
 
-def test_steady_plan_check_and_counter_advance():
-    """_lv_host.steady is True exactly while the params, their grad objects and every param, grad
-    and state tensor's data are the recorded ones; advance returns the counters plus one and
-    stores each in its state dict, bypassing a dict subclass's __setitem__ as the Python path does."""
+def test_plan_record_check_and_counter_advance():
+    """_lv_host.grad_record gives None whenever the params are not the recorded objects at their
+    recorded data pointers, a state tensor's data moved, a grad is missing or does not fit its
+    descriptor (CPU tensors never do: the accepting case runs in the GPU plan tests), and rejects
+    malformed arguments; advance returns the counters plus one and stores each in its state dict,
+    bypassing a dict subclass's __setitem__ as the Python path does."""
     import luminamoon_amd.optimizer.luminav as L
     from luminamoon_amd.optimizer import hip_backend
 
     host = hip_backend.load_host_ext()
-    if host is None or not hasattr(host, "steady"):
+    if host is None or not hasattr(host, "grad_record"):
         pytest.skip("_lv_host.so is not built")
-    params = [torch.nn.Parameter(torch.zeros(n)) for n in (3, 4, 5)]
+    params = [torch.nn.Parameter(torch.zeros(3)), torch.nn.Parameter(torch.zeros(4, dtype=torch.bfloat16))]
     for p in params:
         p.grad = torch.ones_like(p)
-    states = [torch.zeros(3), torch.zeros(4), torch.zeros(5)]
-
-    def rec():
-        grads = [p.grad for p in params]
-        return (L._pack_ptrs(list(map(id, params))), L._ptr_record(params), L._pack_ptrs(list(map(id, grads))),
-                L._ptr_record(grads), L._ptr_record(states))
-
-    pid, pp, gid, gp, sp = rec()
-    assert host.steady(params, pid, pp, gid, gp, states, sp)
-    assert not host.steady(params[:2], pid, pp, gid, gp, states, sp)  # records of another length
-    assert not host.steady([params[1], params[0], params[2]], pid, pp, gid, gp, states, sp)
-    g0 = params[0].grad
-    params[0].grad = torch.ones_like(params[0])  # a new grad object
-    assert not host.steady(params, pid, pp, gid, gp, states, sp)
-    params[0].grad = g0
-    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    states = [torch.zeros(3)]
+    dts, ns = [torch.float32, torch.bfloat16], [3, 4]
+    pid, pp, sp = L._pack_ptrs(list(map(id, params))), L._ptr_record(params), L._ptr_record(states)
+    assert host.grad_record(params, pid, pp, states, sp, dts, ns, 0) is None  # CPU grads do not fit
+    assert host.grad_record(params[::-1], pid, pp, states, sp, dts, ns, 0) is None
+    assert host.grad_record(params, pid, pp, states, L._ptr_record([torch.zeros(3)]), dts, ns, 0) is None
+    assert host.grad_record(params, pid[:8], pp, states, sp, dts, ns, 0) is None
     params[1].grad = None
-    assert not host.steady(params, pid, pp, gid, gp, states, sp)
-    params[1].grad = torch.ones_like(params[1])
-    pid, pp, gid, gp, sp = rec()
-    assert host.steady(params, pid, pp, gid, gp, states, sp)
-    params[2].grad.data = params[2].grad.data.clone()  # the same grad object, its data moved
-    assert not host.steady(params, pid, pp, gid, gp, states, sp)
-    pid, pp, gid, gp, sp = rec()
-    params[2].data = params[2].data.clone()  # a param's data moved
-    assert not host.steady(params, pid, pp, gid, gp, states, sp)
-    pid, pp, gid, gp, sp = rec()
-    states[1].set_(states[1].clone())  # a state tensor's data moved
-    assert not host.steady(params, pid, pp, gid, gp, states, sp)
-    pid, pp, gid, gp, sp = rec()
-    assert host.steady(params, pid, pp, gid, gp, states, sp)
+    assert host.grad_record(params, pid, pp, states, sp, dts, ns, 0) is None
+    assert host.grad_record([], b"", b"", [], b"", [], [], 0) == b""
+    with pytest.raises(ValueError):
+        host.grad_record(params, pid, pp, states, sp, dts[:1], ns, 0)
     with pytest.raises(TypeError):
-        host.steady(tuple(params), pid, pp, gid, gp, states, sp)
+        host.grad_record(params, pid, pp, states, sp, [1, 2], ns, 0)
+    with pytest.raises(TypeError):
+        host.grad_record(tuple(params), pid, pp, states, sp, dts, ns, 0)
 
     class Guarded(dict):
         def __setitem__(self, k, v):
@@ -376,28 +361,6 @@ def test_steady_plan_check_and_counter_advance():
         host.advance([{}, 3], [1, 2], "step")
     with pytest.raises(TypeError):
         host.advance([{}], ["x"], "step")
-
-
-def test_new_grad_set_check_rejects_what_a_descriptor_does_not_take():
-    """_lv_host.fit records a new set of grads only when every one is a dense, contiguous GPU tensor
-    of its descriptor's dtype and size on the plan's device; anything else (None, a CPU tensor)
-    gives None, and malformed arguments raise (the accepting case runs in the GPU plan tests)."""
-    from luminamoon_amd.optimizer import hip_backend
-
-    host = hip_backend.load_host_ext()
-    if host is None or not hasattr(host, "fit"):
-        pytest.skip("_lv_host.so is not built")
-    g = [torch.zeros(3), torch.zeros(4, dtype=torch.bfloat16)]
-    dts, ns = [torch.float32, torch.bfloat16], [3, 4]
-    assert host.fit(g, dts, ns, 0, None) is None  # CPU tensors
-    assert host.fit([None, g[1]], dts, ns, 0, None) is None
-    assert host.fit([], [], [], 0, None) == (b"", b"", [])
-    with pytest.raises(ValueError):
-        host.fit(g, dts[:1], ns, 0, None)
-    with pytest.raises(TypeError):
-        host.fit(g, ["float32", torch.bfloat16], ns, 0, None)
-    with pytest.raises(TypeError):
-        host.fit(g, dts, ["3", 4], 0, None)
 
 
 def test_plan_pointer_helpers_agree_with_python():
