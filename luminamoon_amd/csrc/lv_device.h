@@ -1117,7 +1117,8 @@ __device__ __forceinline__ const LV_CONSTANT TDesc *table_of(const Args &a) {
 }
 
 // A copy of the descriptor of tensor t of a table launch (a reference into the table would not
-// carry its address space).
+// carry its address space), field by field.
+static_assert(sizeof(Desc) == 80, "table_desc copies every field of Desc: extend it with the struct");
 __device__ __forceinline__ Desc table_desc(const Args &a, int t) {
     const LV_CONSTANT Desc &c = table_of(a)[t].d;
     Desc d;
