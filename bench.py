@@ -252,13 +252,19 @@ def stream_shape_fn(lib, shape: int):
 def stream_shape_desc(lib, shape: int) -> str:
     import ctypes
 
-    info = (ctypes.c_int * 5)()
+    info = (ctypes.c_int * 8)()
     if lib.lv_stream_probe_shape_info(shape, info) != 0:
         raise RuntimeError(f"unknown stream shape {shape}")
-    t, g, nt, persist, xcd = list(info)
-    return (f"{t} threads x {4 * g} elements ({g} group{'s' if g > 1 else ''} of 4 per thread), "
-            f"{'non-temporal' if nt else 'plain'} accesses{', persistent grid (8 blocks per CU)' if persist else ''}"
-            f"{', XCD-contiguous' if xcd else ''}")
+    t, g, nt, persist, xcd, buf, la, sa = list(info)
+
+    def policy(aux):
+        bits = [name for bit, name in ((1, "sc0"), (2, "nt"), (16, "sc1")) if aux & bit]
+        return " ".join(bits) or "default"
+
+    access = (f"buffer accesses (loads {policy(la)}, stores {policy(sa)})" if buf else
+              f"{'non-temporal' if nt else 'plain'} accesses")
+    return (f"{t} threads x {4 * g} elements ({g} group{'s' if g > 1 else ''} of 4 per thread), {access}"
+            f"{', persistent grid (8 blocks per CU)' if persist else ''}{', XCD-contiguous' if xcd else ''}")
 
 
 def check_stream_probe(torch, fn, pb: int, sb: int, ns: int) -> None:

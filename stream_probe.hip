@@ -123,25 +123,83 @@ __global__ void __launch_bounds__(T) shape_kernel(void *p, const void *g, void *
     }
 }
 
+// The step's shape and mapping (256 threads, 4 elements per thread, XCD-contiguous) with buffer
+// loads and stores whose cache policy bits are set explicitly: LA for the loads, SA for the stores
+// (bit 0 sc0, bit 1 nt, bit 4 sc1). The buffer of each stream spans exactly the block's elements,
+// so lanes past the last element load zeros and store nothing.
+template <int BYTES> struct Buf;
+template <> struct Buf<2> {  // 4 elements of 2 bytes: 8 bytes a lane
+    using T = u32x2;
+    template <int AUX> static __device__ T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
+    }
+    template <int AUX> static __device__ void store(T x, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+        __builtin_amdgcn_raw_buffer_store_b64(x, r, off, 0, AUX);
+    }
+};
+template <> struct Buf<4> {  // 4 elements of 4 bytes: 16 bytes a lane
+    using T = u32x4;
+    template <int AUX> static __device__ T load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+    }
+    template <int AUX> static __device__ void store(T x, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+        __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, AUX);
+    }
+};
+
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer access, as for gfx9-family dword loads
+
+template <int P, int S, int NS, int LA, int SA>
+__global__ void __launch_bounds__(kThreads) policy_kernel(void *p, const void *g, void *m, void *v, uint64_t n,
+                                                          uint64_t pieces) {
+    const uint64_t per = (pieces + 7u) / 8u;  // the grid is 8 * per blocks
+    const uint64_t piece = (uint64_t)(blockIdx.x % 8u) * per + blockIdx.x / 8u;
+    if (piece >= pieces) return;
+    const uint64_t e0 = piece * kUnit;
+    const int cnt = (int)(n - e0 < kUnit ? n - e0 : kUnit);  // elements of this block
+    auto rsrc = [&](const void *base, int bytes) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(static_cast<const char *>(base)) + e0 * bytes, 0,
+                                                 cnt * bytes, kRsrcWord3);
+    };
+    const __amdgpu_buffer_rsrc_t rp = rsrc(p, P), rg = rsrc(g, P), rm = rsrc(m, S);
+    const uint32_t op = threadIdx.x * 4u * P, os = threadIdx.x * 4u * S;
+    const auto gv = Buf<P>::template load<LA>(rg, op);
+    const auto mv = Buf<S>::template load<LA>(rm, os);
+    typename Buf<S>::T vv{};
+    const __amdgpu_buffer_rsrc_t rv = rsrc(NS == 2 ? v : m, S);  // unused when there is no v
+    if constexpr (NS == 2) vv = Buf<S>::template load<LA>(rv, os);
+    const auto pv = Buf<P>::template load<LA>(rp, op);
+    Buf<P>::template store<SA>(pv ^ gv, rp, op);
+    Buf<S>::template store<SA>(mv ^ gv.x, rm, os);
+    if constexpr (NS == 2) Buf<S>::template store<SA>(vv ^ mv.x, rv, os);
+}
+
 struct ShapeInfo {
     int threads, groups;
     bool nt, persist, xcd;
+    int buffer, load_aux, store_aux;  // buffer: policy_kernel with the given cache policy bits
 };
 
 // The shapes: 0 is stream_probe_kernel's (the step's unit shape); 7 adds the step's XCD mapping.
 constexpr ShapeInfo kShapes[] = {
-    {256, 1, true, false, false},   // 0: 1024 elements per block
-    {256, 2, true, false, false},   // 1: 2048 per block, two groups 1024 apart
-    {256, 4, true, false, false},   // 2: 4096 per block, four groups 1024 apart
-    {1024, 1, true, false, false},  // 3: 4096 per block of 1024 threads
-    {64, 1, true, false, false},    // 4: 256 per block of one wave
-    {256, 1, true, true, false},    // 5: 1024-element pieces, 8 blocks per CU striding over them
-    {256, 1, false, false, false},  // 6: shape 0 with plain loads and stores
-    {256, 1, true, false, true},    // 7: shape 0, XCD-contiguous (the step's mapping)
-    {64, 1, true, false, true},     // 8: shape 4, XCD-contiguous
-    {128, 1, true, false, false},   // 9: 512 per block of two waves
-    {128, 1, true, false, true},    // 10: shape 9, XCD-contiguous
-    {64, 2, true, false, true},     // 11: 512 per block of one wave, XCD-contiguous
+    {256, 1, true, false, false, 0, 0, 0},   // 0: 1024 elements per block
+    {256, 2, true, false, false, 0, 0, 0},   // 1: 2048 per block, two groups 1024 apart
+    {256, 4, true, false, false, 0, 0, 0},   // 2: 4096 per block, four groups 1024 apart
+    {1024, 1, true, false, false, 0, 0, 0},  // 3: 4096 per block of 1024 threads
+    {64, 1, true, false, false, 0, 0, 0},    // 4: 256 per block of one wave
+    {256, 1, true, true, false, 0, 0, 0},    // 5: 1024-element pieces, 8 blocks per CU striding over them
+    {256, 1, false, false, false, 0, 0, 0},  // 6: shape 0 with plain loads and stores
+    {256, 1, true, false, true, 0, 0, 0},    // 7: shape 0, XCD-contiguous (the step's mapping)
+    {64, 1, true, false, true, 0, 0, 0},     // 8: shape 4, XCD-contiguous
+    {128, 1, true, false, false, 0, 0, 0},   // 9: 512 per block of two waves
+    {128, 1, true, false, true, 0, 0, 0},    // 10: shape 9, XCD-contiguous
+    {64, 2, true, false, true, 0, 0, 0},     // 11: 512 per block of one wave, XCD-contiguous
+    {256, 1, true, false, true, 1, 2, 2},    // 12: shape 7 as buffer accesses: loads nt, stores nt
+    {256, 1, true, false, true, 1, 18, 18},  // 13: loads nt sc1, stores nt sc1
+    {256, 1, true, false, true, 1, 3, 19},   // 14: loads sc0 nt, stores sc0 nt sc1
+    {256, 1, true, false, true, 1, 2, 0},    // 15: loads nt, stores default
+    {256, 1, false, false, true, 1, 0, 2},   // 16: loads default, stores nt
+    {256, 1, true, false, true, 1, 2, 17},   // 17: loads nt, stores sc0 sc1
 };
 constexpr int kNumShapes = (int)(sizeof(kShapes) / sizeof(kShapes[0]));
 
@@ -161,6 +219,11 @@ hipError_t launch_shape(void *p, const void *g, void *m, void *v, uint64_t n, hi
     constexpr ShapeInfo si = kShapes[SH];
     const uint64_t pieces = shape_pieces(si, n);
     uint64_t blocks = shape_blocks(si, n);
+    if constexpr (si.buffer) {
+        policy_kernel<P, S, NS, si.load_aux, si.store_aux><<<(uint32_t)blocks, kThreads, 0, stream>>>(p, g, m, v, n,
+                                                                                                     pieces);
+        return hipGetLastError();
+    }
     if (si.persist) {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -187,7 +250,13 @@ hipError_t launch_shape_of(int shape, void *p, const void *g, void *m, void *v, 
     case 8: return launch_shape<P, S, NS, 8>(p, g, m, v, n, stream);
     case 9: return launch_shape<P, S, NS, 9>(p, g, m, v, n, stream);
     case 10: return launch_shape<P, S, NS, 10>(p, g, m, v, n, stream);
-    default: return launch_shape<P, S, NS, 11>(p, g, m, v, n, stream);
+    case 11: return launch_shape<P, S, NS, 11>(p, g, m, v, n, stream);
+    case 12: return launch_shape<P, S, NS, 12>(p, g, m, v, n, stream);
+    case 13: return launch_shape<P, S, NS, 13>(p, g, m, v, n, stream);
+    case 14: return launch_shape<P, S, NS, 14>(p, g, m, v, n, stream);
+    case 15: return launch_shape<P, S, NS, 15>(p, g, m, v, n, stream);
+    case 16: return launch_shape<P, S, NS, 16>(p, g, m, v, n, stream);
+    default: return launch_shape<P, S, NS, 17>(p, g, m, v, n, stream);
     }
 }
 
@@ -227,8 +296,10 @@ extern "C" int lv_stream_probe(int param_bytes, int state_bytes, int nstate, voi
 // Number of shapes lv_stream_probe_shape takes (0 .. count - 1).
 extern "C" int lv_stream_probe_shapes(void) { return kNumShapes; }
 
-// Threads per block, 4-element groups per thread, non-temporal (1/0), persistent (1/0) and
-// XCD-contiguous (1/0) of a shape, into out[5]. Returns 0, or 1 for an unknown shape or a NULL out.
+// Threads per block, 4-element groups per thread, non-temporal (1/0), persistent (1/0),
+// XCD-contiguous (1/0), buffer accesses (1/0) and, for those, the load and store cache policy bits
+// (bit 0 sc0, bit 1 nt, bit 4 sc1) of a shape, into out[8]. Returns 0, or 1 for an unknown shape or
+// a NULL out.
 extern "C" int lv_stream_probe_shape_info(int shape, int *out) {
     if (shape < 0 || shape >= kNumShapes || !out) return 1;
     out[0] = kShapes[shape].threads;
@@ -236,6 +307,9 @@ extern "C" int lv_stream_probe_shape_info(int shape, int *out) {
     out[2] = kShapes[shape].nt ? 1 : 0;
     out[3] = kShapes[shape].persist ? 1 : 0;
     out[4] = kShapes[shape].xcd ? 1 : 0;
+    out[5] = kShapes[shape].buffer;
+    out[6] = kShapes[shape].load_aux;
+    out[7] = kShapes[shape].store_aux;
     return 0;
 }
 

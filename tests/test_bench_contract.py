@@ -156,11 +156,12 @@ def test_stream_probe_shapes_reject_invalid_arguments_before_any_launch():
     lib = bench.stream_probe_lib()
     count = lib.lv_stream_probe_shapes()
     assert count >= 2
-    info = (ctypes.c_int * 5)()
-    assert lib.lv_stream_probe_shape_info(0, info) == 0 and list(info) == [256, 1, 1, 0, 0]
+    info = (ctypes.c_int * 8)()
+    assert lib.lv_stream_probe_shape_info(0, info) == 0 and list(info) == [256, 1, 1, 0, 0, 0, 0, 0]
     for shape in range(count):
         assert lib.lv_stream_probe_shape_info(shape, info) == 0
-        assert info[0] in (64, 128, 256, 1024) and info[1] in (1, 2, 4) and all(x in (0, 1) for x in info[2:])
+        assert info[0] in (64, 128, 256, 1024) and info[1] in (1, 2, 4) and all(x in (0, 1) for x in info[2:6])
+        assert all(0 <= x < 32 for x in info[6:]) and (info[5] or info[6] == info[7] == 0)
         assert bench.stream_shape_desc(lib, shape)
     assert lib.lv_stream_probe_shape_info(count, info) == 1
     assert lib.lv_stream_probe_shape_info(-1, info) == 1
