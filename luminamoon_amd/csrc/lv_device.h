@@ -449,25 +449,26 @@ __device__ __forceinline__ float tanh_pade(float x_in, const PadeK &c = kPade) {
     return (x * p) / q;
 }
 
-// IEEE f32 division without the scaling and fix-up steps. The compiler's correctly rounded
-// quotient is v_div_scale (both operands), v_rcp_f32, fma/mul refinement, v_div_fmas and
-// v_div_fixup: 11 instructions, about 15.5 integer adds of issue time on gfx950 (the scale, fmas
-// and fixup steps issue at about 1.6 each, v_rcp at 3). Where v_div_scale leaves both operands
-// as they are (vcc clear) v_div_fmas is a plain fma, and where v_div_fixup finds no special case
-// it only puts back the sign the quotient already has; the rest is the same v_rcp_f32 and the same
-// seven fma/mul in the same order, so this equals n / d bit for bit when: n and d are normal and
-// finite, |n| >= 2^-103, |n / d| is a normal number (no overflow, not below 2^-126), 1 / d is
-// normal and the exponents of n and d are less than 96 apart. Callers test their own sufficient
-// condition, wave-uniformly, and otherwise divide as usual.
+// IEEE f32 division in five instructions: v_rcp_f32, one Newton step on the reciprocal (r1), the
+// product q0 = n * r1 and one correction by its exact residual, q0 + (n - d * q0) * r1 (Markstein's
+// final step). The compiler's correctly rounded quotient is 11 instructions, about 15.5 integer
+// adds of issue time on gfx950 (v_div_scale on both operands, v_rcp_f32, the refinement,
+// v_div_fmas and v_div_fixup; the scale, fmas and fixup steps issue at about 1.6 each, v_rcp at
+// 3). This equals n / d bit for bit on every pair of significands: n and d in [1, 2), all 2^46
+// pairs, checked on the GPU against the compiler's division, with v_rcp_f32's result checked to
+// scale exactly with d's exponent over [-125, 125] (tests/gpu_checks/exact_check.hip). Other
+// exponents scale every step when |n| >= 2^-100, 2^-125 <= |n / d| (no overflow) and
+// 2^-125 <= d <= 2^125: r1, q0 and the quotient are then normal, and the residual n - d * q0, a
+// multiple of 2^-147, is exact wherever it is subnormal, so every rounding scales with the
+// operands. Callers test their own sufficient condition, wave-uniformly, and otherwise divide as
+// usual.
 __device__ __forceinline__ float div_unscaled(float n, float d) {
     const float r0 = __builtin_amdgcn_rcpf(d);
     const float e0 = __builtin_fmaf(-d, r0, 1.0f);
     const float r1 = __builtin_fmaf(e0, r0, r0);
     const float q0 = n * r1;
     const float e1 = __builtin_fmaf(-d, q0, n);
-    const float q1 = __builtin_fmaf(e1, r1, q0);
-    const float e2 = __builtin_fmaf(-d, q1, n);
-    return __builtin_fmaf(e2, r1, q1);
+    return __builtin_fmaf(e1, r1, q0);
 }
 
 // clm / env of T1, T2 and TD-CLM, where |clm| <= env up to rounding (env adds the

@@ -293,6 +293,79 @@ extern "C" int div_check(unsigned long long *host_counts /* 4 */, uint32_t *host
     return rc;
 }
 
+namespace {
+
+// div_unscaled against IEEE division on every pair of significands: n = 1.nm, d = 1.dm, both in
+// [1, 2), for the 2^23 numerators nm and the denominators dm in [dm0, dm0 + gridDim.x). Under the
+// guards of div_envelope and div_bound every intermediate of div_unscaled is these pairs' scaled
+// by powers of two: v_rcp_f32 scales with d's exponent (check_rcp_scale), e0 does not depend on
+// it, q0, r1 and the quotient are normal, and the residual n - d * q0 is exact wherever its scaled
+// value is subnormal (a multiple of 2^-147 there), so every rounding scales too. Counters: [0]
+// mismatches (ex: dm, nm pairs), [1] pairs checked.
+__global__ void check_div_pairs(uint32_t dm0, unsigned long long *out, uint32_t *ex) {
+    const uint32_t dm = dm0 + blockIdx.x;
+    const float d = __uint_as_float(0x3F800000u | dm);
+    for (uint32_t nm = threadIdx.x; nm < (1u << 23); nm += blockDim.x) {
+        const float n = __uint_as_float(0x3F800000u | nm);
+        if (__float_as_uint(lv::div_unscaled(n, d)) != __float_as_uint(n / d)) {
+            const unsigned long long k = atomicAdd(&out[0], 1ull);
+            if (k < 4) {
+                ex[2 * k] = dm;
+                ex[2 * k + 1] = nm;
+            }
+        }
+    }
+    if (threadIdx.x == 0) atomicAdd(&out[1], 1ull << 23);
+}
+
+// v_rcp_f32 on d = 1.dm * 2^e against v_rcp_f32(1.dm) * 2^-e, for every significand and every e
+// with 2^e and 2^-e normal (e in [-126, 126] less the ends): the reciprocal's significand does
+// not depend on d's exponent. Counters: [2] mismatches (ex: dm, e + 128), [3] pairs checked.
+__global__ void check_rcp_scale(unsigned long long *out, uint32_t *ex) {
+    const uint32_t dm = blockIdx.x * blockDim.x + threadIdx.x;
+    if (dm >= (1u << 23)) return;
+    const float base = __builtin_amdgcn_rcpf(__uint_as_float(0x3F800000u | dm));
+    for (int e = -125; e <= 125; e++) {
+        const float d = __uint_as_float(((uint32_t)(127 + e) << 23) | dm);
+        const float want = __builtin_ldexpf(base, -e);
+        if (__float_as_uint(__builtin_amdgcn_rcpf(d)) != __float_as_uint(want)) {
+            const unsigned long long k = atomicAdd(&out[2], 1ull);
+            if (k < 4) {
+                ex[8 + 2 * k] = dm;
+                ex[8 + 2 * k + 1] = (uint32_t)(e + 128);
+            }
+        }
+    }
+    if ((dm & 255u) == 0u) atomicAdd(&out[3], 256ull * 251ull);
+}
+
+}  // namespace
+
+// div_unscaled on the significand pairs with denominators [dm_first, dm_first + dm_count), and
+// (with_rcp) v_rcp_f32's scaling over every exponent. Counters as check_div_pairs and
+// check_rcp_scale: 4, examples 16. Returns 0, or negative on a HIP error or a range outside 2^23.
+extern "C" int div_pair_check(uint32_t dm_first, uint32_t dm_count, int with_rcp, unsigned long long *host_counts,
+                              uint32_t *host_examples) {
+    if (dm_first > (1u << 23) || dm_count > (1u << 23) - dm_first) return -5;
+    unsigned long long *out = nullptr;
+    uint32_t *ex = nullptr;
+    if (hipMalloc(&out, 4 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMalloc(&ex, 16 * sizeof(uint32_t)) != hipSuccess) return -1;
+    if (hipMemset(out, 0, 4 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    if (hipMemset(ex, 0, 16 * sizeof(uint32_t)) != hipSuccess) return -1;
+    const uint32_t per = 1u << 14;
+    for (uint32_t b = 0; b < dm_count; b += per)
+        check_div_pairs<<<dm_count - b < per ? dm_count - b : per, 256>>>(dm_first + b, out, ex);
+    if (with_rcp) check_rcp_scale<<<(1u << 23) / 256, 256>>>(out, ex);
+    int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -2;
+    if (rc == 0 && hipMemcpy(host_counts, out, 4 * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
+        rc = -3;
+    if (rc == 0 && hipMemcpy(host_examples, ex, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) rc = -3;
+    (void)hipFree(out);
+    (void)hipFree(ex);
+    return rc;
+}
+
 // The graph launches' per-step coefficients computed on the device (lv::step_coeffs, the function
 // the step record kernel calls), for the host to compare with its own: out[4 * i ..] = c1, c2,
 // c_sigma (bits) and the seed base of steps[i].

@@ -24,7 +24,11 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
   fma refinement without its scaling and fix-up steps, taken when a wave-uniform test proves
   them unneeded) against IEEE division: every 2^32 numerator with denominators from n/2 to 2^25,
   T2's clm / env from its own formula for every gradient bit pattern, and the rational bound for
-  every step value.
+  every step value;
+* div_unscaled itself (one Newton step on v_rcp_f32's reciprocal and one correction) against IEEE
+  division on all 2^46 pairs of significands in [1, 2), with v_rcp_f32's scaling by the
+  denominator's exponent checked for every significand and exponent in [-125, 125]: under the
+  guards' conditions every other operand pair is one of these scaled by powers of two.
 """
 from __future__ import annotations
 
@@ -88,3 +92,23 @@ def test_guarded_fast_divisions_equal_ieee_division():
     # numerators with 2^-100 <= |n| <= 2^25: 2 signs x 125 binades x 2^23, sampled one in 2^16,
     # with at least 2 of the 3 denominators in range each
     assert counts[3] >= 2 * 125 * 128 * 2
+
+
+def test_one_correction_division_on_every_significand_pair():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    lib = _lib()
+    lib.div_pair_check.restype = ctypes.c_int
+    lib.div_pair_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
+                                   ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_uint32)]
+    chunk = 1 << 20
+    for first in range(0, 1 << 23, chunk):
+        counts = (ctypes.c_ulonglong * 4)()
+        ex = (ctypes.c_uint32 * 16)()
+        print(f"[case] div_unscaled, denominators {first:#x}..{first + chunk - 1:#x} x 2^23 numerators", flush=True)
+        assert lib.div_pair_check(first, chunk, 1 if first == 0 else 0, counts, ex) == 0
+        assert counts[0] == 0, ("div_unscaled (dm, nm)", [hex(x) for x in ex[0:8]])
+        assert counts[1] == chunk << 23
+        if first == 0:
+            assert counts[2] == 0, ("v_rcp_f32 scaling (dm, e + 128)", [hex(x) for x in ex[8:16]])
+            assert counts[3] == (1 << 23) * 251

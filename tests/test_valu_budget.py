@@ -80,13 +80,13 @@ FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
     "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 93.0,
                               {**IEEE2, "v_sqrt_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 107.0,
+    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 103.0,
                                {**FAST2, "v_sqrt_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
     "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.0,
                             {**IEEE2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 16, 76.0,
+    "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 16, 72.0,
                              {**FAST2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 16, 101.0,
+    "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 16, 95.0,
                                        {"v_rcp_f32": 3, "v_div_fixup_f32": 0, "v_mul_lo_u32": 4,
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
     "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 147.0,
