@@ -622,7 +622,7 @@ __device__ __forceinline__ float compute_u(const Args &a, const StepCoeffs &k, c
             const float env2 = fma_abs(a.lam1, diff, env1);
             const bool v_ok = wave_all(f_bits(v_new) - 0x0F800000u <= kBf16MaxBits - 0x0F800000u);
             float root;
-            if (__builtin_expect(v_ok, 1)) root = sqrt_rn_normal(v_new);
+            if (__builtin_expect(v_ok, 1)) root = sqrt_rn_positive(v_new);  // v_new in [2^-96, 0x7F7F0000]
             else root = sqrt_cr(__builtin_fmaxf(v_new, 0.0f));
             known = (defect_ok ? kKnownM : 0u) | (v_ok ? kKnownV : 0u);
             return div_envelope(clm, __builtin_fmaf(k.c_sigma, root, env2));

@@ -9,7 +9,8 @@
 //     2 hash inputs per input, 2 x 2^32;
 //   sr_bf16_checked against the reference's bf16 stochastic rounding (prng.rs:137-160, restated here)
 //     with 6 noise values per input (0, 1, 0x7FFF, 0x8000, 0xFFFF and a hash of the input), 6 x 2^32;
-//   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN);
+//   sqrt_rn_normal against the IEEE square root on its domain (x >= 2^-96, +-0, +inf, NaN), and
+//     sqrt_rn_positive on its own (2^-96 <= x <= the largest finite f32);
 //   pack_f16_rtz on every f16 value (and the canonical NaNs) against f32 -> f16 RNE, 2^16;
 //   sr_f16_add + pack_f16_rtz against the reference's fp16 stochastic rounding (prng.rs:98-130,
 //     restated here) on every input of its domain (sr_f16_domain) with 6 noise values per input (0, 1, 0xFFF,
@@ -109,7 +110,7 @@ __device__ void record(unsigned long long *count, uint32_t *ex, uint32_t input) 
 // Counters: [0] f32->f16 mismatches, [1] f16->f32 mismatches other than quietened signalling
 // NaNs, [2] quietened signalling NaNs (same sign), [3] sqrt_rn mismatches (two NaNs are equal),
 // [4] xor_fold16 mismatches, [5] sr_fp16_val (input, either hash input), [6] sr_bf16_checked
-// (input, any noise), [7] sqrt_rn_normal on its domain, [8] pack_f16_rtz, [9] sr_f16_add on its
+// (input, any noise), [7] sqrt_rn_normal and sqrt_rn_positive on their domains, [8] pack_f16_rtz, [9] sr_f16_add on its
 // domain (input, any noise) or a domain test that disagrees with its definition, [10] inputs in
 // the sr_f16_domain
 // (not a mismatch: the size of the domain checked); ex[8 * c + k] holds the first inputs of
@@ -150,6 +151,8 @@ __global__ void check_2_32(uint32_t base, unsigned long long *out, uint32_t *ex)
     if (!(x < 0x1p-96f) || x == 0.0f) {
         const uint32_t n = __float_as_uint(lv::sqrt_rn_normal(x));
         if (n != s_ref && !(is_nan(n) && is_nan(s_ref))) record(&out[7], ex + 56, i);
+        if (x >= 0x1p-96f && x <= 0x1.fffffep127f && __float_as_uint(lv::sqrt_rn_positive(x)) != s_ref)
+            record(&out[7], ex + 56, i);
     }
 }
 

@@ -14,7 +14,9 @@ on every input (the check program is tests/gpu_checks/exact_check.hip):
 * sr_bf16_checked (one integer add, with the out-of-range and NaN inputs replaced first when a
   lane of the wave has one) against the reference's integer recipe (prng.rs:137-160): all 2^32
   inputs x 6 noise values;
-* sqrt_rn_normal (no rescaling) against the IEEE square root on every input of its domain;
+* sqrt_rn_normal (v_rsq_f32 and one correction, no rescaling) against the IEEE square root on
+  every input of its domain, and sqrt_rn_positive (the same without its zero, infinity and NaN
+  select) on every input from 2^-96 to the largest finite f32;
 * pack_f16_rtz against f32 -> f16 RNE on every finite f16 value and the canonical NaNs (the
   reference's fp16 quantisation never yields an infinity);
 * sr_f16_add + pack_f16_rtz (the integer add and round-toward-zero pack) against the reference's
@@ -67,7 +69,7 @@ def test_exact_helpers_on_every_input():
     assert counts[4] == 0, ("xor_fold16", [hex(x) for x in ex[32:40]])
     assert counts[5] == 0, ("sr_fp16_val", [hex(x) for x in ex[40:48]])
     assert counts[6] == 0, ("sr_bf16_checked", [hex(x) for x in ex[48:56]])
-    assert counts[7] == 0, ("sqrt_rn_normal", [hex(x) for x in ex[56:64]])
+    assert counts[7] == 0, ("sqrt_rn_normal / sqrt_rn_positive", [hex(x) for x in ex[56:64]])
     assert counts[8] == 0, ("pack_f16_rtz", [hex(x) for x in ex[64:72]])
     assert counts[9] == 0, ("sr_f16_add", [hex(x) for x in ex[72:80]])
     # domain size, sampled where the low 16 bits are zero: per sign, the zero and the multiples of

@@ -66,7 +66,8 @@ def issue_units(op: str) -> float:
 # reference's arithmetic needs on the path: every division has one v_rcp_f32 (the IEEE sequence,
 # which also ends in one v_div_fixup_f32, or in the 16-bit-state kernels its unscaled form under a
 # wave-uniform range test, with no fixup on the hot path), a correctly rounded root one
-# v_sqrt_f32, a hashed (stochastically rounded) stream two v_mul_lo_u32, and a stored fp16 value
+# v_rsq_f32 (its one-correction form), a hashed (stochastically rounded) stream two v_mul_lo_u32,
+# and a stored fp16 value
 # half a v_cvt_pkrtz_f16_f32 (two per pack). A walk that skipped real work (a branch the code
 # never takes) would miss one of them. Stochastic rounding to bf16 or fp16 is one integer add on
 # the path (the v_cvt_sr_bf16_f32 / v_cvt_sr_f16_f32 converters take about 3 times its issue
@@ -78,10 +79,10 @@ def issue_units(op: str) -> float:
 IEEE2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 2}
 FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
-    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 93.0,
-                              {**IEEE2, "v_sqrt_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 103.0,
-                               {**FAST2, "v_sqrt_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
+    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 90.5,
+                              {**IEEE2, "v_rsq_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
+    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 98.0,
+                               {**FAST2, "v_rsq_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
     "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.0,
                             {**IEEE2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
     "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 16, 72.0,
@@ -89,15 +90,15 @@ KERNELS = {
     "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 16, 95.0,
                                        {"v_rcp_f32": 3, "v_div_fixup_f32": 0, "v_mul_lo_u32": 4,
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
-    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 147.0,
-                     {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_sqrt_f32": 2, "v_mul_lo_u32": 0}),
-    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 99.0,
-                               {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_sqrt_f32": 1, "v_mul_lo_u32": 0}),
+    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 141.5,
+                     {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_rsq_f32": 2, "v_mul_lo_u32": 0}),
+    "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 96.5,
+                               {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_rsq_f32": 1, "v_mul_lo_u32": 0}),
 }
 
 CATEGORIES = [
     ("IEEE division steps", r"v_div_scale|v_rcp_f32|v_div_fmas|v_div_fixup"),
-    ("sqrt", r"v_sqrt_f32"),
+    ("root (v_rsq_f32 or v_sqrt_f32)", r"v_rsq_f32|v_sqrt_f32"),
     ("hash multiply", r"v_mul_lo_u32"),
     ("conversion (SR, f16)", r"v_cvt_"),
     ("compare", r"v_cmp"),
