@@ -1538,7 +1538,8 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
     const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
     const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
     // Workgroups are dispatched to the XCDs round-robin (block b runs on XCD b mod X). Map them so
-    // that each XCD streams one contiguous range of units (measured ~1% faster than b -> b).
+    // that each XCD streams one contiguous range of units, or, where the host passes X = 1, block
+    // b on unit b (which launches take which mapping: launch() in luminav_hip.hip).
     // Every block is short-lived, so its prologue is on the critical path: b / X comes from the
     // host's reciprocal (exact for b < 2^23 and X <= 64) instead of an integer division, which
     // measured 1.3% of the cfg5 step.
