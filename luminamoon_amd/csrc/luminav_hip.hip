@@ -330,7 +330,7 @@ static void call_needs(const lv_config *cfg, const lv_tensor *T, int count, uint
     for (int i = 0; i < count; i++) {
         if (T[i].numel == 0) continue;
         active++;
-        const uint64_t u = units_of(T[i].numel, kHalf);
+        const uint64_t u = units_of(T[i].numel, kMinUnitElems);
         units += u;
         slots += table_slots_of(u);
     }
@@ -599,7 +599,7 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
         args.piece_units = grid;
         args.xcd_q = grid / args.xcds;
         args.xcd_r = grid % args.xcds;
-        int rc = launch_one(fn, args, grid, kThreads, stream);
+        int rc = launch_one(fn, args, grid, lv::unit_threads(mode, pt, st, pass, args.flags), stream);
         if (rc != LV_STATUS_SUCCESS) return rc;
         if (radial) {
             uint32_t chunks = 0;
@@ -754,7 +754,7 @@ static int prepare_call(const lv_config *cfg, const lv_tensor *tensors, int coun
         if (T.param_dtype < 0 || T.param_dtype > 2 || T.grad_dtype < 0 || T.grad_dtype > 2 || T.state_dtype < 0 ||
             T.state_dtype > 2)
             return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: invalid dtype code", i);
-        if (T.numel > (uint64_t)0xFFFFFFFFull * kHalf)
+        if (T.numel > (uint64_t)0xFFFFFFFFull * kMinUnitElems)
             return fail(LV_STATUS_INVALID_CONFIG, "tensor %d: too many elements", i);
         // worker.rs:95-98 and worker.rs:153-156: an fp32 param aliasing its master has none.
         const bool mp_present = T.master_param && !(T.param_dtype == LV_DTYPE_F32 && (void *)T.master_param == T.param);

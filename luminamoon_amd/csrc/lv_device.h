@@ -42,9 +42,9 @@ constexpr int kMaxDesc = 48;                 // tensors per inline launch (kerne
 constexpr uint32_t kSlots = 64;              // cautious-count slots per tensor (unit launches)
 constexpr uint32_t kSlotWords = kSlots + 1;  // + one fold word per tensor
 constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-byte segment
-// Slot word: mask count << kTicketBits | blocks that reported. A tensor has < 2^32 units of
-// >= 1024 elements and at most 2^42 elements, so a slot sees <= 2^26 blocks (27 bits) and
-// counts <= 2^36 elements (37 bits). Fold word: count << 7 | slots completed (<= 64).
+// Slot word: mask count << kTicketBits | blocks that reported. A tensor has < 2^32 units (of
+// >= 256 elements; at most 2^40 elements), so a slot sees <= 2^26 blocks (27 bits) and counts
+// <= 2^36 elements (37 bits). Fold word: count << 7 | slots completed (<= 64).
 constexpr int kTicketBits = 27;
 constexpr int kFoldBits = 7;
 constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
@@ -98,11 +98,26 @@ constexpr int unit_min_blocks(int mode, int pt, int st, int pass, uint32_t flags
     return unit_subs(mode, pt, st, pass, flags) > 1 ? 8 : 1;
 }
 
+// Threads per block of the unit kernel for this mode, dtypes, pass and flag word (the launch's
+// word; the run-time-flag kernels have 256). The steady CLM step in f32 with the reference
+// defaults runs one-wave blocks (units of 256 elements): in one process on the same buffers they
+// ran 0.938-0.966x of 256-thread blocks (cfg3, and a 1e9-element bucket). The other kernels keep
+// 256: T1 with f32 state ran 1.040-1.046x with one-wave blocks (cfg4), and the T2 headline
+// (cfg5) 1.014x.
+constexpr int unit_threads(int mode, int pt, int st, int pass, uint32_t flags) {
+    return (mode == LV_BUFFER_DUAL && pt == LV_DTYPE_F32 && st == LV_DTYPE_F32 && pass == kFused &&
+            flags == static_flags(pt, pass))
+               ? 64
+               : kThreads;
+}
+
 // Elements per work unit of a unit launch.
 constexpr uint32_t unit_elems(int mode, int pt, int st, int pass, uint32_t flags) {
-    return kHalf * (uint32_t)unit_halves(mode, pt, st) * (uint32_t)unit_subs(mode, pt, st, pass, flags);
+    return 4u * (uint32_t)unit_threads(mode, pt, st, pass, flags) * (uint32_t)unit_halves(mode, pt, st) *
+           (uint32_t)unit_subs(mode, pt, st, pass, flags);
 }
 constexpr uint32_t kMaxUnitElems = 4 * kHalf;
+constexpr uint32_t kMinUnitElems = 4 * 64;  // one-wave blocks, one group of 4 per lane
 
 // One tensor of a launch (80 bytes): in the kernel arguments (inline launches) or in the
 // workspace (table launches).
@@ -1074,14 +1089,15 @@ __device__ __forceinline__ unsigned long long wave_sum(unsigned long long x) {
 // Block-wide sums in a fixed order (lanes by butterfly, then the 4 waves in order); the result
 // is valid in thread 0, which reads the shared slots after the barrier: a second call by the
 // same block needs a barrier in between.
+template <int TPB>
 struct BlockSums {
-    double su[kThreads / 64];
-    double sp[kThreads / 64];
-    unsigned long long cnt[kThreads / 64];
+    double su[TPB / 64];
+    double sp[TPB / 64];
+    unsigned long long cnt[TPB / 64];
 };
 
-template <typename C>
-__device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp, C &cnt) {
+template <int TPB, typename C>
+__device__ __forceinline__ void block_sums(BlockSums<TPB> &sh, double &su, double &sp, C &cnt) {
     su = wave_sum(su);
     sp = wave_sum(sp);
     cnt = wave_sum(cnt);
@@ -1097,7 +1113,7 @@ __device__ __forceinline__ void block_sums(BlockSums &sh, double &su, double &sp
         sp = sh.sp[0];
         cnt = (C)sh.cnt[0];
 #pragma unroll
-        for (int k = 1; k < kThreads / 64; k++) {
+        for (int k = 1; k < TPB / 64; k++) {
             su += sh.su[k];
             sp += sh.sp[k];
             cnt += (C)sh.cnt[k];
@@ -1484,7 +1500,7 @@ constexpr uint32_t lane_split(int H, uint32_t FL) {
 // 16-byte alignment (element by element, coalesced across the wave), or inactive ranges
 // (`cover`: 0 none, 1 partly, 2 wholly; `first` the first range that ends after ub). cnt
 // accumulates the lane's own count.
-template <int MODE, int PT, int ST, int PASS, int H, uint32_t HS>
+template <int MODE, int PT, int ST, int PASS, int H, uint32_t HS, int TPB>
 __device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, const View &tv, uint32_t flags, bool radial,
                                                uint64_t ub, int cover, uint32_t first, uint32_t &cnt, double &su,
                                                double &sp) {
@@ -1505,7 +1521,7 @@ __device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, con
     } else if (cover == 0) {
 #pragma unroll 1
         for (uint32_t j = 0; j < 4u * H; j++) {
-            const uint64_t e = ub + (uint64_t)j * kThreads + threadIdx.x;
+            const uint64_t e = ub + (uint64_t)j * TPB + threadIdx.x;
             if (e < tv.n) scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, e, e + 1, cnt, su, sp);
         }
     } else if (cover != 2 || radial) {
@@ -1515,7 +1531,7 @@ __device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, con
     }
 }
 
-// Unit launch: each block updates exactly one work unit (1024, 2048 or 4096 elements: unit_elems) and
+// Unit launch: each block updates exactly one work unit (256, 1024, 2048 or 4096 elements: unit_elems) and
 // exits.
 // The hardware keeps every CU full with fresh blocks, so the loads of some blocks overlap the
 // arithmetic of others without a software pipeline; on MI355X this launch shape streams HBM
@@ -1531,9 +1547,11 @@ __device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, con
 // which case every option test folds at compile time and the per-element code is straight-line.
 // TABLE: the tensor table is in device memory (a.dtab) and the heads in a.ubegin.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL, bool TABLE>
-__global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, FL)) unit_kernel(const Args a) {
+__global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL), unit_min_blocks(MODE, PT, ST, PASS, FL))
+    unit_kernel(const Args a) {
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
-    __shared__ BlockSums sh;
+    constexpr int TPB = unit_threads(MODE, PT, ST, PASS, FL);  // threads per block
+    __shared__ BlockSums<TPB> sh;
 
     const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
     const bool radial = kCounting && (flags & kFRadial);  // squared norms summed in this pass
@@ -1564,7 +1582,8 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
     constexpr int H = unit_halves(MODE, PT, ST);
     constexpr int S = unit_subs(MODE, PT, ST, PASS, FL);
     constexpr uint32_t HS = lane_split(H, FL);
-    constexpr uint64_t kSub = (uint64_t)kHalf * H;  // elements per sub-unit
+    static_assert(H == 1 || TPB == kThreads, "16-bit state splits its lanes at 1024 elements");
+    constexpr uint64_t kSub = 4ull * TPB * H;  // elements per sub-unit
     constexpr uint64_t kUnit = kSub * S;
     // units start at the tensor's first 16-byte aligned element (tv.head > 0: an unaligned view)
     const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit + tv.head;
@@ -1607,7 +1626,7 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
         // its elements still enter the radial norms.
         if (!kCounting && cover == 2 && !(tv.head && unit + 1 == tv.t_end)) return;
         if constexpr (S == 1) {
-            subunit_nonvec<MODE, PT, ST, PASS, H, HS>(a, D, tv, flags, radial, ubase, cover, first, cnt, su, sp);
+            subunit_nonvec<MODE, PT, ST, PASS, H, HS, TPB>(a, D, tv, flags, radial, ubase, cover, first, cnt, su, sp);
         } else {
 #pragma unroll 1
             for (int sub = 0; sub < S; sub++) {
@@ -1615,7 +1634,7 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
                 if (ub >= tv.n) break;
                 uint32_t sfirst = 0;
                 const int scover = D.nskip ? inactive_cover(D, ub, ub + kSub < tv.n ? ub + kSub : tv.n, sfirst) : 0;
-                subunit_nonvec<MODE, PT, ST, PASS, H, HS>(a, D, tv, flags, radial, ub, scover, sfirst, cnt, su, sp);
+                subunit_nonvec<MODE, PT, ST, PASS, H, HS, TPB>(a, D, tv, flags, radial, ub, scover, sfirst, cnt, su, sp);
             }
         }
     }
@@ -1648,7 +1667,7 @@ __global__ void __launch_bounds__(kThreads, unit_min_blocks(MODE, PT, ST, PASS, 
             if (threadIdx.x == 0) {
                 uint32_t tot = 0;
 #pragma unroll
-                for (int k = 0; k < kThreads / 64; k++) tot += (uint32_t)sh.cnt[k];
+                for (int k = 0; k < TPB / 64; k++) tot += (uint32_t)sh.cnt[k];
                 report_count<MODE, PASS, TABLE>(a, D, tv, unit, tot);
             }
         }
@@ -1676,7 +1695,7 @@ __host__ __device__ inline void piece_span(const Args &a, int t, uint32_t ub, ui
 // workspace zero (a later call may use the same bytes as count words).
 template <int MODE, int PASS>
 __global__ void __launch_bounds__(kThreads) fold_kernel(const Args a) {
-    __shared__ BlockSums sh;
+    __shared__ BlockSums<kThreads> sh;
     __shared__ uint32_t last;
     if (a.step_rec && a.step_rec->status != 0) return;  // refused graph step: the unit launch wrote nothing
     const uint32_t ub = a.unit_base, ue = a.unit_base + a.piece_units;

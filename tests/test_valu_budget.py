@@ -90,7 +90,7 @@ KERNELS = {
     "cfg4 T1 fp16, fp16-container m": ("_ZN2lv11unit_kernelILi3ELi2ELi1ELi1ELj603ELb0EEEvNS_4ArgsE", 16, 95.0,
                                        {"v_rcp_f32": 3, "v_div_fixup_f32": 0, "v_mul_lo_u32": 4,
                                         "v_cvt_sr_bf16_f32": 0, "v_cvt_sr_f16_f32": 0, "v_cvt_pkrtz_f16_f32": 0.5}),
-    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 141.5,
+    "cfg3 CLM f32": ("_ZN2lv11unit_kernelILi2ELi0ELi0ELi1ELj75ELb0EEEvNS_4ArgsE", 4, 142.5,
                      {"v_rcp_f32": 4, "v_div_fixup_f32": 4, "v_rsq_f32": 2, "v_mul_lo_u32": 0}),
     "cfg2 TD-CLM f32, table": ("_ZN2lv11unit_kernelILi1ELi0ELi0ELi1ELj75ELb1EEEvNS_4ArgsE", 4, 96.5,
                                {"v_rcp_f32": 3, "v_div_fixup_f32": 3, "v_rsq_f32": 1, "v_mul_lo_u32": 0}),
@@ -218,9 +218,12 @@ def _successors(blocks, k, flags):
 
 def hot_path(path: str, name: str) -> list[str]:
     """Instructions of the cheapest path (in VALU instructions) from the block holding
-    `s_setprio` (1, or 0 in the two-sub-unit kernels) to the first block holding `s_barrier`."""
+    `s_setprio` (1, or 0 in the two-sub-unit kernels) to the first block holding `s_barrier`, or,
+    in a kernel of one-wave blocks (no barrier), the first holding the count report's atomic."""
     lines = open(path).read().split("\n")
     blocks = _blocks(lines, name)
+    marker = ("s_barrier" if any(x.startswith("s_barrier") for _, ins in blocks for x in ins)
+              else "global_atomic_add_x2")
     start = next(n for n, (_, ins) in enumerate(blocks) if any(x.startswith("s_setprio") for x in ins))
     cost = [sum(1 for x in ins if x.startswith("v_")) for _, ins in blocks]
     # Dijkstra over (block, known flags)
@@ -233,7 +236,7 @@ def hot_path(path: str, name: str) -> list[str]:
             continue
         done.add(st)
         n, fl = st
-        if n != start and any(x.startswith("s_barrier") for x in blocks[n][1]):
+        if n != start and any(x.startswith(marker) for x in blocks[n][1]):
             end = st
             break
         flags = _step(blocks[n][1], dict(fl))
@@ -254,7 +257,7 @@ def hot_path(path: str, name: str) -> list[str]:
         if n == start:
             ins = ins[next(i for i, x in enumerate(ins) if x.startswith("s_setprio")):]
         if n == end[0]:
-            ins = ins[:next(i for i, x in enumerate(ins) if x.startswith("s_barrier"))]
+            ins = ins[:next(i for i, x in enumerate(ins) if x.startswith(marker))]
         out.extend(ins)
     return out
 
