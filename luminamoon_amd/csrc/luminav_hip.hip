@@ -319,7 +319,8 @@ static Layout make_layout(char *ws, uint64_t table_slots, uint32_t radial_units)
 
 // What a call needs, from its tensors alone (an upper bound over every class the call forms):
 // table count slots when more than kMaxDesc tensors step, and radial unit records up to one piece
-// when the config uses the radial bound. Units are counted at the smallest unit size.
+// when the config uses the radial bound. Units are counted at the smallest unit size of table and
+// radial launches, 1024 elements (the one-wave blocks of unit_threads are inline launches only).
 static void call_needs(const lv_config *cfg, const lv_tensor *T, int count, uint64_t &table_slots, uint32_t &radial_units) {
     table_slots = 0;
     radial_units = 0;
@@ -330,7 +331,7 @@ static void call_needs(const lv_config *cfg, const lv_tensor *T, int count, uint
     for (int i = 0; i < count; i++) {
         if (T[i].numel == 0) continue;
         active++;
-        const uint64_t u = units_of(T[i].numel, kMinUnitElems);
+        const uint64_t u = units_of(T[i].numel, kHalf);
         units += u;
         slots += table_slots_of(u);
     }
@@ -599,7 +600,7 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
         args.piece_units = grid;
         args.xcd_q = grid / args.xcds;
         args.xcd_r = grid % args.xcds;
-        int rc = launch_one(fn, args, grid, lv::unit_threads(mode, pt, st, pass, args.flags), stream);
+        int rc = launch_one(fn, args, grid, lv::unit_threads(mode, pt, st, pass, args.flags, table), stream);
         if (rc != LV_STATUS_SUCCESS) return rc;
         if (radial) {
             uint32_t chunks = 0;
@@ -796,7 +797,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             Args args;
             fill_args_common(args, cfg, h, bound);
             args.step_rec = rec;
-            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags);
+            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags, true);
             std::vector<TDesc> &tab = *tab_buf;
             if (tab.size() < (size_t)n) tab.resize((size_t)n);
             uint64_t units = 0, slot = 0;
@@ -839,7 +840,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             Args args;
             fill_args_common(args, cfg, h, bound);
             args.step_rec = rec;
-            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags);
+            const uint32_t unit_elems = lv::unit_elems(cfg->buffer, h.pt, h.st, h.pass, args.flags, false);
             args.ndesc = end - begin;
             uint64_t units = 0;
             for (int k = begin; k < end; k++) {

@@ -98,22 +98,23 @@ constexpr int unit_min_blocks(int mode, int pt, int st, int pass, uint32_t flags
     return unit_subs(mode, pt, st, pass, flags) > 1 ? 8 : 1;
 }
 
-// Threads per block of the unit kernel for this mode, dtypes, pass and flag word (the launch's
-// word; the run-time-flag kernels have 256). The steady CLM step in f32 with the reference
-// defaults runs one-wave blocks (units of 256 elements): in one process on the same buffers they
-// ran 0.938-0.966x of 256-thread blocks (cfg3, and a 1e9-element bucket). The other kernels keep
-// 256: T1 with f32 state ran 1.040-1.046x with one-wave blocks (cfg4), and the T2 headline
-// (cfg5) 1.014x.
-constexpr int unit_threads(int mode, int pt, int st, int pass, uint32_t flags) {
-    return (mode == LV_BUFFER_DUAL && pt == LV_DTYPE_F32 && st == LV_DTYPE_F32 && pass == kFused &&
+// Threads per block of the unit kernel for this mode, dtypes, pass, flag word (the launch's word;
+// the run-time-flag kernels have 256) and launch kind. The steady inline CLM step in f32 with the
+// reference defaults runs one-wave blocks (units of 256 elements): in one process on the same
+// buffers they ran 0.938-0.966x of 256-thread blocks (cfg3, and a 1e9-element bucket). The other
+// kernels keep 256: T1 with f32 state ran 1.040-1.046x with one-wave blocks (cfg4), the T2
+// headline (cfg5) 1.014x, and TD-CLM's table launch of 64 tensors (cfg2) 1.03x (its inline
+// buckets 0.980-0.986x).
+constexpr int unit_threads(int mode, int pt, int st, int pass, uint32_t flags, bool table) {
+    return (!table && mode == LV_BUFFER_DUAL && pt == LV_DTYPE_F32 && st == LV_DTYPE_F32 && pass == kFused &&
             flags == static_flags(pt, pass))
                ? 64
                : kThreads;
 }
 
 // Elements per work unit of a unit launch.
-constexpr uint32_t unit_elems(int mode, int pt, int st, int pass, uint32_t flags) {
-    return 4u * (uint32_t)unit_threads(mode, pt, st, pass, flags) * (uint32_t)unit_halves(mode, pt, st) *
+constexpr uint32_t unit_elems(int mode, int pt, int st, int pass, uint32_t flags, bool table) {
+    return 4u * (uint32_t)unit_threads(mode, pt, st, pass, flags, table) * (uint32_t)unit_halves(mode, pt, st) *
            (uint32_t)unit_subs(mode, pt, st, pass, flags);
 }
 constexpr uint32_t kMaxUnitElems = 4 * kHalf;
@@ -1547,10 +1548,10 @@ __device__ __forceinline__ void subunit_nonvec(const Args &a, const Desc &D, con
 // which case every option test folds at compile time and the per-element code is straight-line.
 // TABLE: the tensor table is in device memory (a.dtab) and the heads in a.ubegin.
 template <int MODE, int PT, int ST, int PASS, uint32_t FL, bool TABLE>
-__global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL), unit_min_blocks(MODE, PT, ST, PASS, FL))
+__global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL, TABLE), unit_min_blocks(MODE, PT, ST, PASS, FL))
     unit_kernel(const Args a) {
     constexpr bool kCounting = (PASS == kFused || PASS == kCount);
-    constexpr int TPB = unit_threads(MODE, PT, ST, PASS, FL);  // threads per block
+    constexpr int TPB = unit_threads(MODE, PT, ST, PASS, FL, TABLE);  // threads per block
     __shared__ BlockSums<TPB> sh;
 
     const uint32_t flags = (FL & kFDynamic) ? a.flags : FL;
