@@ -83,7 +83,7 @@ PMC_TRAFFIC = {
     (4, "coordinate", "param", "none", "f16"): dict(kernel="lv::unit_kernel<3, 2, 1, 1, 603u, false>",
                                                     fetch_kib=2793131.0000, write_kib=3730812.5938, **_PROBE),
     (3, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<2, 0, 0, 1, 75u, false>",
-                                                fetch_kib=965684.1562, write_kib=1451873.4062, **_PROBE),
+                                                fetch_kib=966654.7578, write_kib=1463180.2812, **_PROBE),
     (2, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<1, 0, 0, 1, 75u, true>",
                                                 fetch_kib=20746.9141, write_kib=27580.0938, **_PROBE),
 }
