@@ -564,6 +564,7 @@ static int order_after(WsOrder *o, hipStream_t stream) {
 // ------------------------------------------------------------------ launches
 
 // Unit launches of one class over args.total_units units, in pieces of at most kMaxGrid blocks
+// (kMaxGridIdentity when block b maps to unit b)
 // (`radial_piece` for radial counting launches, the unit records of one piece; LV_MAX_GRID_BLOCKS
 // lowers the cap, so tests can split small launches). A counting launch folds its counts in its
 // last blocks; a radial one runs fold_kernel after every piece.
@@ -573,21 +574,29 @@ static int launch(Args &args, int mode, int pt, int st, int pass, hipStream_t st
     if (table && radial) return fail(LV_STATUS_INVALID_CONFIG, "radial counting launches are inline");
     if (args.total_units == 0) return LV_STATUS_SUCCESS;
     // The block mapping. XCD-contiguous (each XCD streams one contiguous eighth of the units) is
-    // the default. f32-state launches of up to kIdentityMapUnits blocks map block b to unit b
-    // instead (xcds = 1): against the XCD-contiguous mapping, in one process on the same buffers,
-    // they ran 0.5-3.3% faster (cfg2's 64-tensor table launch, cfg3, cfg4, and T2 buckets of
-    // 2.5e8-2e9 elements), while larger ones (T1 at 4e9, T2 at 3.5e9-6.7e9 elements) ran 1.2-2.9%
-    // slower, and 16-bit-state launches ran level to 4.6% slower. Results are the same either way:
-    // units are independent and the count is exact in any order.
-    const bool identity_map = st == LV_DTYPE_F32 && !radial && args.total_units <= kIdentityMapUnits;
+    // the default. f32-state launches of one-wave blocks, and of up to kIdentityMapUnits 256-thread
+    // blocks, map block b to unit b instead (xcds = 1). Against the XCD-contiguous mapping, in one
+    // process on the same buffers: 256-thread f32-state launches ran 0.5-3.3% faster (cfg2's
+    // 64-tensor table launch, cfg3, cfg4, and T2 buckets of 2.5e8-2e9 elements) and larger ones
+    // 1.2-2.9% slower (T1 at 4e9, T2 at 3.5e9-6.7e9 elements); one-wave T2 blocks ran 3-4% faster
+    // at 1e9 and 3.5e9 elements and 2% faster at 6.7e9; 16-bit-state launches ran level to 4.6%
+    // slower. Results are the same either way: units are independent and the count is exact in
+    // any order.
+    const bool identity_map = st == LV_DTYPE_F32 && !radial &&
+                              (lv::unit_threads(mode, pt, st, pass, args.flags, table) < kThreads ||
+                               args.total_units <= kIdentityMapUnits);
     args.xcds = identity_map ? 1u : device_xcds();
     // b / X == (b * recip) >> 40 for b < 2^23 = kMaxGrid and X <= 64: recip exceeds 2^40 / X by at
     // most 1, so the product exceeds b * 2^40 / X by less than b < 2^23, i.e. by < 2^-17 after the
     // shift, while the fraction of b / X is at most 1 - 1/X <= 1 - 2^-6.
+    // With X = 1 (identity-mapped launches) the kernel takes unit = base + b and skips this
+    // product, which would overflow 64 bits from b = 2^24 (recip = 2^40 + 1).
     static_assert(kMaxGrid <= (1u << 23), "the reciprocal is exact for grids up to 2^23 blocks");
     static_assert(kRadialPiece <= kMaxGrid, "a radial piece is one unit launch");
     args.xcd_recip = ((uint64_t)1 << 40) / args.xcds + 1;
-    uint32_t max_grid = radial ? radial_piece : kMaxGrid;
+    // identity-mapped launches are of one-wave blocks or of at most kIdentityMapUnits blocks
+    static_assert((uint64_t)kMaxGridIdentity * 64 < (1ull << 32) && kIdentityMapUnits <= kMaxGrid, "grid x threads < 2^32");
+    uint32_t max_grid = radial ? radial_piece : (identity_map ? kMaxGridIdentity : kMaxGrid);
     if (const char *e = std::getenv("LV_MAX_GRID_BLOCKS")) {
         long v = std::atol(e);
         if (v > 0 && (uint32_t)v < max_grid) max_grid = (uint32_t)v;

@@ -48,6 +48,9 @@ constexpr uint32_t kSlotStride = 8;          // u64 per slot: one slot per 64-by
 constexpr int kTicketBits = 27;
 constexpr int kFoldBits = 7;
 constexpr uint32_t kMaxGrid = 1u << 23;      // blocks per unit launch (grid x 256 threads < 2^32)
+// Blocks per identity-mapped unit launch (one XCD: b / 1 is exact for any b). One-wave blocks:
+// 2^25 x 64 threads < 2^32, so a cfg5 step (26.3M one-wave units) is one launch.
+constexpr uint32_t kMaxGridIdentity = 1u << 25;
 // Radial counting launches: units per piece (one workspace record each: 2 doubles + a u32 count),
 // and unit records one fold block sums into a chunk record.
 constexpr uint32_t kRadialPiece = 1u << 22;
@@ -99,17 +102,17 @@ constexpr int unit_min_blocks(int mode, int pt, int st, int pass, uint32_t flags
 }
 
 // Threads per block of the unit kernel for this mode, dtypes, pass, flag word (the launch's word;
-// the run-time-flag kernels have 256) and launch kind. The steady inline CLM step in f32 with the
-// reference defaults runs one-wave blocks (units of 256 elements): in one process on the same
-// buffers they ran 0.938-0.966x of 256-thread blocks (cfg3, and a 1e9-element bucket). The other
-// kernels keep 256: T1 with f32 state ran 1.040-1.046x with one-wave blocks (cfg4), the T2
-// headline (cfg5) 1.014x, and TD-CLM's table launch of 64 tensors (cfg2) 1.03x (its inline
-// buckets 0.980-0.986x).
+// the run-time-flag kernels have 256) and launch kind. Two steady inline steps with f32 state and
+// the reference defaults run one-wave blocks (units of 256 elements), which launch() maps block b
+// to unit b. In one process on the same buffers, against 256-thread blocks:
+// - CLM in f32 (cfg3's kernel): 0.938-0.966x (cfg3, and a 1e9-element bucket);
+// - T2 with bf16 params (the headline's kernel): 0.966x at 1e9 elements, 0.959x at 3.5e9, and
+//   0.992-1.005x at cfg5's 6.7e9 (five processes).
+// The other kernels keep 256: T1 with f32 state ran 1.040-1.046x with one-wave blocks (cfg4),
+// TD-CLM's table launch of 64 tensors (cfg2) 1.03x (its inline buckets 0.980-0.986x).
 constexpr int unit_threads(int mode, int pt, int st, int pass, uint32_t flags, bool table) {
-    return (!table && mode == LV_BUFFER_DUAL && pt == LV_DTYPE_F32 && st == LV_DTYPE_F32 && pass == kFused &&
-            flags == static_flags(pt, pass))
-               ? 64
-               : kThreads;
+    const bool one_wave = (mode == LV_BUFFER_DUAL && pt == LV_DTYPE_F32) || (mode == LV_BUFFER_T2 && pt == LV_DTYPE_BF16);
+    return (!table && one_wave && st == LV_DTYPE_F32 && pass == kFused && flags == static_flags(pt, pass)) ? 64 : kThreads;
 }
 
 // Elements per work unit of a unit launch.
@@ -1562,10 +1565,17 @@ __global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL, TABLE), u
     // Every block is short-lived, so its prologue is on the critical path: b / X comes from the
     // host's reciprocal (exact for b < 2^23 and X <= 64) instead of an integer division, which
     // measured 1.3% of the cfg5 step.
+    // With one XCD the mapping is b itself: an identity-mapped launch has up to kMaxGridIdentity
+    // = 2^25 blocks, past the reciprocal's range (b * recip overflows 64 bits from b = 2^24).
     const uint32_t b = blockIdx.x;
-    const uint32_t i = (uint32_t)(((uint64_t)b * a.xcd_recip) >> 40);
-    const uint32_t x = b - i * a.xcds;
-    const uint32_t unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
+    uint32_t unit;
+    if (a.xcds == 1) {
+        unit = a.unit_base + b;
+    } else {
+        const uint32_t i = (uint32_t)(((uint64_t)b * a.xcd_recip) >> 40);
+        const uint32_t x = b - i * a.xcds;
+        unit = a.unit_base + x * a.xcd_q + (x < a.xcd_r ? x : a.xcd_r) + i;
+    }
     const int t = find_tensor<TABLE>(a, unit);
     Desc table_d;
     if constexpr (TABLE) table_d = table_desc(a, t);

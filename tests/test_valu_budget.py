@@ -79,7 +79,7 @@ def issue_units(op: str) -> float:
 IEEE2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 2}
 FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
-    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 90.5,
+    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 91.0,
                               {**IEEE2, "v_rsq_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
     "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 98.0,
                                {**FAST2, "v_rsq_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
