@@ -73,7 +73,7 @@ WORKLOADS = {
 _PROBE = dict(probe_bytes=float(1 << 31), probe_fetch_kib=1048582.5, probe_write_kib=2097152.0)
 PMC_TRAFFIC = {
     (5, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 0, 1, 331u, false>",
-                                                fetch_kib=39495825.9688, write_kib=66010492.8750, **_PROBE),
+                                                fetch_kib=39552260.4375, write_kib=66627416.6250, **_PROBE),
     (5, "coordinate", "param", "none", ""): dict(kernel="lv::unit_kernel<4, 1, 1, 1, 331u, false>",
                                                  fetch_kib=26327611.5625, write_kib=39585768.0000, **_PROBE),
     (4, "coordinate", "fp32", "none", ""): dict(kernel="lv::unit_kernel<3, 1, 0, 1, 331u, false>",
