@@ -72,10 +72,11 @@ def test_cpu_baseline_with_master_and_fp16():
 def test_pmc_traffic_is_the_algorithmic_bytes_plus_the_count_atomics():
     algorithmic = bench.N5 * 22
     traffic = bench.pmc_traffic_bytes(5)
-    blocks = bench.N5 // 1024
-    assert abs(traffic - (algorithmic + 32 * blocks)) / algorithmic < 5e-4
+    blocks = bench.N5 // 256  # one-wave blocks of 256 elements
+    # each count atomic writes 32 B (and its return reads a few more)
+    assert abs(traffic - (algorithmic + 32 * blocks)) / algorithmic < 1.5e-3
     # the other measured variants: within 0.5% of the algorithmic bytes (+ 32 B per count atomic)
-    for key, (bpp, unit) in {(3, "coordinate", "fp32", "none", ""): (28, 1024),
+    for key, (bpp, unit) in {(3, "coordinate", "fp32", "none", ""): (28, 256),
                              (4, "coordinate", "fp32", "none", ""): (14, 1024),
                              (4, "coordinate", "param", "none", ""): (10, 2048),
                              (4, "coordinate", "param", "none", "f16"): (10, 2048),
