@@ -659,11 +659,40 @@ static bool head_for(const lv_tensor &T, const Item &it, bool dual, uint32_t ali
     return false;
 }
 
-static bool vector_head(const lv_tensor &T, const Item &it, bool dual, uint32_t &head) {
+// For kernels of one-wave blocks (units of kMinUnitElems elements): the smallest h < kMinUnitElems
+// at which every stream starts a whole unit of its own element size, that is at an element index
+// (address / element size) that is a multiple of kMinUnitElems, so each block moves the same
+// whole 512-byte (16-bit) and 1 KiB (f32) pieces of its streams as in an aligned tensor. A view
+// at +k elements of aligned buffers has h = 256 - k. Against the 128-byte-line head, a 2^27-element
+// T2 view at +1, +33 and +63 elements ran 1.033-1.037x the aligned view in one-wave blocks.
+static bool unit_head(const lv_tensor &T, const Item &it, bool dual, uint32_t &head) {
+    struct Stream {
+        uintptr_t addr;
+        int bytes;
+    } st[5];
+    int ns = 0;
+    st[ns++] = {(uintptr_t)T.param, dtype_bytes(it.pt)};
+    st[ns++] = {(uintptr_t)T.grad, dtype_bytes(it.gt)};
+    st[ns++] = {(uintptr_t)T.exp_avg, dtype_bytes(it.st)};
+    if (dual) st[ns++] = {(uintptr_t)T.exp_avg_sq, dtype_bytes(it.st)};
+    if (it.master) st[ns++] = {(uintptr_t)T.master_param, 4};
+    uint64_t e = 0;
+    for (int k = 0; k < ns; k++) {
+        if (st[k].addr % (uintptr_t)st[k].bytes) return false;
+        const uint64_t ek = (uint64_t)(st[k].addr / (uintptr_t)st[k].bytes) % kMinUnitElems;
+        if (k && ek != e) return false;
+        e = ek;
+    }
+    head = (uint32_t)((kMinUnitElems - e) % kMinUnitElems);
+    return (uint64_t)head < T.numel;
+}
+
+static bool vector_head(const lv_tensor &T, const Item &it, bool dual, uint32_t unit_elems, uint32_t &head) {
+    if (unit_elems == kMinUnitElems && unit_head(T, it, dual, head)) return true;
     return head_for(T, it, dual, 128u, 64u, head) || head_for(T, it, dual, 16u, 8u, head);
 }
 
-static void fill_desc(Desc &D, const lv_tensor &T, const Item &it, bool dual) {
+static void fill_desc(Desc &D, const lv_tensor &T, const Item &it, bool dual, uint32_t unit_elems) {
     D.p = T.param;
     D.g = T.grad;
     D.m = T.exp_avg;
@@ -676,7 +705,7 @@ static void fill_desc(Desc &D, const lv_tensor &T, const Item &it, bool dual) {
     D.ibase = (uint32_t)T.index_base;
     D.nskip = (uint32_t)T.n_inactive;  // < 2^24 (prepare_call)
     uint32_t head = 0;
-    D.vec = vector_head(T, it, dual, head) ? 1u : 0u;
+    D.vec = vector_head(T, it, dual, unit_elems, head) ? 1u : 0u;
     D.head = head;
     D.skip = T.n_inactive ? T.inactive : nullptr;
 }
@@ -814,7 +843,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
                 const lv_tensor &T = tensors[items[begin + k].idx];
                 TDesc &E = tab[(size_t)k];
                 std::memset(&E, 0, sizeof E);
-                fill_desc(E.d, T, items[begin + k], dual);
+                fill_desc(E.d, T, items[begin + k], dual, unit_elems);
                 const uint64_t u = desc_units(E.d, unit_elems);
                 E.d.unit_begin = (uint32_t)units;
                 units += u;
@@ -855,7 +884,7 @@ static int run_call(const lv_config *cfg, const lv_tensor *tensors, Item *items,
             for (int k = begin; k < end; k++) {
                 Desc &D = args.d[k - begin];
                 const lv_tensor &T = tensors[items[k].idx];
-                fill_desc(D, T, items[k], dual);
+                fill_desc(D, T, items[k], dual, unit_elems);
                 D.unit_begin = (uint32_t)units;
                 units += desc_units(D, unit_elems);
                 if (units > 0xFFFFFFFFull) return fail(LV_STATUS_INVALID_CONFIG, "too many work units in one launch");

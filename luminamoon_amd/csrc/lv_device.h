@@ -1598,6 +1598,16 @@ __global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL, TABLE), u
     constexpr uint64_t kUnit = kSub * S;
     // units start at the tensor's first 16-byte aligned element (tv.head > 0: an unaligned view)
     const uint64_t ubase = (uint64_t)(unit - tv.t_begin) * kUnit + tv.head;
+    // Whether this block also takes the head. One-wave kernels (identity-mapped, heads of up to 255
+    // elements) use the tensor's first unit, whose block starts early in the launch: with the last
+    // unit, whose head round trips fall on the launch's tail, a 2^27-element T2 view at +1
+    // element ran 1.030x the aligned view, with the first 1.022x (and with the head spread over
+    // the first units' blocks, 64 elements each, 1.036x). The others keep the last unit, which
+    // also keeps the radial sums' fold order. Only after open_step: tv.t_end is set there.
+    const auto takes_head = [&]() {
+        if constexpr (TPB == kThreads) return tv.head && unit + 1u == tv.t_end;
+        else return tv.head && unit == tv.t_begin;
+    };
     int cover = 0;
     uint32_t first = 0;
     if (D.nskip) cover = inactive_cover(D, ubase, ubase + kUnit < tv.n ? ubase + kUnit : tv.n, first);
@@ -1635,7 +1645,7 @@ __global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL, TABLE), u
         }
         // A wholly inactive unit has a zero gradient (its mask count is 0) and writes nothing;
         // its elements still enter the radial norms.
-        if (!kCounting && cover == 2 && !(tv.head && unit + 1 == tv.t_end)) return;
+        if (!kCounting && cover == 2 && !takes_head()) return;
         if constexpr (S == 1) {
             subunit_nonvec<MODE, PT, ST, PASS, H, HS, TPB>(a, D, tv, flags, radial, ubase, cover, first, cnt, su, sp);
         } else {
@@ -1649,15 +1659,23 @@ __global__ void __launch_bounds__(unit_threads(MODE, PT, ST, PASS, FL, TABLE), u
             }
         }
     }
-    // An unaligned view's head [0, tv.head) (its streams are aligned from element tv.head on): the
-    // block of the tensor's last unit takes it, one element per thread, after its unit.
+    // An unaligned view's head [0, tv.head) (its streams are aligned from element tv.head on; at
+    // most 255 elements) is taken by one block, after its unit, element j in thread j mod TPB.
     // Block-uniform; its count joins cnt as the wave's (vector path) or the lane's count.
-    if (tv.head && unit + 1 == tv.t_end) {
+    if (takes_head()) {
         uint32_t hc = 0, hfirst = 0;
         const int hcover = D.nskip ? inactive_cover(D, 0, tv.head, hfirst) : 0;
-        if (threadIdx.x < tv.head && (kCounting || hcover != 2))
-            scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, threadIdx.x, threadIdx.x + 1, hc, su, sp,
-                                             hcover ? D.nskip : 0, hfirst);
+        if (kCounting || hcover != 2) {
+            if constexpr (TPB == kThreads) {  // a head of at most 63 elements: one per thread
+                if (threadIdx.x < tv.head)
+                    scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, threadIdx.x, threadIdx.x + 1, hc, su, sp,
+                                                     hcover ? D.nskip : 0, hfirst);
+            } else {
+                for (uint32_t j = threadIdx.x; j < tv.head; j += TPB)
+                    scalar_range<MODE, PT, ST, PASS>(a, D, tv, flags, radial, j, j + 1, hc, su, sp, hcover ? D.nskip : 0,
+                                                     hfirst);
+            }
+        }
         if constexpr (kCounting) cnt += vec ? wave_sum(hc) : hc;
     }
     if constexpr (kCounting) {

@@ -79,11 +79,11 @@ def issue_units(op: str) -> float:
 IEEE2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 2}
 FAST2 = {"v_rcp_f32": 2, "v_div_fixup_f32": 0}
 KERNELS = {
-    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 91.0,
+    "cfg5 T2 bf16, f32 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 91.5,
                               {**IEEE2, "v_rsq_f32": 1, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
-    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 98.0,
+    "cfg5 T2 bf16, bf16 m/v": ("_ZN2lv11unit_kernelILi4ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 8, 98.5,
                                {**FAST2, "v_rsq_f32": 1, "v_mul_lo_u32": 6, "v_cvt_sr_bf16_f32": 0}),
-    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.0,
+    "cfg4 T1 bf16, f32 m": ("_ZN2lv11unit_kernelILi3ELi1ELi0ELi1ELj331ELb0EEEvNS_4ArgsE", 4, 74.5,
                             {**IEEE2, "v_mul_lo_u32": 2, "v_cvt_sr_bf16_f32": 0}),
     "cfg4 T1 bf16, bf16 m": ("_ZN2lv11unit_kernelILi3ELi1ELi1ELi1ELj331ELb0EEEvNS_4ArgsE", 16, 72.0,
                              {**FAST2, "v_mul_lo_u32": 4, "v_cvt_sr_bf16_f32": 0}),
